@@ -1,0 +1,145 @@
+/*
+ * mlk_hip.h — C ABI of the MI355X (gfx950) execution backend for MLK+
+ * KernelModules (libmlk_hip.so). Plain pointers and sizes only.
+ *
+ * The backend replaces the reference's GPU artifact path:
+ *   buildGpuKernelArtifact[InDir] / LoadedKernel / cudaToolchainAvailable
+ *     backends/cpu/include/mlk/backend/backend_driver.h:91-228
+ *   the generated artifact's mlk_kernel entry (multi-dim and legacy 1-D)
+ *     docs/kernel_abi.md:25-40, backend_driver.h:15-46,
+ *     backends/cpu/src/cuda_emitter.cpp:1130-1375, :1762-1867
+ *   cudaArtifactBitExactPolicy
+ *     backends/cpu/include/mlk/backend/cuda_emitter.h:106-137
+ * A module crosses the boundary as the "mlk-kernel" JSON document that
+ * KernelModule::toJson writes (compiler/src/support/kernel_ir.cpp:97-254),
+ * with "math" also written on Call nodes.
+ *
+ * Status codes (artifact ABI, docs/kernel_abi.md:25-40): 0 ok, 1 negative
+ * store address, 2 runtime allocation/copy, 3 launch or synchronization,
+ * 4 no usable device. Extensions: 6 binding mismatch (wrong count, dtype or
+ * size), 7 module refused at build (see mlkhip_last_error).
+ */
+#ifndef MLK_HIP_H
+#define MLK_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    MLKHIP_OK = 0,
+    MLKHIP_NEG_STORE = 1,
+    MLKHIP_RUNTIME = 2,
+    MLKHIP_LAUNCH = 3,
+    MLKHIP_NO_DEVICE = 4,
+    MLKHIP_BAD_BINDING = 6,
+    MLKHIP_REFUSED = 7
+};
+
+/* Device element types (KernelBuffer::dtype subset). */
+enum { MLKHIP_F32 = 0, MLKHIP_F16 = 1, MLKHIP_F64 = 2 };
+
+typedef struct mlkhip_artifact mlkhip_artifact;
+
+/* One device-resident buffer of the typed entry point. */
+typedef struct mlkhip_binding {
+    void* ptr;          /* device address; NULL for a temp lets the artifact own it */
+    int64_t elements;   /* capacity in elements */
+    int32_t dtype;      /* MLKHIP_F32 / MLKHIP_F16 / MLKHIP_F64, must equal the module's */
+    int32_t pad;
+} mlkhip_binding;
+
+/* ---- driver (replaces backend_driver.h:91-228) ------------------------ */
+
+/* Message of the last failing call on this thread. */
+const char* mlkhip_last_error(void);
+
+/* Replaces cudaToolchainAvailable (backend_driver.h:98-104): 1 when a HIP
+ * device is visible and its architecture starts with `arch`. */
+int mlkhip_device_available(const char* arch);
+
+/* Replaces validArch (backend_driver.cpp:693-699) for AMD targets: 1 when
+ * `arch` is gfx followed by 3 or 4 hex digits (gfx950, gfx90a, gfx1100). */
+int mlkhip_valid_arch(const char* arch);
+
+/* Replaces buildGpuKernelArtifact[InDir] (backend_driver.h:218-228): plans
+ * the module onto the gfx950 kernels, instantiates and compiles the
+ * template kernels it needs (hipRTC, cached in `cache_dir` when given) and
+ * loads them. `arch` is declared, never defaulted. */
+int mlkhip_build(const char* module_json, size_t len, const char* arch, const char* cache_dir,
+                 mlkhip_artifact** out);
+
+/* Plans without compiling or loading (no device needed). Writes the class
+ * and policy names; returns 0 or MLKHIP_REFUSED. */
+int mlkhip_plan(const char* module_json, size_t len, char* class_name, size_t class_cap,
+                char* policy, size_t policy_cap, int* n_steps);
+
+/* Instantiates the template source of step `step` (elementwise steps) and
+ * compiles it for `arch` without loading; returns the code-object size, 0
+ * for steps that use precompiled kernels, or -1. `source` may be NULL. */
+long long mlkhip_compile_check(const char* module_json, size_t len, int step, const char* arch,
+                               char* source, size_t source_cap);
+
+void mlkhip_release(mlkhip_artifact* a);
+
+int mlkhip_is_multidim(const mlkhip_artifact* a);
+const char* mlkhip_class_name(const mlkhip_artifact* a);
+
+/* Replaces cudaArtifactBitExactPolicy (cuda_emitter.h:106-137): the
+ * tolerance policy id the artifact's results are certified under. */
+const char* mlkhip_policy(const mlkhip_artifact* a);
+
+/* Number of bindable buffers (input | output | temp, table order) and the
+ * module's dtype / element count of bindable `i` (elements = -1 when the
+ * buffer is sized by the run's dynamic element count). */
+int mlkhip_num_bindables(const mlkhip_artifact* a);
+int mlkhip_bindable_info(const mlkhip_artifact* a, int i, int32_t* dtype, int64_t* elements,
+                         int* is_input, int* is_output, int* is_temp);
+
+/* ---- artifact ABI (docs/kernel_abi.md:25-40) --------------------------- */
+
+/* Multi-dim form: one (f64 host pointer, dims) pair per bindable buffer in
+ * table order (temps: pass NULL; the artifact materializes zeroed device
+ * scratch), the scalar table, the dynamic element count. Converts to the
+ * module dtypes (RNE) on upload, back to f64 on download; outputs are
+ * uploaded too, since += and max stores read them. Synchronous. */
+int mlkhip_kernel(const mlkhip_artifact* a, double* const* ptrs, const int64_t* const* dims,
+                  int n_bindables, const double* scalars, int64_t n_scalars, int64_t elements);
+
+/* Legacy 1-D form (the reference's void mlk_kernel(..., int64_t n, scalars)):
+ * bindable pointers in table order, n = element count. Returns a status
+ * instead of swallowing it. */
+int mlkhip_kernel_1d(const mlkhip_artifact* a, double* const* ptrs, int n_ptrs, int64_t n,
+                     const double* scalars, int64_t n_scalars);
+
+/* Device-resident typed entry (the timing path): no copies, no allocation
+ * except artifact-owned temp scratch; enqueued on `stream` (a hipStream_t,
+ * NULL = default stream), asynchronous. */
+int mlkhip_run_device(const mlkhip_artifact* a, const mlkhip_binding* binds, int n_binds,
+                      const double* scalars, int64_t n_scalars, int64_t elements, void* stream);
+
+/* Times `reps` back-to-back launches of the device entry after `warmup`
+ * untimed ones, with HIP events on `stream`; writes per-launch milliseconds
+ * (reps values) into `ms_out`. */
+int mlkhip_time_device(const mlkhip_artifact* a, const mlkhip_binding* binds, int n_binds,
+                       const double* scalars, int64_t n_scalars, int64_t elements, void* stream,
+                       int warmup, int reps, float* ms_out);
+
+/* ---- device memory plumbing for hosts without another HIP runtime ----- */
+int mlkhip_malloc(void** p, size_t bytes);
+int mlkhip_free(void* p);
+int mlkhip_memcpy_h2d(void* dst, const void* src, size_t bytes);
+int mlkhip_memcpy_d2h(void* dst, const void* src, size_t bytes);
+int mlkhip_fill32(void* p, uint32_t value, size_t bytes);
+int mlkhip_synchronize(void);
+int mlkhip_stream_create(void** s);
+int mlkhip_stream_destroy(void* s);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MLK_HIP_H */

@@ -1,0 +1,340 @@
+// Fused elementwise kernel template: the Loop{Compute; Store} class of
+// runtime/src/execution/kernel_buffers.cpp:342-402 (1-D) and of the
+// poly.synth broadcast nests (compiler/src/passes/poly/poly.synth.cpp:231-353).
+//
+// The host planner instantiates this template for one KernelModule by
+// prepending a prelude that fixes, at compile time, the box extents, every
+// stream's dtype and affine coefficients, the output map and accumulate mode,
+// and `mlk_chain`, the module's expression chain as straight-line f64 code
+// (the reference executor evaluates every chain in f64). The instance is
+// compiled in-process with hipRTC for the declared gfx950 target and cached.
+// Without a prelude the file compiles standalone with a sample instance (the
+// C1 chain), which is how the build checks it.
+//
+// Mapping: lane c owns kPer consecutive elements of one innermost row of the
+// box (row = c / chunksPerRow). A stream with innermost coefficient 1 is read
+// with 16-byte loads when the lane's run is 16-byte aligned, coefficient 0 is
+// one broadcast load per lane, any other coefficient is a gather. The output
+// is written the same way. Index arithmetic divides by compile-time extents.
+// Compiled with -ffp-contract=off: f64 mul/add round separately, as on the
+// reference's x86-64 build; the only fused multiply-adds are the explicit
+// ones of the f32 residual polynomial in mlk_p7_sin_f32out.
+#ifndef __HIPCC_RTC__
+#include <hip/hip_runtime.h>
+#endif
+
+#ifndef MLK_GENERATED
+#define MLK_NIN 1
+constexpr int kRank = 1;
+constexpr bool kDynamicExtent = false;
+constexpr long long kExt[4] = {1 << 24, 1, 1, 1};
+constexpr int kInDt[MLK_NIN] = {0};
+constexpr long long kInOff[MLK_NIN] = {0};
+constexpr long long kInC[MLK_NIN][4] = {{1, 0, 0, 0}};
+constexpr int kOutDt = 0;
+constexpr long long kOutOff = 0;
+constexpr long long kOutC[4] = {1, 0, 0, 0};
+constexpr int kAccum = 0;
+#define MLK_CHAIN_BODY                      \
+    const double t0 = in[0] * in[0];        \
+    const double t1 = 3.0 * in[0];          \
+    const double t2 = t0 + t1;              \
+    const double t3 = mlk_p7_sin_f32out(t2); \
+    return t3;
+#endif
+
+typedef float mlk_f32x4 __attribute__((ext_vector_type(4)));
+typedef double mlk_f64x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 mlk_f16x8 __attribute__((ext_vector_type(8)));
+
+namespace mlk {
+
+constexpr int kThreads = 256;
+constexpr int kPer = 16;
+
+// math_families.h:22-65: Cody-Waite split of pi/2 and the residual polynomials.
+constexpr double kPiHalf = 1.57079632679489661923;
+constexpr double kTwoOverPi = 0.63661977236758134308;
+constexpr double kPio2Hi = 1.5707963267948965580e+00;
+constexpr double kPio2Lo = 6.1232339957367660359e-17;
+constexpr double kS[6] = {1.58962301576546568060e-10, -2.50507477628578072866e-8,
+                          2.75573136213857245213e-6, -1.98412698295895385996e-4,
+                          8.33333333332211858878e-3, -1.66666666666666307295e-1};
+constexpr double kC[6] = {-1.13585365213876817300e-11, 2.08757530072652689750e-9,
+                          -2.75573142103085808917e-7, 2.48015872890001867312e-5,
+                          -1.38888888888783992457e-3, 4.16666666666666435770e-2};
+
+__device__ __forceinline__ int quadrantOf(double n) {
+    if (__builtin_fabs(n) < 4503599627370496.0) {  // |n| < 2^52: exact in int64
+        return static_cast<int>(static_cast<long long>(n) & 3LL);
+    }
+    int q = static_cast<int>(fmod(n, 4.0));
+    return q < 0 ? q + 4 : q;
+}
+
+}  // namespace mlk
+
+/// poly7 sin, operation for operation as math_families.h:81-90 (f64).
+__device__ __forceinline__ double mlk_p7_sin(double x) {
+    using namespace mlk;
+    const double n = floor(x / kPiHalf + 0.5);
+    const double r = (x - n * kPio2Hi) - n * kPio2Lo;
+    const int q = quadrantOf(n);
+    const double r2 = r * r;
+    double v;
+    if (q & 1) {
+        double p = kC[0];
+        for (int i = 1; i < 6; ++i) p = p * r2 + kC[i];
+        v = 1.0 - r2 * 0.5 + r2 * r2 * p;
+    } else {
+        double p = kS[0];
+        for (int i = 1; i < 6; ++i) p = p * r2 + kS[i];
+        v = r + r * r2 * p;
+    }
+    return (q & 2) ? -v : v;
+}
+
+/// poly7 sin for a value rounded to f32 right after (the planner uses it
+/// only when sin is the chain's last op and the output is f32/f16). The
+/// reduction r = (x - n*hi) - n*lo stays in f64; the residual polynomials run
+/// in f32 on r rounded to f32 (|r| <= pi/4: ~1 f32 ULP, plus r's own 0.5 ULP
+/// relative rounding). n = floor(x*2/pi + 0.5) can differ from the
+/// reference's floor(x/(pi/2) + 0.5) only within an ULP of an odd multiple of
+/// pi/4, where both reductions are valid and agree to polynomial accuracy.
+__device__ __forceinline__ double mlk_p7_sin_f32out(double x) {
+    using namespace mlk;
+    const double n = floor(x * kTwoOverPi + 0.5);
+    const double r = (x - n * kPio2Hi) - n * kPio2Lo;
+    const int q = quadrantOf(n);
+    const float rf = static_cast<float>(r);
+    const float r2 = rf * rf;
+    float ps = static_cast<float>(kS[0]);
+    float pc = static_cast<float>(kC[0]);
+#pragma unroll
+    for (int i = 1; i < 6; ++i) {
+        ps = __builtin_fmaf(ps, r2, static_cast<float>(kS[i]));
+        pc = __builtin_fmaf(pc, r2, static_cast<float>(kC[i]));
+    }
+    const float s = __builtin_fmaf(rf * r2, ps, rf);
+    const float c = __builtin_fmaf(r2 * r2, pc, __builtin_fmaf(-0.5f, r2, 1.0f));
+    float v = (q & 1) ? c : s;
+    v = (q & 2) ? -v : v;
+    return r == r ? static_cast<double>(v) : r;  // NaN/inf arguments give NaN
+}
+
+struct mlk_scalars {
+    double v[8];
+};
+
+__device__ __forceinline__ double mlk_chain(const double* in, const mlk_scalars& sc) {
+    (void)in;
+    (void)sc;
+    MLK_CHAIN_BODY
+}
+
+namespace mlk {
+
+// dtype codes: 0 f32, 1 f16, 2 f64 (mlkd_dtype).
+template <int DT>
+__device__ __forceinline__ double loadOne(const void* p, long long i) {
+    if constexpr (DT == 0) return static_cast<double>(static_cast<const float*>(p)[i]);
+    else if constexpr (DT == 1)
+        return static_cast<double>(static_cast<float>(static_cast<const _Float16*>(p)[i]));
+    else return static_cast<const double*>(p)[i];
+}
+
+/// f64 -> f16 with one rounding: round-to-odd into f32 (truncate, set the last
+/// bit when inexact), then RNE to f16.
+__device__ __forceinline__ _Float16 toHalf(double d) {
+    float t = __double2float_rz(d);
+    if (static_cast<double>(t) != d && t == t) t = __uint_as_float(__float_as_uint(t) | 1u);
+    return static_cast<_Float16>(t);
+}
+
+template <int DT>
+__device__ __forceinline__ void storeOne(void* p, long long i, double v) {
+    if constexpr (DT == 0) static_cast<float*>(p)[i] = static_cast<float>(v);
+    else if constexpr (DT == 1) static_cast<_Float16*>(p)[i] = toHalf(v);
+    else static_cast<double*>(p)[i] = v;
+}
+
+template <int DT>
+constexpr int kBytes = DT == 0 ? 4 : (DT == 1 ? 2 : 8);
+
+/// kPer consecutive elements from a 16-byte aligned run.
+template <int DT>
+__device__ __forceinline__ void loadRunVec(const void* p, long long i, double (&v)[kPer]) {
+    if constexpr (DT == 0) {
+        const mlk_f32x4* q = reinterpret_cast<const mlk_f32x4*>(static_cast<const float*>(p) + i);
+        mlk_f32x4 f[kPer / 4];
+#pragma unroll
+        for (int c = 0; c < kPer / 4; ++c) f[c] = __builtin_nontemporal_load(q + c);
+#pragma unroll
+        for (int c = 0; c < kPer / 4; ++c) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[4 * c + e] = static_cast<double>(f[c][e]);
+        }
+    } else if constexpr (DT == 1) {
+        const mlk_f16x8* q = reinterpret_cast<const mlk_f16x8*>(static_cast<const _Float16*>(p) + i);
+        mlk_f16x8 h[kPer / 8];
+#pragma unroll
+        for (int c = 0; c < kPer / 8; ++c) h[c] = __builtin_nontemporal_load(q + c);
+#pragma unroll
+        for (int c = 0; c < kPer / 8; ++c) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[8 * c + e] = static_cast<double>(static_cast<float>(h[c][e]));
+        }
+    } else {
+        const mlk_f64x2* q = reinterpret_cast<const mlk_f64x2*>(static_cast<const double*>(p) + i);
+#pragma unroll
+        for (int c = 0; c < kPer / 2; ++c) {
+            const mlk_f64x2 d = __builtin_nontemporal_load(q + c);
+            v[2 * c] = d[0];
+            v[2 * c + 1] = d[1];
+        }
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ void storeRunVec(void* p, long long i, const double (&v)[kPer]) {
+    if constexpr (DT == 0) {
+        mlk_f32x4* q = reinterpret_cast<mlk_f32x4*>(static_cast<float*>(p) + i);
+#pragma unroll
+        for (int c = 0; c < kPer / 4; ++c) {
+            mlk_f32x4 f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) f[e] = static_cast<float>(v[4 * c + e]);
+            __builtin_nontemporal_store(f, q + c);
+        }
+    } else if constexpr (DT == 1) {
+        mlk_f16x8* q = reinterpret_cast<mlk_f16x8*>(static_cast<_Float16*>(p) + i);
+#pragma unroll
+        for (int c = 0; c < kPer / 8; ++c) {
+            mlk_f16x8 h;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) h[e] = toHalf(v[8 * c + e]);
+            __builtin_nontemporal_store(h, q + c);
+        }
+    } else {
+        mlk_f64x2* q = reinterpret_cast<mlk_f64x2*>(static_cast<double*>(p) + i);
+#pragma unroll
+        for (int c = 0; c < kPer / 2; ++c) {
+            mlk_f64x2 d;
+            d[0] = v[2 * c];
+            d[1] = v[2 * c + 1];
+            __builtin_nontemporal_store(d, q + c);
+        }
+    }
+}
+
+constexpr long long outerRows() {
+    long long r = 1;
+    for (int d = 0; d < kRank - 1; ++d) r *= kExt[d];
+    return r;
+}
+
+template <int K>
+__device__ __forceinline__ void loadStream(const void* p, const long long (&var)[4], long long col0,
+                                           bool full, long long W, double (&v)[kPer]) {
+    constexpr int DT = kInDt[K];
+    long long base = kInOff[K];
+#pragma unroll
+    for (int d = 0; d < kRank - 1; ++d) base += kInC[K][d] * var[d];
+    constexpr long long ci = kInC[K][kRank - 1];
+    if constexpr (ci == 0) {
+        const double x = loadOne<DT>(p, base);
+#pragma unroll
+        for (int e = 0; e < kPer; ++e) v[e] = x;
+    } else {
+        const long long first = base + ci * col0;
+        const bool vec = ci == 1 && full &&
+                         ((reinterpret_cast<unsigned long long>(p) + first * kBytes<DT>) & 15ull) == 0;
+        if (vec) {
+            loadRunVec<DT>(p, first, v);
+        } else {
+#pragma unroll
+            for (int e = 0; e < kPer; ++e) {
+                v[e] = (col0 + e < W) ? loadOne<DT>(p, first + ci * e) : 0.0;
+            }
+        }
+    }
+}
+
+template <int K>
+__device__ __forceinline__ void loadAll(const void* const (&ptr)[4], const long long (&var)[4],
+                                        long long col0, bool full, long long W,
+                                        double (&in)[MLK_NIN][kPer]) {
+    if constexpr (K < MLK_NIN) {
+        loadStream<K>(ptr[K], var, col0, full, W, in[K]);
+        loadAll<K + 1>(ptr, var, col0, full, W, in);
+    }
+}
+
+}  // namespace mlk
+
+extern "C" __global__ __launch_bounds__(256) void mlk_elementwise(const void* p0, const void* p1,
+                                                                  const void* p2, const void* p3,
+                                                                  void* out, const mlk_scalars sc,
+                                                                  long long dynExtent) {
+    using namespace mlk;
+    // The 1-D dynamic form (loop end = the run's element count) takes its
+    // extent at launch; every other extent is a compile-time constant.
+    const long long W = kDynamicExtent ? dynExtent : kExt[kRank - 1];
+    const long long chunksPerRow = (W + kPer - 1) / kPer;
+    constexpr long long rows = outerRows();
+    const long long total = rows * chunksPerRow;
+    const void* const ptr[4] = {p0, p1, p2, p3};
+    const long long stride = static_cast<long long>(gridDim.x) * kThreads;
+    for (long long c = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x; c < total;
+         c += stride) {
+        const long long row = c / chunksPerRow;
+        const long long col0 = (c - row * chunksPerRow) * kPer;
+        const bool full = col0 + kPer <= W;
+        long long var[4] = {0, 0, 0, 0};
+        {
+            long long rem = row;
+#pragma unroll
+            for (int d = kRank - 2; d >= 0; --d) {
+                var[d] = rem % kExt[d];
+                rem /= kExt[d];
+            }
+        }
+        double in[MLK_NIN][kPer];
+        loadAll<0>(ptr, var, col0, full, W, in);
+        double res[kPer];
+#pragma unroll
+        for (int e = 0; e < kPer; ++e) {
+            double x[MLK_NIN];
+#pragma unroll
+            for (int k = 0; k < MLK_NIN; ++k) x[k] = in[k][e];
+            res[e] = mlk_chain(x, sc);
+        }
+        long long obase = kOutOff;
+#pragma unroll
+        for (int d = 0; d < kRank - 1; ++d) obase += kOutC[d] * var[d];
+        constexpr long long oc = kOutC[kRank - 1];
+        const long long ofirst = obase + oc * col0;
+        if constexpr (kAccum != 0) {
+#pragma unroll
+            for (int e = 0; e < kPer; ++e) {
+                if (col0 + e < W) {
+                    const long long at = ofirst + oc * e;
+                    const double old = loadOne<kOutDt>(out, at);
+                    const double v = kAccum == 1 ? old + res[e] : ((res[e] > old) ? res[e] : old);
+                    storeOne<kOutDt>(out, at, v);
+                }
+            }
+        } else {
+            const bool vec = oc == 1 && full &&
+                             ((reinterpret_cast<unsigned long long>(out) + ofirst * kBytes<kOutDt>) & 15ull) == 0;
+            if (vec) {
+                storeRunVec<kOutDt>(out, ofirst, res);
+            } else {
+#pragma unroll
+                for (int e = 0; e < kPer; ++e) {
+                    if (col0 + e < W) storeOne<kOutDt>(out, ofirst + oc * e, res[e]);
+                }
+            }
+        }
+    }
+}

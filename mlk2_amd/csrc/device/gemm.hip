@@ -1,0 +1,388 @@
+// Dense C[M,N] (+)= A[M,K] * B[K,N], row-major: Call(MatMul)
+// (runtime/src/execution/kernel_buffers.cpp:406-432, C accumulated in place)
+// and the poly.synth init+accumulate nest (compiler/src/passes/poly/
+// poly.synth.cpp:58-147, C = 0 then +=).
+//
+// f16 x f16 -> f32 (tensor_f16_gpu): v_mfma_f32_32x32x16_f16. Workgroup tile
+// 256x256, K step 64, 512 threads = 8 waves as 2 (M) x 4 (N); each wave owns
+// 128x64 = 4x2 MFMA tiles (128 accumulator VGPRs). A and B tiles are double
+// buffered in LDS (2 x 72 KiB): the next K step's global loads are issued
+// before the current step's MFMAs and written to the other buffer after
+// them, one barrier per step. A is stored as loaded ([m][k], k contiguous);
+// B is transposed in registers on its way to LDS ([n][k]) so that both MFMA
+// operands are single 16-byte LDS reads (8 consecutive k per lane). Rows of
+// both LDS tiles are padded by 16 bytes. Workgroups are mapped XCD-aware:
+// consecutive workgroup ids go to different XCDs, so the 32 tiles one XCD
+// runs form a 4x8 block that shares A and B panels in that XCD's L2.
+//
+// f32 x f32 -> f32: v_mfma_f32_32x32x2_f32, 64x64 tiles (256 tiles at 1024^2
+// fill the 256 CUs), K step 32, A transposed into LDS ([k][m]) and B stored as
+// loaded ([k][n]) so each MFMA operand is one conflict-free 4-byte read.
+//
+// Any other shape or dtype mix runs the general tiled kernel (f32 or f64
+// accumulation, bounds-checked).
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+
+#include "runtime_abi.h"
+
+namespace {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------- f16 ----
+constexpr int kBM = 256, kBN = 256, kBK = 64;
+constexpr int kPadK = kBK + 8;           // halves per LDS row (16-byte pad)
+constexpr int kTileHalves = 256 * kPadK;  // one LDS tile (A or B)
+
+__device__ __forceinline__ void xcdTile(int tilesM, int tilesN, int& tm, int& tn) {
+    const int id = blockIdx.x;
+    const int total = tilesM * tilesN;
+    // Group tiles 4 (M) x 8 (N) per XCD when the grid is a multiple of that.
+    if (tilesM % 4 == 0 && tilesN % 8 == 0 && total % 256 == 0) {
+        const int xcd = id % 8;
+        const int local = id / 8;            // 0 .. total/8-1
+        const int groupsN = tilesN / 8;
+        const int roundTiles = 256;          // 8 XCDs x 32 tiles per round
+        const int round = (id / roundTiles);
+        const int localInRound = local % 32;
+        const int groupId = round * 8 + xcd;
+        const int gm = groupId / groupsN;
+        const int gn = groupId % groupsN;
+        tm = gm * 4 + localInRound / 8;
+        tn = gn * 8 + localInRound % 8;
+        return;
+    }
+    tm = id / tilesN;
+    tn = id % tilesN;
+}
+
+__global__ __launch_bounds__(512) void gemmF16Mfma(const _Float16* __restrict__ A,
+                                                   const _Float16* __restrict__ B,
+                                                   float* __restrict__ C, int M, int N, int K,
+                                                   int64_t lda, int64_t ldb, int64_t ldc,
+                                                   int accumulate) {
+    extern __shared__ __align__(16) _Float16 lds[];
+    _Float16* As = lds;                      // [2][256][kPadK]
+    _Float16* Bs = lds + 2 * kTileHalves;    // [2][256][kPadK]
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave >> 2;   // 0..1
+    const int wn = wave & 3;    // 0..3
+    int tm, tn;
+    xcdTile(M / kBM, N / kBN, tm, tn);
+    const int64_t row0 = static_cast<int64_t>(tm) * kBM;
+    const int64_t col0 = static_cast<int64_t>(tn) * kBN;
+
+    // Loader roles: threads 0..255 load A (8 x 16 B each), 256..511 load a
+    // 8 (k) x 8 (n) block of B each.
+    const bool loadsA = tid < 256;
+    const int t = tid & 255;
+    const int bk = t >> 5;     // B block: k rows bk*8 .. +7
+    const int bn = t & 31;     // B block: n cols bn*8 .. +7
+    u32x4 reg[8];
+
+    auto globalLoad = [&](int k0) {
+        if (loadsA) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int c = j * 256 + t;      // 16-byte chunk of the 256x64 tile
+                const int r = c >> 3;
+                const int ch = c & 7;
+                reg[j] = *reinterpret_cast<const u32x4*>(A + (row0 + r) * lda + k0 + ch * 8);
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                reg[r] = *reinterpret_cast<const u32x4*>(B + static_cast<int64_t>(k0 + bk * 8 + r) * ldb +
+                                                        col0 + bn * 8);
+            }
+        }
+    };
+    auto ldsStore = [&](int buf) {
+        if (loadsA) {
+            _Float16* dst = As + buf * kTileHalves;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int c = j * 256 + t;
+                const int r = c >> 3;
+                const int ch = c & 7;
+                *reinterpret_cast<u32x4*>(dst + r * kPadK + ch * 8) = reg[j];
+            }
+        } else {
+            _Float16* dst = Bs + buf * kTileHalves;
+            // 8x8 transpose of 16-bit values: column n of the block becomes
+            // 8 consecutive k values.
+#pragma unroll
+            for (int n = 0; n < 8; ++n) {
+                const int p = n >> 1;
+                const uint32_t sel = (n & 1) ? 0x07060302u : 0x05040100u;
+                u32x4 o;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    o[j] = __builtin_amdgcn_perm(reg[2 * j + 1][p], reg[2 * j][p], sel);
+                }
+                *reinterpret_cast<u32x4*>(dst + (bn * 8 + n) * kPadK + bk * 8) = o;
+            }
+        }
+    };
+
+    f32x16 acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+        }
+    }
+
+    const int steps = K / kBK;
+    globalLoad(0);
+    ldsStore(0);
+    __syncthreads();
+    const int lrow = lane & 31;
+    const int lk = (lane >> 5) * 8;
+    for (int s = 0; s < steps; ++s) {
+        const int buf = s & 1;
+        if (s + 1 < steps) globalLoad((s + 1) * kBK);
+        const _Float16* as = As + buf * kTileHalves + (wm * 128 + lrow) * kPadK + lk;
+        const _Float16* bs = Bs + buf * kTileHalves + (wn * 64 + lrow) * kPadK + lk;
+#pragma unroll
+        for (int kk = 0; kk < kBK; kk += 16) {
+            f16x8 a[4], b[2];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const f16x8*>(as + i * 32 * kPadK + kk);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) b[j] = *reinterpret_cast<const f16x8*>(bs + j * 32 * kPadK + kk);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+                }
+            }
+        }
+        if (s + 1 < steps) {
+            ldsStore(buf ^ 1);
+        }
+        __syncthreads();
+    }
+
+    // D layout of a 32x32 MFMA tile: lane l, register r holds
+    // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int64_t cBase = col0 + wn * 64 + j * 32 + (lane & 31);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int64_t row = row0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                float* dst = C + row * ldc + cBase;
+                const float v = acc[i][j][r];
+                *dst = accumulate ? *dst + v : v;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------- f32 ----
+constexpr int kFM = 64, kFN = 64, kFK = 32;
+
+__global__ __launch_bounds__(256) void gemmF32Mfma(const float* __restrict__ A,
+                                                   const float* __restrict__ B,
+                                                   float* __restrict__ C, int M, int N, int K,
+                                                   int64_t lda, int64_t ldb, int64_t ldc,
+                                                   int accumulate) {
+    __shared__ float At[2][kFK][kFM + 4];   // transposed: [k][m]
+    __shared__ float Bs[2][kFK][kFN + 4];   // as loaded: [k][n]
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;   // 2x2 waves, 32x32 each
+    const int tilesN = N / kFN;
+    const int64_t row0 = static_cast<int64_t>(blockIdx.x / tilesN) * kFM;
+    const int64_t col0 = static_cast<int64_t>(blockIdx.x % tilesN) * kFN;
+
+    // A tile 64x32 floats = 512 float4: 2 per thread; B tile 32x64 = 512 float4.
+    f32x4 ra[2], rb[2];
+    auto globalLoad = [&](int k0) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int c = j * 256 + tid;
+            const int r = c >> 3, ch = c & 7;       // A: 64 rows x 8 chunks
+            ra[j] = *reinterpret_cast<const f32x4*>(A + (row0 + r) * lda + k0 + ch * 4);
+            const int kr = c >> 4, nc = c & 15;     // B: 32 rows x 16 chunks
+            rb[j] = *reinterpret_cast<const f32x4*>(B + static_cast<int64_t>(k0 + kr) * ldb + col0 + nc * 4);
+        }
+    };
+    auto ldsStore = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int c = j * 256 + tid;
+            const int r = c >> 3, ch = c & 7;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) At[buf][ch * 4 + e][r] = ra[j][e];
+            const int kr = c >> 4, nc = c & 15;
+            *reinterpret_cast<f32x4*>(&Bs[buf][kr][nc * 4]) = rb[j];
+        }
+    };
+    f32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+    const int steps = K / kFK;
+    globalLoad(0);
+    ldsStore(0);
+    __syncthreads();
+    const int lcol = lane & 31;
+    const int lk = lane >> 5;
+    for (int s = 0; s < steps; ++s) {
+        const int buf = s & 1;
+        if (s + 1 < steps) globalLoad((s + 1) * kFK);
+#pragma unroll
+        for (int kk = 0; kk < kFK; kk += 2) {
+            const float a = At[buf][kk + lk][wm * 32 + lcol];
+            const float b = Bs[buf][kk + lk][wn * 32 + lcol];
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc, 0, 0, 0);
+        }
+        if (s + 1 < steps) ldsStore(buf ^ 1);
+        __syncthreads();
+    }
+    const int64_t cBase = col0 + wn * 32 + (lane & 31);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int64_t row = row0 + wm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        float* dst = C + row * ldc + cBase;
+        *dst = accumulate ? *dst + acc[r] : acc[r];
+    }
+}
+
+// ------------------------------------------------------------- general ---
+template <typename T>
+__device__ __forceinline__ T ldAny(const void* p, int dt, int64_t i) {
+    if (dt == MLKD_F32) return static_cast<T>(static_cast<const float*>(p)[i]);
+    if (dt == MLKD_F16) return static_cast<T>(static_cast<float>(static_cast<const _Float16*>(p)[i]));
+    return static_cast<T>(static_cast<const double*>(p)[i]);
+}
+
+template <typename T>
+__device__ __forceinline__ void stAny(void* p, int dt, int64_t i, T v) {
+    if (dt == MLKD_F32) {
+        static_cast<float*>(p)[i] = static_cast<float>(v);
+    } else if (dt == MLKD_F16) {
+        static_cast<_Float16*>(p)[i] = static_cast<_Float16>(static_cast<float>(v));
+    } else {
+        static_cast<double*>(p)[i] = static_cast<double>(v);
+    }
+}
+
+/// 64x64 output tile per 256 threads, 4x4 per thread, K slabs of 16 through
+/// LDS; k ascending per output element.
+template <typename T>
+__global__ __launch_bounds__(256) void gemmGeneral(mlkd_gemm p) {
+    __shared__ T As[16][64 + 1];
+    __shared__ T Bs[16][64 + 1];
+    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+    const int64_t tilesN = (p.n + 63) / 64;
+    const int64_t row0 = (blockIdx.x / tilesN) * 64;
+    const int64_t col0 = (blockIdx.x % tilesN) * 64;
+    T acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = T(0);
+    }
+    for (int64_t k0 = 0; k0 < p.k; k0 += 16) {
+        for (int e = threadIdx.x; e < 16 * 64; e += 256) {
+            const int kk = e / 64, mm = e % 64;
+            const int64_t r = row0 + mm, kA = k0 + kk;
+            As[kk][mm] = (r < p.m && kA < p.k) ? ldAny<T>(p.a, p.a_dtype, r * p.lda + kA) : T(0);
+            const int64_t c = col0 + mm;
+            Bs[kk][mm] = (c < p.n && kA < p.k) ? ldAny<T>(p.b, p.b_dtype, kA * p.ldb + c) : T(0);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < 16; ++kk) {
+            T a[4], b[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) a[i] = As[kk][ty * 4 + i];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) b[j] = Bs[kk][tx * 4 + j];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] += a[i] * b[j];
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t r = row0 + ty * 4 + i, c = col0 + tx * 4 + j;
+            if (r < p.m && c < p.n) {
+                const int64_t at = r * p.ldc + c;
+                const T old = p.accumulate ? ldAny<T>(p.c, p.c_dtype, at) : T(0);
+                stAny<T>(p.c, p.c_dtype, at, old + acc[i][j]);
+            }
+        }
+    }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+extern "C" int mlkd_launch_gemm(const mlkd_gemm* p, void* stream) {
+    if (p == nullptr || p->m < 0 || p->n < 0 || p->k < 0) return MLKD_RT_LAUNCH;
+    if (p->m == 0 || p->n == 0) return 0;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const bool fits32 = p->m < (1LL << 31) && p->n < (1LL << 31) && p->k < (1LL << 31);
+    if (p->k > 0 && fits32 && p->a_dtype == MLKD_F16 && p->b_dtype == MLKD_F16 &&
+        p->c_dtype == MLKD_F32 && p->m % kBM == 0 && p->n % kBN == 0 && p->k % kBK == 0 &&
+        p->lda % 8 == 0 && p->ldb % 8 == 0 && aligned16(p->a) && aligned16(p->b)) {
+        const int tiles = static_cast<int>((p->m / kBM) * (p->n / kBN));
+        const size_t ldsBytes = 4 * kTileHalves * sizeof(_Float16);
+        static bool ldsRaised = false;
+        if (!ldsRaised) {
+            if (hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF16Mfma),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    static_cast<int>(ldsBytes)) != hipSuccess) {
+                return MLKD_RT_LAUNCH;
+            }
+            ldsRaised = true;
+        }
+        hipLaunchKernelGGL(gemmF16Mfma, dim3(tiles), dim3(512), ldsBytes, st,
+                           static_cast<const _Float16*>(p->a), static_cast<const _Float16*>(p->b),
+                           static_cast<float*>(p->c), static_cast<int>(p->m), static_cast<int>(p->n),
+                           static_cast<int>(p->k), p->lda, p->ldb, p->ldc, p->accumulate);
+        return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
+    }
+    if (p->k > 0 && fits32 && p->a_dtype == MLKD_F32 && p->b_dtype == MLKD_F32 &&
+        p->c_dtype == MLKD_F32 && p->m % kFM == 0 && p->n % kFN == 0 && p->k % kFK == 0 &&
+        p->lda % 4 == 0 && p->ldb % 4 == 0 && aligned16(p->a) && aligned16(p->b)) {
+        const int tiles = static_cast<int>((p->m / kFM) * (p->n / kFN));
+        hipLaunchKernelGGL(gemmF32Mfma, dim3(tiles), dim3(256), 0, st,
+                           static_cast<const float*>(p->a), static_cast<const float*>(p->b),
+                           static_cast<float*>(p->c), static_cast<int>(p->m), static_cast<int>(p->n),
+                           static_cast<int>(p->k), p->lda, p->ldb, p->ldc, p->accumulate);
+        return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
+    }
+    const int64_t tiles = ((p->m + 63) / 64) * ((p->n + 63) / 64);
+    if (tiles > 0x7FFFFFFF) return MLKD_RT_LAUNCH;
+    const bool wide = p->a_dtype == MLKD_F64 || p->b_dtype == MLKD_F64 || p->c_dtype == MLKD_F64;
+    if (wide) {
+        hipLaunchKernelGGL(gemmGeneral<double>, dim3(static_cast<unsigned>(tiles)), dim3(256), 0, st, *p);
+    } else {
+        hipLaunchKernelGGL(gemmGeneral<float>, dim3(static_cast<unsigned>(tiles)), dim3(256), 0, st, *p);
+    }
+    return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
+}

@@ -1,0 +1,62 @@
+// The thin C ABI between the C++ host code and the HIP side: runtime
+// wrappers (runtime.hip) and one launcher per kernel class. Host code includes
+// only this header; it never includes HIP headers.
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../device_abi.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/// Status codes of the artifact ABI (docs/kernel_abi.md:25-40).
+enum {
+    MLKD_RT_OK = 0,
+    MLKD_RT_NEG_FLAT = 1,
+    MLKD_RT_ALLOC = 2,
+    MLKD_RT_LAUNCH = 3,
+    MLKD_RT_NO_DEVICE = 4,
+};
+
+int mlkd_rt_device_count(void);
+int mlkd_rt_device_arch(int dev, char* buf, size_t cap);
+int mlkd_rt_device_info(int dev, int* cu_count, int64_t* max_grid_x, int* max_block,
+                        int64_t* global_mem);
+int mlkd_rt_malloc(void** p, size_t bytes);
+int mlkd_rt_free(void* p);
+int mlkd_rt_h2d(void* dst, const void* src, size_t bytes, void* stream);
+int mlkd_rt_d2h(void* dst, const void* src, size_t bytes, void* stream);
+int mlkd_rt_d2d(void* dst, const void* src, size_t bytes, void* stream);
+int mlkd_rt_fill32(void* p, uint32_t value, size_t bytes, void* stream);
+int mlkd_rt_sync(void* stream);
+int mlkd_rt_device_sync(void);
+int mlkd_rt_stream_create(void** s);
+int mlkd_rt_stream_destroy(void* s);
+int mlkd_rt_event_create(void** e);
+int mlkd_rt_event_destroy(void* e);
+int mlkd_rt_event_record(void* e, void* stream);
+int mlkd_rt_event_elapsed_ms(void* start, void* stop, float* ms);
+const char* mlkd_rt_last_error(void);
+
+/// hipRTC instances of kernel templates (jit.hip).
+int mlkd_jit_build(const char* src, size_t len, const char* name, const char* arch,
+                   const char* cache_dir, void** fn_out, uint64_t* fingerprint_out, char* log,
+                   size_t cap);
+long long mlkd_jit_compile_only(const char* src, size_t len, const char* arch, char* log,
+                                size_t cap);
+int mlkd_jit_launch_elementwise(void* fn, unsigned grid, const void* const* in, void* out,
+                                const mlkd_scalars* scalars, long long dyn_extent, void* stream);
+int mlkd_launch_rowsum(const mlkd_softmax* p, void* stream);
+
+/// Kernel launchers (device/*.hip). Each validates nothing beyond launch
+/// shape: the host planner has already proved every address in bounds.
+int mlkd_launch_softmax(const mlkd_softmax* p, void* stream);
+int mlkd_launch_gemm(const mlkd_gemm* p, void* stream);
+int mlkd_launch_score_softmax(const mlkd_score_softmax* p, void* stream);
+
+#ifdef __cplusplus
+}
+#endif

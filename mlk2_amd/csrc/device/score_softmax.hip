@@ -1,0 +1,126 @@
+// Config-5 class: S[b*seq + i, :] = softmax((Q[b,i,:] . K[b,:,:]^T) / div +
+// bias), the composition of Call(MatMul) (kernel_buffers.cpp:406-432), the
+// broadcast elementwise chain Add(Div(S, c), bias[j]) (poly.synth.cpp:
+// 231-353) and the stable softmax (kernel_buffers.cpp:290-340).
+//
+// Scores: v_mfma_f32_32x32x16_f16. Both MFMA operands come straight from HBM
+// with 16-byte loads: Q rows are k-contiguous, and K rows are exactly the
+// columns of K^T, also k-contiguous, so no transpose is needed. A workgroup
+// of 4 waves computes a 64 (i) x 128 (j) block, each wave 32 x 64; the
+// epilogue divides by `div`, adds bias[j] and writes f32 scores into S. The
+// softmax then runs in place over the rows of S with the wave-per-row kernel.
+// Other shapes or dtypes run a scalar f64 path with the same two stages.
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+
+#include "runtime_abi.h"
+
+namespace {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__global__ __launch_bounds__(256) void scoresF16(const _Float16* __restrict__ Q,
+                                                 const _Float16* __restrict__ K,
+                                                 const float* __restrict__ bias,
+                                                 float* __restrict__ S, int seq, int dim,
+                                                 float div) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int tilesJ = seq / 128;
+    const int tilesI = seq / 64;
+    const int64_t b = blockIdx.x / (tilesI * tilesJ);
+    const int rem = blockIdx.x % (tilesI * tilesJ);
+    const int i0 = (rem / tilesJ) * 64 + (wave >> 1) * 32;
+    const int j0 = (rem % tilesJ) * 128 + (wave & 1) * 64;
+    const _Float16* q = Q + (b * seq + i0 + (lane & 31)) * dim + (lane >> 5) * 8;
+    const _Float16* k0 = K + (b * seq + j0 + (lane & 31)) * dim + (lane >> 5) * 8;
+    const _Float16* k1 = k0 + static_cast<int64_t>(32) * dim;
+    f32x16 acc0, acc1;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        acc0[r] = 0.0f;
+        acc1[r] = 0.0f;
+    }
+    for (int kk = 0; kk < dim; kk += 16) {
+        const f16x8 a = *reinterpret_cast<const f16x8*>(q + kk);
+        const f16x8 x0 = *reinterpret_cast<const f16x8*>(k0 + kk);
+        const f16x8 x1 = *reinterpret_cast<const f16x8*>(k1 + kk);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, x0, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, x1, acc1, 0, 0, 0);
+    }
+    const int col = lane & 31;
+    const float bj0 = bias[j0 + col];
+    const float bj1 = bias[j0 + 32 + col];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int64_t row = b * seq + i0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        float* dst = S + row * seq + j0 + col;
+        dst[0] = acc0[r] / div + bj0;
+        dst[32] = acc1[r] / div + bj1;
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ double ldAny(const void* p, int dt, int64_t i) {
+    if (dt == MLKD_F32) return static_cast<const float*>(p)[i];
+    if (dt == MLKD_F16) return static_cast<float>(static_cast<const _Float16*>(p)[i]);
+    return static_cast<const double*>(p)[i];
+}
+
+__global__ __launch_bounds__(256) void scoresGeneral(mlkd_score_softmax p) {
+    const int64_t total = p.batch * p.seq * p.seq;
+    for (int64_t t = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; t < total;
+         t += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t j = t % p.seq;
+        const int64_t bi = t / p.seq;  // b*seq + i
+        const int64_t b = bi / p.seq;
+        double acc = 0.0;
+        for (int64_t k = 0; k < p.dim; ++k) {
+            acc += ldAny<double>(p.q, p.qk_dtype, bi * p.dim + k) *
+                   ldAny<double>(p.k, p.qk_dtype, (b * p.seq + j) * p.dim + k);
+        }
+        const double v = acc / p.div + ldAny<double>(p.bias, p.bias_dtype, j);
+        if (p.s_dtype == MLKD_F32) {
+            static_cast<float*>(p.s)[t] = static_cast<float>(v);
+        } else if (p.s_dtype == MLKD_F64) {
+            static_cast<double*>(p.s)[t] = v;
+        } else {
+            static_cast<_Float16*>(p.s)[t] = static_cast<_Float16>(static_cast<float>(v));
+        }
+    }
+}
+
+}  // namespace
+
+extern "C" int mlkd_launch_score_softmax(const mlkd_score_softmax* p, void* stream) {
+    if (p == nullptr || p->batch < 0 || p->seq < 0 || p->dim < 0) return MLKD_RT_LAUNCH;
+    if (p->batch == 0 || p->seq == 0) return 0;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const bool fast = p->qk_dtype == MLKD_F16 && p->bias_dtype == MLKD_F32 && p->s_dtype == MLKD_F32 &&
+                      p->seq % 128 == 0 && p->dim % 16 == 0 && p->dim > 0 && p->seq < (1 << 20) &&
+                      (reinterpret_cast<uintptr_t>(p->q) & 15u) == 0 &&
+                      (reinterpret_cast<uintptr_t>(p->k) & 15u) == 0 && p->dim % 8 == 0;
+    if (fast) {
+        const int64_t blocks = p->batch * (p->seq / 64) * (p->seq / 128);
+        if (blocks > 0x7FFFFFFF) return MLKD_RT_LAUNCH;
+        hipLaunchKernelGGL(scoresF16, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st,
+                           static_cast<const _Float16*>(p->q), static_cast<const _Float16*>(p->k),
+                           static_cast<const float*>(p->bias), static_cast<float*>(p->s),
+                           static_cast<int>(p->seq), static_cast<int>(p->dim), static_cast<float>(p->div));
+    } else {
+        hipLaunchKernelGGL(scoresGeneral, dim3(8192), dim3(256), 0, st, *p);
+    }
+    if (hipGetLastError() != hipSuccess) return MLKD_RT_LAUNCH;
+    mlkd_softmax sm;
+    sm.x = p->s;
+    sm.y = p->s;
+    sm.x_dtype = p->s_dtype;
+    sm.y_dtype = p->s_dtype;
+    sm.rows = p->batch * p->seq;
+    sm.cols = p->seq;
+    sm.x_row_stride = p->seq;
+    sm.y_row_stride = p->seq;
+    return mlkd_launch_softmax(&sm, stream);
+}

@@ -1,0 +1,215 @@
+// Row-wise stable softmax: Call(Softmax) (runtime/src/execution/
+// kernel_buffers.cpp:290-340) and the synthesized six-statement nest of
+// compiler/src/passes/poly/poly.synth.cpp:363-523, which computes the same
+// values through materialized temps. Per row: r = max over x (a NaN never
+// replaces the running max, matching (x > r) ? x : r); y = exp(x - r);
+// s = sum y; y = s != 0 ? y / s : 0. The temps are never materialized: the
+// row lives in registers between its one HBM read and its one HBM write.
+//
+// Fast path (f32 in/out, cols % 4 == 0, cols <= 256*CH): one wave per row,
+// each lane holds CH float4 of the row (16-byte coalesced loads), the max and
+// the sum are wave reductions (ds_swizzle/DPP through __shfl_xor), no LDS and
+// no barriers. exp runs in f32 on x - r (x - r is exact whenever x is near r,
+// which is where the large outputs are); the row sum accumulates in f64, so
+// the normalisation error stays ~1 f32 ULP of each output.
+// General path (any dtype, any cols): one workgroup per row, three passes over
+// the row with LDS reductions, f64 throughout.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdint.h>
+
+#include "runtime_abi.h"
+
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float waveMax(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+__device__ __forceinline__ double waveSum(double v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+template <int CH>
+__global__ __launch_bounds__(256) void softmaxWaveRow(const float* x,
+                                                      float* y, int64_t rows,
+                                                      int64_t cols, int64_t xs, int64_t ys) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int64_t waves = static_cast<int64_t>(gridDim.x) * 4;
+    for (int64_t row = wave; row < rows; row += waves) {
+        const float* xr = x + row * xs;
+        float* yr = y + row * ys;
+        f32x4 v[CH];
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int64_t col = (static_cast<int64_t>(c) * 64 + lane) * 4;
+            if (col < cols) {
+                v[c] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(xr + col));
+            } else {
+                v[c] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+            }
+        }
+        float m = -INFINITY;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) m = fmaxf(m, v[c][e]);
+        }
+        m = waveMax(m);
+        double s = 0.0;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int64_t col = (static_cast<int64_t>(c) * 64 + lane) * 4;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float ex = expf(v[c][e] - m);
+                v[c][e] = ex;
+                if (col < cols) s += static_cast<double>(ex);
+            }
+        }
+        s = waveSum(s);
+        const float inv = s != 0.0 ? static_cast<float>(1.0 / s) : 0.0f;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int64_t col = (static_cast<int64_t>(c) * 64 + lane) * 4;
+            if (col < cols) {
+                f32x4 o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[e] = s != 0.0 ? v[c][e] * inv : 0.0f;
+                __builtin_nontemporal_store(o, reinterpret_cast<f32x4*>(yr + col));
+            }
+        }
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ double ld(const void* p, int64_t i) {
+    return static_cast<double>(static_cast<const T*>(p)[i]);
+}
+
+__device__ __forceinline__ double loadAny(const void* p, int dt, int64_t i) {
+    if (dt == MLKD_F32) return ld<float>(p, i);
+    if (dt == MLKD_F16) return static_cast<double>(static_cast<float>(static_cast<const _Float16*>(p)[i]));
+    return ld<double>(p, i);
+}
+
+__device__ __forceinline__ void storeAny(void* p, int dt, int64_t i, double v) {
+    if (dt == MLKD_F32) {
+        static_cast<float*>(p)[i] = static_cast<float>(v);
+    } else if (dt == MLKD_F16) {
+        static_cast<_Float16*>(p)[i] = static_cast<_Float16>(static_cast<float>(v));
+    } else {
+        static_cast<double*>(p)[i] = v;
+    }
+}
+
+__device__ __forceinline__ double blockReduce(double v, bool isMax, double* scratch) {
+    const int lane = threadIdx.x & 63;
+    const int w = threadIdx.x >> 6;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const double o = __shfl_xor(v, off, 64);
+        v = isMax ? ((o > v) ? o : v) : v + o;
+    }
+    if (lane == 0) scratch[w] = v;
+    __syncthreads();
+    double r = scratch[0];
+    for (int i = 1; i < static_cast<int>(blockDim.x >> 6); ++i) {
+        r = isMax ? ((scratch[i] > r) ? scratch[i] : r) : r + scratch[i];
+    }
+    __syncthreads();
+    return r;
+}
+
+/// General path: any dtype, any row length. f64 arithmetic as the reference.
+__global__ __launch_bounds__(256) void softmaxBlockRow(mlkd_softmax p) {
+    __shared__ double scratch[4];
+    for (int64_t row = blockIdx.x; row < p.rows; row += gridDim.x) {
+        const int64_t xo = row * p.x_row_stride;
+        const int64_t yo = row * p.y_row_stride;
+        double r = -INFINITY;
+        for (int64_t c = threadIdx.x; c < p.cols; c += blockDim.x) {
+            const double v = loadAny(p.x, p.x_dtype, xo + c);
+            r = (v > r) ? v : r;
+        }
+        r = blockReduce(r, true, scratch);
+        double s = 0.0;
+        for (int64_t c = threadIdx.x; c < p.cols; c += blockDim.x) {
+            s += exp(loadAny(p.x, p.x_dtype, xo + c) - r);
+        }
+        s = blockReduce(s, false, scratch);
+        for (int64_t c = threadIdx.x; c < p.cols; c += blockDim.x) {
+            const double e = exp(loadAny(p.x, p.x_dtype, xo + c) - r);
+            storeAny(p.y, p.y_dtype, yo + c, s != 0.0 ? e / s : 0.0);
+        }
+    }
+}
+
+template <int CH>
+int launchWave(const mlkd_softmax& p, hipStream_t st) {
+    int64_t blocks = (p.rows + 3) / 4;
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL(softmaxWaveRow<CH>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st,
+                       static_cast<const float*>(p.x), static_cast<float*>(p.y), p.rows, p.cols,
+                       p.x_row_stride, p.y_row_stride);
+    return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
+}
+
+}  // namespace
+
+extern "C" int mlkd_launch_softmax(const mlkd_softmax* p, void* stream) {
+    if (p == nullptr || p->rows < 0 || p->cols < 0) return MLKD_RT_LAUNCH;
+    if (p->rows == 0 || p->cols == 0) return 0;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const bool aligned = (reinterpret_cast<uintptr_t>(p->x) & 15u) == 0 &&
+                         (reinterpret_cast<uintptr_t>(p->y) & 15u) == 0 &&
+                         (p->x_row_stride & 3) == 0 && (p->y_row_stride & 3) == 0;
+    if (p->x_dtype == MLKD_F32 && p->y_dtype == MLKD_F32 && (p->cols & 3) == 0 && aligned) {
+        if (p->cols <= 256) return launchWave<1>(*p, st);
+        if (p->cols <= 512) return launchWave<2>(*p, st);
+        if (p->cols <= 1024) return launchWave<4>(*p, st);
+        if (p->cols <= 2048) return launchWave<8>(*p, st);
+        if (p->cols <= 4096) return launchWave<16>(*p, st);
+        if (p->cols <= 8192) return launchWave<32>(*p, st);
+    }
+    int64_t blocks = p->rows < 65536 ? p->rows : 65536;
+    hipLaunchKernelGGL(softmaxBlockRow, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, *p);
+    return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
+}
+
+namespace {
+
+/// Row sum (Call(ReduceSum), kernel_buffers.cpp:237-277, and the poly.synth
+/// ReduceSum nest): one wave per row, f64 accumulation (strided per lane,
+/// then a wave reduction).
+__global__ __launch_bounds__(256) void rowSumWave(mlkd_softmax p) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int64_t waves = static_cast<int64_t>(gridDim.x) * 4;
+    for (int64_t row = wave; row < p.rows; row += waves) {
+        double s = 0.0;
+        for (int64_t c = lane; c < p.cols; c += 64) s += loadAny(p.x, p.x_dtype, row * p.x_row_stride + c);
+        s = waveSum(s);
+        if (lane == 0) storeAny(p.y, p.y_dtype, row * p.y_row_stride, s);
+    }
+}
+
+}  // namespace
+
+extern "C" int mlkd_launch_rowsum(const mlkd_softmax* p, void* stream) {
+    if (p == nullptr || p->rows < 0 || p->cols < 0) return MLKD_RT_LAUNCH;
+    if (p->rows == 0) return 0;
+    int64_t blocks = (p->rows + 3) / 4;
+    if (blocks > 16384) blocks = 16384;
+    hipLaunchKernelGGL(rowSumWave, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), *p);
+    return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
+}

@@ -1,0 +1,58 @@
+// Plain-C launch descriptors shared by the C++ host planner and the HIP
+// kernels. The host proves every address of a launch in bounds before it
+// fills one of these; the device code never sees the Kernel IR itself.
+#pragma once
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/// Element types a device buffer may hold (KernelBuffer::dtype subset,
+/// compiler/include/mlk/type/domain.h:53-60).
+enum mlkd_dtype { MLKD_F32 = 0, MLKD_F16 = 1, MLKD_F64 = 2 };
+
+/// Runtime scalar parameters of a chain (ScalarParam operands,
+/// kernel_ir.h:58-70); indices past the bound table read 0.0 like the
+/// reference evaluator (kernel_buffers.cpp:114-117).
+enum { MLKD_MAX_SCALARS = 8 };
+typedef struct mlkd_scalars {
+    double v[MLKD_MAX_SCALARS];
+} mlkd_scalars;
+
+/// Row softmax / row sum: Y[r, :] = f(X[r, :]) over rows x cols, row strides
+/// in elements.
+typedef struct mlkd_softmax {
+    const void* x;
+    void* y;
+    int32_t x_dtype, y_dtype;
+    int64_t rows, cols;
+    int64_t x_row_stride, y_row_stride;
+} mlkd_softmax;
+
+/// C[M,N] (+)= A[M,K] * B[K,N], row-major, leading dims in elements.
+typedef struct mlkd_gemm {
+    const void* a;
+    const void* b;
+    void* c;
+    int32_t a_dtype, b_dtype, c_dtype;
+    int32_t accumulate;   /* 1: C += A*B (Call form); 0: C = A*B */
+    int64_t m, n, k;
+    int64_t lda, ldb, ldc;
+} mlkd_gemm;
+
+/// S[b*seq + i, j] = softmax_j((Q[b,i,:] . K[b,j,:]) / div + bias[j]).
+typedef struct mlkd_score_softmax {
+    const void* q;
+    const void* k;
+    const void* bias;
+    void* s;
+    int32_t qk_dtype, bias_dtype, s_dtype, pad;
+    int64_t batch, seq, dim;
+    double div;
+} mlkd_score_softmax;
+
+#ifdef __cplusplus
+}
+#endif

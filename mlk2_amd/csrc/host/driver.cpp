@@ -1,0 +1,556 @@
+// HIP backend driver and the C ABI of include/mlk_hip.h.
+#include "driver.h"
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+
+#include "../device/runtime_abi.h"
+#include "../../../include/mlk_hip.h"
+
+namespace mlk::hip {
+
+namespace {
+
+int dtypeCode(Dtype d) { return d == Dtype::F32 ? MLKD_F32 : (d == Dtype::F16 ? MLKD_F16 : MLKD_F64); }
+
+unsigned gridFor(int64_t chunks) {
+    int64_t blocks = (chunks + 255) / 256;
+    // Grid-stride beyond 64 workgroups of 4 waves per CU on 256 CUs.
+    if (blocks > 16384) blocks = 16384;
+    if (blocks < 1) blocks = 1;
+    return static_cast<unsigned>(blocks);
+}
+
+/// f64 -> f16 bits with one rounding (round to nearest even), including
+/// subnormals, overflow to inf and NaN.
+uint16_t toHalfBits(double d) {
+    const _Float16 h = static_cast<_Float16>(d);
+    uint16_t bits = 0;
+    std::memcpy(&bits, &h, sizeof(bits));
+    return bits;
+}
+
+double fromHalfBits(uint16_t bits) {
+    _Float16 h;
+    std::memcpy(&h, &bits, sizeof(h));
+    return static_cast<double>(h);
+}
+
+}  // namespace
+
+bool validArch(const std::string& arch) {
+    if (arch.size() < 6 || arch.size() > 7 || arch.compare(0, 3, "gfx") != 0) return false;
+    for (size_t i = 3; i < arch.size(); ++i) {
+        const char c = arch[i];
+        const bool hex = (c >= '0' && c <= '9') || (c >= 'a' && c <= 'f');
+        if (!hex) return false;
+    }
+    return true;
+}
+
+Result<std::unique_ptr<HipLoadedKernel>> buildHipKernelArtifact(const KernelModule& km,
+                                                                const HipBackendDriverConfig& config) {
+    if (!validArch(config.arch)) {
+        return err(ErrorCode::InvalidArgument, "invalid HIP target '" + config.arch + "' (want gfx<hex>)");
+    }
+    auto plan = planModule(km);
+    if (!plan.has_value()) return err(plan.error().code, plan.error().message);
+    std::unique_ptr<HipLoadedKernel> k(new HipLoadedKernel());
+    k->km_ = km;
+    k->plan_ = std::move(*plan);
+    k->arch_ = config.arch;
+    k->bindIndex_.assign(km.buffers.size(), -1);
+    for (uint32_t b = 0; b < km.buffers.size(); ++b) {
+        const KernelBuffer& kb = km.buffers[b];
+        if (kb.isInput || kb.isOutput || kb.isTemp) {
+            k->bindIndex_[b] = static_cast<int>(k->bindables_.size());
+            k->bindables_.push_back(b);
+        }
+    }
+    for (const Step& st : k->plan_.steps) {
+        const uint32_t ids[] = {st.out.buffer, st.x, st.y, st.a, st.b, st.c, st.q, st.kk, st.bias, st.s};
+        for (const uint32_t id : ids) {
+            if (id != kInvalidId && (id >= km.buffers.size() || k->bindIndex_[id] < 0)) {
+                return err(ErrorCode::InvalidGraph, "step references a buffer that is not bindable");
+            }
+        }
+        for (const StreamRef& s : st.inputs) {
+            if (s.buffer >= km.buffers.size() || k->bindIndex_[s.buffer] < 0) {
+                return err(ErrorCode::InvalidGraph, "operand buffer is not bindable");
+            }
+        }
+    }
+    const int devices = mlkd_rt_device_count();
+    if (devices <= 0) return err(ErrorCode::UnsupportedCapability, "no HIP device visible");
+    char devArch[128] = {0};
+    if (mlkd_rt_device_arch(0, devArch, sizeof(devArch)) != 0 ||
+        std::strncmp(devArch, config.arch.c_str(), config.arch.size()) != 0) {
+        return err(ErrorCode::UnsupportedCapability,
+                   "declared target " + config.arch + " does not match device " + devArch);
+    }
+    for (Step& st : k->plan_.steps) {
+        if (st.kind != StepKind::Elementwise) continue;
+        st.source = elementwiseSource(km, st);
+        char log[4096] = {0};
+        void* fn = nullptr;
+        uint64_t fp = 0;
+        const int rc = mlkd_jit_build(st.source.data(), st.source.size(), "mlk_elementwise",
+                                      config.arch.c_str(), config.cacheDir.c_str(), &fn, &fp, log,
+                                      sizeof(log));
+        if (rc != 0) return err(ErrorCode::UnsupportedCapability, std::string("template instance: ") + log);
+        st.fn = fn;
+    }
+    k->scratch_.assign(km.buffers.size(), nullptr);
+    k->scratchElems_.assign(km.buffers.size(), 0);
+    return k;
+}
+
+int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* scalars,
+                               int64_t nScalars, int64_t elements, void* stream,
+                               std::string& why) const {
+    if (n != static_cast<int>(bindables_.size())) {
+        why = "expected " + std::to_string(bindables_.size()) + " bindings, got " + std::to_string(n);
+        return MLKHIP_BAD_BINDING;
+    }
+    std::vector<void*> ptr(km_.buffers.size(), nullptr);
+    for (int i = 0; i < n; ++i) {
+        const uint32_t b = bindables_[static_cast<size_t>(i)];
+        const KernelBuffer& kb = km_.buffers[b];
+        const int64_t need = bufferElements(kb, elements);
+        if (kb.isTemp && binds[i].ptr == nullptr) {
+            if (!plan_.tempNeeded[b]) continue;
+            std::lock_guard<std::mutex> g(scratchLock_);
+            if (scratch_[b] == nullptr || scratchElems_[b] < need) {
+                if (scratch_[b] != nullptr) mlkd_rt_free(scratch_[b]);
+                scratch_[b] = nullptr;
+                if (mlkd_rt_malloc(&scratch_[b], static_cast<size_t>(need) * dtypeBytes(kb.dtype) + 16) != 0) {
+                    why = "temp scratch allocation failed";
+                    return MLKHIP_RUNTIME;
+                }
+                scratchElems_[b] = need;
+            }
+            ptr[b] = scratch_[b];
+        } else {
+            if (binds[i].dtype != dtypeCode(kb.dtype)) {
+                why = "binding " + std::to_string(i) + " (" + kb.name + ") has the wrong dtype";
+                return MLKHIP_BAD_BINDING;
+            }
+            if (need < 0 || binds[i].elements < need || (binds[i].ptr == nullptr && need > 0)) {
+                why = "binding " + std::to_string(i) + " (" + kb.name + ") holds " +
+                      std::to_string(binds[i].elements) + " elements, module needs " + std::to_string(need);
+                return MLKHIP_BAD_BINDING;
+            }
+            ptr[b] = binds[i].ptr;
+        }
+        if (kb.isTemp && plan_.tempNeeded[b]) {
+            // Fresh zeroed scratch per run (kernel_buffers.cpp:852-878).
+            const size_t bytes = static_cast<size_t>(need) * dtypeBytes(kb.dtype);
+            const size_t padded = (bytes + 3) & ~static_cast<size_t>(3);
+            if (mlkd_rt_fill32(ptr[b], 0u, padded, stream) != 0) {
+                why = "temp zero-fill failed";
+                return MLKHIP_LAUNCH;
+            }
+        }
+    }
+    mlkd_scalars sc;
+    for (int i = 0; i < MLKD_MAX_SCALARS; ++i) sc.v[i] = (scalars != nullptr && i < nScalars) ? scalars[i] : 0.0;
+    for (const Step& st : plan_.steps) {
+        int rc = 0;
+        switch (st.kind) {
+            case StepKind::Fail:
+                if (st.failCode != 0) {
+                    why = "negative store address";
+                    return st.failCode;
+                }
+                break;
+            case StepKind::Elementwise: {
+                int64_t ext0 = st.extent[0];
+                if (st.dynamicExtent) {
+                    ext0 = elements - st.dynBegin;
+                    if (ext0 <= 0) break;
+                    for (const StreamRef& s : st.inputs) {
+                        const int64_t have = binds[bindIndex_[s.buffer]].elements;
+                        if (st.dynBegin < 0 || have < elements) {
+                            why = "dynamic 1-D loop reaches past an operand buffer";
+                            return MLKHIP_BAD_BINDING;
+                        }
+                    }
+                    if (binds[bindIndex_[st.out.buffer]].elements < elements) {
+                        why = "dynamic 1-D loop reaches past the output buffer";
+                        return MLKHIP_BAD_BINDING;
+                    }
+                }
+                const void* in[4] = {nullptr, nullptr, nullptr, nullptr};
+                for (size_t i = 0; i < st.inputs.size(); ++i) {
+                    in[i] = ptr[st.inputs[i].buffer];
+                    if (st.dynamicExtent) {
+                        in[i] = static_cast<const char*>(in[i]) +
+                                st.dynBegin * dtypeBytes(km_.buffers[st.inputs[i].buffer].dtype);
+                    }
+                }
+                void* out = ptr[st.out.buffer];
+                if (st.dynamicExtent) {
+                    out = static_cast<char*>(out) + st.dynBegin * dtypeBytes(km_.buffers[st.out.buffer].dtype);
+                }
+                int64_t rows = 1;
+                for (int d = 0; d < st.rank - 1; ++d) rows *= st.extent[d];
+                const int64_t w = st.rank == 1 ? ext0 : st.extent[st.rank - 1];
+                const int64_t chunks = rows * ((w + 15) / 16);
+                rc = mlkd_jit_launch_elementwise(st.fn, gridFor(chunks), in, out, &sc, ext0, stream);
+                break;
+            }
+            case StepKind::Softmax:
+            case StepKind::RowSum: {
+                mlkd_softmax p;
+                p.x = ptr[st.x];
+                p.y = ptr[st.y];
+                p.x_dtype = dtypeCode(km_.buffers[st.x].dtype);
+                p.y_dtype = dtypeCode(km_.buffers[st.y].dtype);
+                p.rows = st.rows;
+                p.cols = st.cols;
+                p.x_row_stride = st.cols;
+                p.y_row_stride = st.kind == StepKind::Softmax ? st.cols : 1;
+                rc = st.kind == StepKind::Softmax ? mlkd_launch_softmax(&p, stream) : mlkd_launch_rowsum(&p, stream);
+                break;
+            }
+            case StepKind::Gemm: {
+                mlkd_gemm p;
+                p.a = ptr[st.a];
+                p.b = ptr[st.b];
+                p.c = ptr[st.c];
+                p.a_dtype = dtypeCode(km_.buffers[st.a].dtype);
+                p.b_dtype = dtypeCode(km_.buffers[st.b].dtype);
+                p.c_dtype = dtypeCode(km_.buffers[st.c].dtype);
+                p.accumulate = st.accumulate ? 1 : 0;
+                p.m = st.m;
+                p.n = st.n;
+                p.k = st.k;
+                p.lda = st.lda;
+                p.ldb = st.ldb;
+                p.ldc = st.ldc;
+                rc = mlkd_launch_gemm(&p, stream);
+                break;
+            }
+            case StepKind::ScoreSoftmax: {
+                mlkd_score_softmax p;
+                p.q = ptr[st.q];
+                p.k = ptr[st.kk];
+                p.bias = ptr[st.bias];
+                p.s = ptr[st.s];
+                p.qk_dtype = dtypeCode(km_.buffers[st.q].dtype);
+                if (km_.buffers[st.kk].dtype != km_.buffers[st.q].dtype) {
+                    why = "score-softmax needs Q and K of one dtype";
+                    return MLKHIP_REFUSED;
+                }
+                p.bias_dtype = dtypeCode(km_.buffers[st.bias].dtype);
+                p.s_dtype = dtypeCode(km_.buffers[st.s].dtype);
+                p.pad = 0;
+                p.batch = st.batch;
+                p.seq = st.seq;
+                p.dim = st.dim;
+                p.div = st.div;
+                rc = mlkd_launch_score_softmax(&p, stream);
+                break;
+            }
+        }
+        if (rc != 0) {
+            why = std::string("launch failed: ") + mlkd_rt_last_error();
+            return rc;
+        }
+    }
+    return MLKHIP_OK;
+}
+
+int HipLoadedKernel::runHost(double* const* ptrs, int n, const double* scalars, int64_t nScalars,
+                             int64_t elements, std::string& why) const {
+    if (n != static_cast<int>(bindables_.size())) {
+        why = "expected " + std::to_string(bindables_.size()) + " bindables, got " + std::to_string(n);
+        return MLKHIP_BAD_BINDING;
+    }
+    // Buffers written by some step are copied back (outputs, and any input
+    // a Store targets, as the reference writes through the caller's array).
+    std::vector<bool> written(km_.buffers.size(), false);
+    for (const Step& st : plan_.steps) {
+        const uint32_t w[] = {st.out.buffer, st.y, st.c, st.s};
+        for (const uint32_t b : w) {
+            if (b != kInvalidId && b < written.size()) written[b] = true;
+        }
+    }
+    std::vector<DeviceBinding> binds(bindables_.size());
+    std::vector<void*> owned;
+    auto cleanup = [&]() {
+        for (void* p : owned) mlkd_rt_free(p);
+    };
+    int rc = MLKHIP_OK;
+    for (size_t i = 0; i < bindables_.size(); ++i) {
+        const KernelBuffer& kb = km_.buffers[bindables_[i]];
+        binds[i].dtype = dtypeCode(kb.dtype);
+        if (kb.isTemp) continue;  // the artifact materializes temps
+        const int64_t cnt = bufferElements(kb, elements);
+        if (cnt < 0) {
+            why = "buffer " + kb.name + " has no size";
+            cleanup();
+            return MLKHIP_BAD_BINDING;
+        }
+        binds[i].elements = cnt;
+        if (cnt == 0) continue;
+        if (ptrs[i] == nullptr) {
+            why = "buffer " + kb.name + " not bound";
+            cleanup();
+            return MLKHIP_BAD_BINDING;
+        }
+        const size_t bytes = static_cast<size_t>(cnt) * dtypeBytes(kb.dtype);
+        void* d = nullptr;
+        if (mlkd_rt_malloc(&d, bytes) != 0) {
+            why = "device allocation failed";
+            cleanup();
+            return MLKHIP_RUNTIME;
+        }
+        owned.push_back(d);
+        binds[i].ptr = d;
+        std::vector<unsigned char> stage(bytes);
+        const double* src = ptrs[i];
+        if (kb.dtype == Dtype::F64) {
+            std::memcpy(stage.data(), src, bytes);
+        } else if (kb.dtype == Dtype::F32) {
+            float* f = reinterpret_cast<float*>(stage.data());
+            for (int64_t e = 0; e < cnt; ++e) f[e] = static_cast<float>(src[e]);
+        } else {
+            uint16_t* h = reinterpret_cast<uint16_t*>(stage.data());
+            for (int64_t e = 0; e < cnt; ++e) h[e] = toHalfBits(src[e]);
+        }
+        if (mlkd_rt_h2d(d, stage.data(), bytes, nullptr) != 0 || mlkd_rt_sync(nullptr) != 0) {
+            why = "host-to-device copy failed";
+            cleanup();
+            return MLKHIP_RUNTIME;
+        }
+    }
+    rc = runDevice(binds.data(), static_cast<int>(binds.size()), scalars, nScalars, elements, nullptr, why);
+    if (rc == MLKHIP_OK && mlkd_rt_sync(nullptr) != 0) {
+        why = "device synchronization failed";
+        rc = MLKHIP_LAUNCH;
+    }
+    if (rc == MLKHIP_OK) {
+        for (size_t i = 0; i < bindables_.size(); ++i) {
+            const uint32_t b = bindables_[i];
+            const KernelBuffer& kb = km_.buffers[b];
+            if (kb.isTemp || !written[b] || binds[i].elements == 0) continue;
+            const int64_t cnt = binds[i].elements;
+            const size_t bytes = static_cast<size_t>(cnt) * dtypeBytes(kb.dtype);
+            std::vector<unsigned char> stage(bytes);
+            if (mlkd_rt_d2h(stage.data(), binds[i].ptr, bytes, nullptr) != 0 || mlkd_rt_sync(nullptr) != 0) {
+                why = "device-to-host copy failed";
+                rc = MLKHIP_RUNTIME;
+                break;
+            }
+            double* dst = ptrs[i];
+            if (kb.dtype == Dtype::F64) {
+                std::memcpy(dst, stage.data(), bytes);
+            } else if (kb.dtype == Dtype::F32) {
+                const float* f = reinterpret_cast<const float*>(stage.data());
+                for (int64_t e = 0; e < cnt; ++e) dst[e] = static_cast<double>(f[e]);
+            } else {
+                const uint16_t* h = reinterpret_cast<const uint16_t*>(stage.data());
+                for (int64_t e = 0; e < cnt; ++e) dst[e] = fromHalfBits(h[e]);
+            }
+        }
+    }
+    cleanup();
+    return rc;
+}
+
+}  // namespace mlk::hip
+
+// ------------------------------------------------------------------ C ABI --
+using mlk::hip::HipLoadedKernel;
+
+struct mlkhip_artifact {
+    std::unique_ptr<HipLoadedKernel> k;
+};
+
+namespace {
+thread_local std::string gLastError;
+
+int setError(int code, const std::string& m) {
+    gLastError = m;
+    return code;
+}
+
+int mapBuildError(mlk::ErrorCode c) {
+    return c == mlk::ErrorCode::UnsupportedCapability || c == mlk::ErrorCode::InvalidGraph ||
+                   c == mlk::ErrorCode::ParseError || c == mlk::ErrorCode::InvalidArgument
+               ? MLKHIP_REFUSED
+               : MLKHIP_RUNTIME;
+}
+
+void copyOut(char* dst, size_t cap, const std::string& s) {
+    if (dst == nullptr || cap == 0) return;
+    const size_t n = s.size() < cap - 1 ? s.size() : cap - 1;
+    std::memcpy(dst, s.data(), n);
+    dst[n] = '\0';
+}
+}  // namespace
+
+extern "C" {
+
+const char* mlkhip_last_error(void) { return gLastError.c_str(); }
+
+int mlkhip_valid_arch(const char* arch) { return arch != nullptr && mlk::hip::validArch(arch) ? 1 : 0; }
+
+int mlkhip_device_available(const char* arch) {
+    if (mlkd_rt_device_count() <= 0) return 0;
+    char dev[128] = {0};
+    if (mlkd_rt_device_arch(0, dev, sizeof(dev)) != 0) return 0;
+    if (arch == nullptr || arch[0] == '\0') return 1;
+    return std::strncmp(dev, arch, std::strlen(arch)) == 0 ? 1 : 0;
+}
+
+int mlkhip_build(const char* module_json, size_t len, const char* arch, const char* cache_dir,
+                 mlkhip_artifact** out) {
+    if (out == nullptr || module_json == nullptr) return setError(MLKHIP_REFUSED, "null argument");
+    *out = nullptr;
+    auto km = mlk::hip::parseKernelModule(module_json, len);
+    if (!km.has_value()) return setError(MLKHIP_REFUSED, km.error().message);
+    mlk::hip::HipBackendDriverConfig cfg;
+    cfg.arch = arch != nullptr ? arch : "";
+    cfg.cacheDir = cache_dir != nullptr ? cache_dir : "";
+    auto k = mlk::hip::buildHipKernelArtifact(*km, cfg);
+    if (!k.has_value()) {
+        const bool noDevice = k.error().message.find("no HIP device") != std::string::npos;
+        return setError(noDevice ? MLKHIP_NO_DEVICE : mapBuildError(k.error().code), k.error().message);
+    }
+    *out = new mlkhip_artifact{std::move(*k)};
+    return MLKHIP_OK;
+}
+
+int mlkhip_plan(const char* module_json, size_t len, char* class_name, size_t class_cap, char* policy,
+                size_t policy_cap, int* n_steps) {
+    auto km = mlk::hip::parseKernelModule(module_json, len);
+    if (!km.has_value()) return setError(MLKHIP_REFUSED, km.error().message);
+    auto plan = mlk::hip::planModule(*km);
+    if (!plan.has_value()) return setError(MLKHIP_REFUSED, plan.error().message);
+    copyOut(class_name, class_cap, plan->className);
+    copyOut(policy, policy_cap, plan->policy);
+    if (n_steps != nullptr) *n_steps = static_cast<int>(plan->steps.size());
+    return MLKHIP_OK;
+}
+
+long long mlkhip_compile_check(const char* module_json, size_t len, int step, const char* arch,
+                               char* source, size_t source_cap) {
+    auto km = mlk::hip::parseKernelModule(module_json, len);
+    if (!km.has_value()) return setError(-1, km.error().message);
+    auto plan = mlk::hip::planModule(*km);
+    if (!plan.has_value()) return setError(-1, plan.error().message);
+    if (step < 0 || static_cast<size_t>(step) >= plan->steps.size()) return setError(-1, "step out of range");
+    const mlk::hip::Step& st = plan->steps[static_cast<size_t>(step)];
+    if (st.kind != mlk::hip::StepKind::Elementwise) return 0;
+    const std::string src = mlk::hip::elementwiseSource(*km, st);
+    copyOut(source, source_cap, src);
+    if (arch == nullptr || !mlk::hip::validArch(arch)) return setError(-1, "invalid arch");
+    char log[4096] = {0};
+    const long long n = mlkd_jit_compile_only(src.data(), src.size(), arch, log, sizeof(log));
+    if (n < 0) return setError(-1, log);
+    return n;
+}
+
+void mlkhip_release(mlkhip_artifact* a) { delete a; }
+
+int mlkhip_is_multidim(const mlkhip_artifact* a) { return a != nullptr && a->k->plan().multiDim ? 1 : 0; }
+
+const char* mlkhip_class_name(const mlkhip_artifact* a) { return a != nullptr ? a->k->plan().className.c_str() : ""; }
+
+const char* mlkhip_policy(const mlkhip_artifact* a) { return a != nullptr ? a->k->plan().policy.c_str() : ""; }
+
+int mlkhip_num_bindables(const mlkhip_artifact* a) {
+    return a != nullptr ? static_cast<int>(a->k->bindables().size()) : 0;
+}
+
+int mlkhip_bindable_info(const mlkhip_artifact* a, int i, int32_t* dtype, int64_t* elements, int* is_input,
+                         int* is_output, int* is_temp) {
+    if (a == nullptr || i < 0 || static_cast<size_t>(i) >= a->k->bindables().size()) return MLKHIP_BAD_BINDING;
+    const mlk::hip::KernelBuffer& b = a->k->module().buffers[a->k->bindables()[static_cast<size_t>(i)]];
+    if (dtype) *dtype = b.dtype == mlk::hip::Dtype::F32 ? MLKHIP_F32 : (b.dtype == mlk::hip::Dtype::F16 ? MLKHIP_F16 : MLKHIP_F64);
+    if (elements) *elements = mlk::hip::bufferElements(b, -1);
+    if (is_input) *is_input = b.isInput ? 1 : 0;
+    if (is_output) *is_output = b.isOutput ? 1 : 0;
+    if (is_temp) *is_temp = b.isTemp ? 1 : 0;
+    return MLKHIP_OK;
+}
+
+int mlkhip_kernel(const mlkhip_artifact* a, double* const* ptrs, const int64_t* const* dims, int n_bindables,
+                  const double* scalars, int64_t n_scalars, int64_t elements) {
+    (void)dims;  // logical dims come from the module, as in the reference (the executor trusts the binder)
+    if (a == nullptr) return setError(MLKHIP_BAD_BINDING, "null artifact");
+    std::string why;
+    const int rc = a->k->runHost(ptrs, n_bindables, scalars, n_scalars, elements, why);
+    if (rc != MLKHIP_OK) setError(rc, why);
+    return rc;
+}
+
+int mlkhip_kernel_1d(const mlkhip_artifact* a, double* const* ptrs, int n_ptrs, int64_t n, const double* scalars,
+                     int64_t n_scalars) {
+    if (a == nullptr) return setError(MLKHIP_BAD_BINDING, "null artifact");
+    std::string why;
+    const int rc = a->k->runHost(ptrs, n_ptrs, scalars, n_scalars, n, why);
+    if (rc != MLKHIP_OK) setError(rc, why);
+    return rc;
+}
+
+int mlkhip_run_device(const mlkhip_artifact* a, const mlkhip_binding* binds, int n_binds, const double* scalars,
+                      int64_t n_scalars, int64_t elements, void* stream) {
+    if (a == nullptr) return setError(MLKHIP_BAD_BINDING, "null artifact");
+    std::vector<mlk::hip::DeviceBinding> b(static_cast<size_t>(n_binds > 0 ? n_binds : 0));
+    for (int i = 0; i < n_binds; ++i) {
+        b[static_cast<size_t>(i)].ptr = binds[i].ptr;
+        b[static_cast<size_t>(i)].elements = binds[i].elements;
+        b[static_cast<size_t>(i)].dtype = binds[i].dtype;
+    }
+    std::string why;
+    const int rc = a->k->runDevice(b.data(), n_binds, scalars, n_scalars, elements, stream, why);
+    if (rc != MLKHIP_OK) setError(rc, why);
+    return rc;
+}
+
+int mlkhip_time_device(const mlkhip_artifact* a, const mlkhip_binding* binds, int n_binds, const double* scalars,
+                       int64_t n_scalars, int64_t elements, void* stream, int warmup, int reps, float* ms_out) {
+    for (int w = 0; w < warmup; ++w) {
+        const int rc = mlkhip_run_device(a, binds, n_binds, scalars, n_scalars, elements, stream);
+        if (rc != MLKHIP_OK) return rc;
+    }
+    void* e0 = nullptr;
+    void* e1 = nullptr;
+    if (mlkd_rt_event_create(&e0) != 0 || mlkd_rt_event_create(&e1) != 0) return setError(MLKHIP_LAUNCH, "event create");
+    int rc = MLKHIP_OK;
+    for (int r = 0; r < reps && rc == MLKHIP_OK; ++r) {
+        mlkd_rt_event_record(e0, stream);
+        rc = mlkhip_run_device(a, binds, n_binds, scalars, n_scalars, elements, stream);
+        mlkd_rt_event_record(e1, stream);
+        float ms = 0.0f;
+        if (rc == MLKHIP_OK && mlkd_rt_event_elapsed_ms(e0, e1, &ms) != 0) rc = setError(MLKHIP_LAUNCH, "event timing");
+        if (ms_out != nullptr) ms_out[r] = ms;
+    }
+    mlkd_rt_event_destroy(e0);
+    mlkd_rt_event_destroy(e1);
+    return rc;
+}
+
+int mlkhip_malloc(void** p, size_t bytes) { return mlkd_rt_malloc(p, bytes); }
+int mlkhip_free(void* p) { return mlkd_rt_free(p); }
+int mlkhip_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+    const int rc = mlkd_rt_h2d(dst, src, bytes, nullptr);
+    return rc != 0 ? rc : mlkd_rt_sync(nullptr);
+}
+int mlkhip_memcpy_d2h(void* dst, const void* src, size_t bytes) {
+    const int rc = mlkd_rt_d2h(dst, src, bytes, nullptr);
+    return rc != 0 ? rc : mlkd_rt_sync(nullptr);
+}
+int mlkhip_fill32(void* p, uint32_t value, size_t bytes) {
+    const int rc = mlkd_rt_fill32(p, value, bytes, nullptr);
+    return rc != 0 ? rc : mlkd_rt_sync(nullptr);
+}
+int mlkhip_synchronize(void) { return mlkd_rt_device_sync(); }
+int mlkhip_stream_create(void** s) { return mlkd_rt_stream_create(s); }
+int mlkhip_stream_destroy(void* s) { return mlkd_rt_stream_destroy(s); }
+
+}  // extern "C"

@@ -1,0 +1,918 @@
+// Class recognition for the HIP backend.
+//
+// Tier-1 modules (no multi-dim feature) follow the reference executor's
+// top-level loop (runtime/src/execution/kernel_buffers.cpp:921-1085): every
+// Loop node runs its Compute children over [begin, end) paired with the
+// first Store child; Call nodes run MatMul / Softmax / ReduceSum. Multi-dim
+// modules follow the walker (:902-920): roots in id order, each recognized
+// as one of
+//   * a perfect loop nest ending in one Compute+Store pair (the poly.synth
+//     broadcast elementwise nest, poly.synth.cpp:231-353)   -> elementwise
+//   * the poly.synth GEMM nest (:58-147)                     -> gemm
+//   * the poly.synth ReduceSum nest (:153-229)               -> row sum
+//   * the poly.synth softmax nest (:363-523)                 -> softmax
+//   * a Call node                                            -> as Tier 1
+// and the three-root window batched-QK^T nest / scale+bias nest / softmax
+// nest over one temp score matrix is fused into one score-softmax launch.
+#include "planner.h"
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+
+#include "../device_abi.h"
+
+namespace mlk::hip {
+
+namespace {
+
+using K = KernelOperand::Kind;
+
+int64_t bufElems(const KernelBuffer& b) { return bufferElements(b, -1); }
+
+/// min/max of offset + sum c_d * v_d over v_d in [0, e_d).
+void affineRange(const StreamRef& s, int rank, const int64_t* ext, int64_t& lo, int64_t& hi) {
+    lo = hi = s.offset;
+    for (int d = 0; d < rank; ++d) {
+        const int64_t span = s.coeff[d] * (ext[d] - 1);
+        if (span < 0) lo += span; else hi += span;
+    }
+}
+
+/// Sufficient injectivity test of an affine map over a box: sorted by
+/// |coeff|, each coefficient exceeds the largest offset the smaller ones can
+/// reach.
+bool injective(const StreamRef& s, int rank, const int64_t* ext) {
+    int64_t c[4];
+    int64_t e[4];
+    int n = 0;
+    for (int d = 0; d < rank; ++d) {
+        if (ext[d] <= 1) continue;
+        const int64_t a = s.coeff[d] < 0 ? -s.coeff[d] : s.coeff[d];
+        if (a == 0) return false;
+        c[n] = a;
+        e[n] = ext[d];
+        ++n;
+    }
+    for (int i = 0; i < n; ++i) {
+        for (int j = i + 1; j < n; ++j) {
+            if (c[j] < c[i]) {
+                std::swap(c[i], c[j]);
+                std::swap(e[i], e[j]);
+            }
+        }
+    }
+    int64_t reach = 0;
+    for (int i = 0; i < n; ++i) {
+        if (c[i] <= reach) return false;
+        reach += c[i] * (e[i] - 1);
+    }
+    return true;
+}
+
+bool sameMap(const StreamRef& a, const StreamRef& b, int rank) {
+    if (a.buffer != b.buffer || a.offset != b.offset) return false;
+    for (int d = 0; d < rank; ++d) {
+        if (a.coeff[d] != b.coeff[d]) return false;
+    }
+    return true;
+}
+
+std::string literal(double v) {
+    if (std::isnan(v)) return "__builtin_nan(\"\")";
+    if (std::isinf(v)) return v > 0 ? "__builtin_inf()" : "(-__builtin_inf())";
+    char buf[64];
+    std::snprintf(buf, sizeof(buf), "%a", v);
+    return std::string("(") + buf + ")";
+}
+
+/// Builds the f64 chain body; stream(o) returns the stream index of an
+/// element operand. The reference evaluation (kernel_buffers.cpp:106-178):
+/// unary ops ignore b, Temp reads earlier results, ScalarParam past the
+/// table reads 0.0.
+template <class StreamOf>
+Result<std::string> chainCode(const std::vector<KernelExpr>& exprs, bool poly7, bool f32Out,
+                              StreamOf streamOf) {
+    if (exprs.empty() || exprs.size() > 64) {
+        return err(ErrorCode::UnsupportedCapability, "chain length outside 1..64");
+    }
+    std::string body;
+    auto operand = [&](const KernelOperand& o, size_t self, std::string& out) -> bool {
+        switch (o.kind) {
+            case K::Const: out = literal(o.constValue); return true;
+            case K::ElemA:
+            case K::ElemB:
+            case K::ElemIdx: {
+                const int s = streamOf(o);
+                if (s < 0) return false;
+                out = "in[" + std::to_string(s) + "]";
+                return true;
+            }
+            case K::ScalarParam:
+                if (o.index < 0 || o.index >= MLKD_MAX_SCALARS) return false;
+                out = "sc.v[" + std::to_string(o.index) + "]";
+                return true;
+            case K::Temp:
+                if (o.index < 0 || static_cast<size_t>(o.index) >= self) return false;
+                out = "t" + std::to_string(o.index);
+                return true;
+        }
+        return false;
+    };
+    for (size_t k = 0; k < exprs.size(); ++k) {
+        const KernelExpr& e = exprs[k];
+        std::string a, b = "0.0";
+        if (!operand(e.a, k, a)) {
+            return err(ErrorCode::UnsupportedCapability,
+                       "chain operand not realizable (forward temp, scalar index >= 8 or unbound stream)");
+        }
+        if (!isUnaryMath(e.op) && !operand(e.b, k, b)) {
+            return err(ErrorCode::UnsupportedCapability,
+                       "chain operand not realizable (forward temp, scalar index >= 8 or unbound stream)");
+        }
+        const std::string id = std::to_string(k);
+        body += "    const double a" + id + " = " + a + ";\n";
+        body += "    const double b" + id + " = " + b + ";\n";
+        body += "    (void)b" + id + ";\n";
+        const std::string A = "a" + id, B = "b" + id;
+        std::string v;
+        const bool last = k + 1 == exprs.size();
+        switch (e.op) {
+            case MathOp::Add: v = A + " + " + B; break;
+            case MathOp::Sub: v = A + " - " + B; break;
+            case MathOp::Mul: v = A + " * " + B; break;
+            case MathOp::Div: v = "(" + B + " != 0.0) ? " + A + " / " + B + " : 0.0"; break;
+            case MathOp::Neg: v = "-" + A; break;
+            case MathOp::Pow:
+                v = "(" + A + " == 2.0 && " + B + " == 2.0) ? " + A + " * " + A + " : pow(" + A + ", " + B + ")";
+                break;
+            case MathOp::Exp: v = "exp(" + A + ")"; break;
+            case MathOp::Log: v = "(" + A + " > 0.0) ? log(" + A + ") : 0.0"; break;
+            case MathOp::Sin:
+                v = poly7 ? ((last && f32Out) ? "mlk_p7_sin_f32out(" + A + ")" : "mlk_p7_sin(" + A + ")")
+                          : "sin(" + A + ")";
+                break;
+            case MathOp::Cos: v = "cos(" + A + ")"; break;
+            case MathOp::Tan: v = "tan(" + A + ")"; break;
+            case MathOp::Tanh: v = "tanh(" + A + ")"; break;
+            case MathOp::Sqrt: v = "(" + A + " >= 0.0) ? sqrt(" + A + ") : 0.0"; break;
+            case MathOp::Rsqrt: v = "(" + A + " > 0.0) ? 1.0 / sqrt(" + A + ") : 0.0"; break;
+            case MathOp::Erf: v = "erf(" + A + ")"; break;
+            case MathOp::Gelu:
+                v = "0.5 * " + A + " * (1.0 + tanh(0.7978845608028654 * (" + A + " + 0.044715 * " + A +
+                    " * " + A + " * " + A + ")))";
+                break;
+            default: v = "0.0"; break;
+        }
+        body += "    const double t" + id + " = " + v + ";\n";
+    }
+    body += "    return t" + std::to_string(exprs.size() - 1) + ";\n";
+    return body;
+}
+
+struct NestInfo {
+    int depth{0};
+    int64_t begin[4]{0, 0, 0, 0};
+    int64_t extent[4]{1, 1, 1, 1};
+    const KernelNode* compute{nullptr};
+    const KernelNode* store{nullptr};
+};
+
+/// Constant bounds of a loop (the walker's bound rules, :579-601, minus the
+/// affine forms, which a perfect rectangular nest does not use).
+bool constBounds(const KernelModule& km, const KernelNode& n, int64_t& b, int64_t& e) {
+    if (n.step != 1 || !n.beginCoeffs.empty() || !n.endCoeffs.empty()) return false;
+    b = n.begin;
+    if (n.end == kDynamicBound) {
+        if (n.endBuf == kInvalidId || n.endBuf >= km.buffers.size() || n.endDim < 0 ||
+            n.endDim >= static_cast<int32_t>(km.buffers[n.endBuf].dims.size())) {
+            return false;
+        }
+        e = km.buffers[n.endBuf].dims[static_cast<size_t>(n.endDim)];
+    } else {
+        e = n.end;
+    }
+    return true;
+}
+
+/// Perfect nest: Loop -> Loop -> ... -> Loop{Compute, Store}.
+bool perfectNest(const KernelModule& km, uint32_t root, NestInfo& ni) {
+    uint32_t cur = root;
+    for (;;) {
+        if (cur >= km.nodes.size() || ni.depth >= 4) return false;
+        const KernelNode& n = km.nodes[cur];
+        if (n.op != KernelOp::Loop) return false;
+        int64_t b = 0, e = 0;
+        if (!constBounds(km, n, b, e)) return false;
+        ni.begin[ni.depth] = b;
+        ni.extent[ni.depth] = e - b;
+        ++ni.depth;
+        if (n.children.size() == 1) {
+            cur = n.children[0];
+            continue;
+        }
+        if (n.children.size() != 2) return false;
+        const uint32_t c0 = n.children[0], c1 = n.children[1];
+        if (c0 >= km.nodes.size() || c1 >= km.nodes.size()) return false;
+        if (km.nodes[c0].op != KernelOp::Compute || km.nodes[c1].op != KernelOp::Store) return false;
+        ni.compute = &km.nodes[c0];
+        ni.store = &km.nodes[c1];
+        return true;
+    }
+}
+
+/// Normalizes an ElemIdx (or store) map onto box-relative variables.
+StreamRef mapRef(uint32_t buffer, const std::vector<int64_t>& coeffs, int64_t offset,
+                 const NestInfo& ni) {
+    StreamRef s;
+    s.buffer = buffer;
+    s.offset = offset;
+    for (int d = 0; d < ni.depth && d < static_cast<int>(coeffs.size()); ++d) {
+        s.coeff[d] = coeffs[static_cast<size_t>(d)];
+        s.offset += coeffs[static_cast<size_t>(d)] * ni.begin[d];
+    }
+    return s;
+}
+
+Result<void> checkInBounds(const KernelModule& km, const StreamRef& s, int rank, const int64_t* ext,
+                           const char* role) {
+    if (s.buffer >= km.buffers.size()) return err(ErrorCode::InvalidGraph, std::string(role) + " buffer id out of range");
+    const int64_t n = bufElems(km.buffers[s.buffer]);
+    int64_t lo = 0, hi = 0;
+    affineRange(s, rank, ext, lo, hi);
+    if (n <= 0 || lo < 0 || hi >= n) {
+        return err(ErrorCode::InvalidGraph,
+                   std::string(role) + " reaches outside its buffer (" + std::to_string(lo) + ".." +
+                       std::to_string(hi) + " of " + std::to_string(n) + " elements)");
+    }
+    return {};
+}
+
+/// Elementwise step over a perfect nest (poly.synth broadcast form, or any
+/// rectangular nest with an injective output map).
+Result<Step> elementwiseNest(const KernelModule& km, const NestInfo& ni) {
+    Step st;
+    st.kind = StepKind::Elementwise;
+    st.what = "elementwise-nd";
+    st.rank = ni.depth;
+    for (int d = 0; d < ni.depth; ++d) st.extent[d] = ni.extent[d];
+    for (int d = 0; d < ni.depth; ++d) {
+        if (st.extent[d] <= 0) {
+            st.kind = StepKind::Fail;  // empty loop: nothing executes
+            st.what = "empty";
+            return st;
+        }
+    }
+    const KernelNode& cp = *ni.compute;
+    const KernelNode& so = *ni.store;
+    for (const KernelExpr& e : cp.exprs) {
+        for (const KernelOperand* o : {&e.a, &e.b}) {
+            if (o->kind == K::ElemA || o->kind == K::ElemB) {
+                return err(ErrorCode::InvalidGraph, "walker: legacy element operand in a multi-dim compute");
+            }
+        }
+    }
+    if (so.bufferOut >= km.buffers.size()) return err(ErrorCode::InvalidArgument, "walker: output buffer not bound");
+    st.out = mapRef(so.bufferOut, so.outIndexCoeffs, so.outIndexOffset, ni);
+    st.accum = so.accum;
+    {
+        int64_t lo = 0, hi = 0;
+        affineRange(st.out, st.rank, st.extent, lo, hi);
+        if (lo < 0) {
+            st.kind = StepKind::Fail;
+            st.what = "negative-store";
+            st.failCode = 1;
+            return st;
+        }
+    }
+    MLK_TRYV(checkInBounds(km, st.out, st.rank, st.extent, "store"));
+    if (!injective(st.out, st.rank, st.extent)) {
+        return err(ErrorCode::UnsupportedCapability,
+                   "store map is not injective over the nest (a reduction, not an elementwise class)");
+    }
+    std::vector<StreamRef>& ins = st.inputs;
+    bool bad = false;
+    auto streamOf = [&](const KernelOperand& o) -> int {
+        if (o.kind != K::ElemIdx || o.index < 0 || static_cast<size_t>(o.index) >= km.buffers.size()) {
+            bad = true;
+            return -1;
+        }
+        const StreamRef s = mapRef(static_cast<uint32_t>(o.index), o.idxCoeffs, o.idxOffset, ni);
+        for (size_t i = 0; i < ins.size(); ++i) {
+            if (sameMap(ins[i], s, st.rank)) return static_cast<int>(i);
+        }
+        if (ins.size() >= 4) {
+            bad = true;
+            return -1;
+        }
+        ins.push_back(s);
+        return static_cast<int>(ins.size() - 1);
+    };
+    const Dtype od = km.buffers[so.bufferOut].dtype;
+    const bool f32Out = (od == Dtype::F32 || od == Dtype::F16) && so.accum == AccumMode::None;
+    auto body = chainCode(cp.exprs, cp.family == "poly7", f32Out, streamOf);
+    if (!body.has_value()) return err(body.error().code, body.error().message);
+    if (bad) return err(ErrorCode::UnsupportedCapability, "more than 4 distinct element streams");
+    for (const StreamRef& s : ins) {
+        MLK_TRYV(checkInBounds(km, s, st.rank, st.extent, "operand"));
+        if (s.buffer == so.bufferOut && !sameMap(s, st.out, st.rank)) {
+            return err(ErrorCode::UnsupportedCapability,
+                       "operand reads the stored buffer at another element (loop-carried)");
+        }
+    }
+    st.chainBody = *body;
+    return st;
+}
+
+/// Tier-1 Loop: each Compute child with the first Store child
+/// (kernel_buffers.cpp:921-1000, runElementwiseRange :342-402).
+Result<std::vector<Step>> tier1Loop(const KernelModule& km, const KernelNode& loop) {
+    std::vector<Step> out;
+    const KernelNode* store = nullptr;
+    for (const uint32_t sid : loop.children) {
+        if (sid < km.nodes.size() && km.nodes[sid].op == KernelOp::Store) {
+            store = &km.nodes[sid];
+            break;
+        }
+    }
+    for (const uint32_t cid : loop.children) {
+        if (cid >= km.nodes.size()) return err(ErrorCode::InvalidGraph, "kernel child node out of range");
+    }
+    for (const uint32_t cid : loop.children) {
+        const KernelNode& c = km.nodes[cid];
+        if (c.op != KernelOp::Compute) continue;
+        const KernelNode& so = store != nullptr ? *store : c;
+        bool needsA = c.exprs.empty(), needsB = c.exprs.empty();
+        for (const KernelExpr& e : c.exprs) {
+            for (const KernelOperand* o : {&e.a, &e.b}) {
+                needsA = needsA || o->kind == K::ElemA;
+                needsB = needsB || o->kind == K::ElemB;
+            }
+        }
+        auto valid = [&](uint32_t bid) { return bid != kInvalidId && bid < km.buffers.size(); };
+        // Unbound operands or output: the reference skips the pair.
+        if (!valid(so.bufferOut) || (needsA && !valid(c.bufferA)) || (needsB && !valid(c.bufferB))) continue;
+        Step st;
+        st.kind = StepKind::Elementwise;
+        st.what = "elementwise-1d";
+        st.rank = 1;
+        int64_t begin = loop.begin;
+        int64_t end = loop.end;
+        if (end == kDynamicBound) {
+            st.dynamicExtent = true;
+            st.dynBegin = begin;
+        } else {
+            if (end < begin) end = begin;
+            st.extent[0] = end - begin;
+        }
+        std::vector<KernelExpr> exprs = c.exprs;
+        if (exprs.empty()) {  // legacy single op over ElemA, ElemB
+            KernelExpr e;
+            e.op = c.math;
+            e.a.kind = K::ElemA;
+            e.b.kind = K::ElemB;
+            exprs.push_back(e);
+        }
+        auto ref = [&](uint32_t bid) {
+            StreamRef s;
+            s.buffer = bid;
+            s.offset = st.dynamicExtent ? 0 : begin;
+            s.coeff[0] = 1;
+            return s;
+        };
+        int slotA = -1, slotB = -1;
+        auto streamOf = [&](const KernelOperand& o) -> int {
+            if (o.kind == K::ElemA) {
+                if (slotA < 0) {
+                    st.inputs.push_back(ref(c.bufferA));
+                    slotA = static_cast<int>(st.inputs.size() - 1);
+                }
+                return slotA;
+            }
+            if (o.kind == K::ElemB) {
+                if (slotB < 0) {
+                    st.inputs.push_back(ref(c.bufferB));
+                    slotB = static_cast<int>(st.inputs.size() - 1);
+                }
+                return slotB;
+            }
+            return -1;  // ElemIdx is a multi-dim operand
+        };
+        const Dtype od = km.buffers[so.bufferOut].dtype;
+        auto body = chainCode(exprs, c.family == "poly7", od == Dtype::F32 || od == Dtype::F16, streamOf);
+        if (!body.has_value()) return err(body.error().code, body.error().message);
+        st.chainBody = *body;
+        st.out = ref(so.bufferOut);
+        if (!st.dynamicExtent) {
+            if (st.extent[0] == 0) continue;
+            if (begin < 0) return err(ErrorCode::InvalidGraph, "1-D loop begins below element 0");
+            for (const StreamRef& s : st.inputs) {
+                MLK_TRYV(checkInBounds(km, s, 1, st.extent, "1-D operand"));
+            }
+            MLK_TRYV(checkInBounds(km, st.out, 1, st.extent, "1-D store"));
+        }
+        out.push_back(std::move(st));
+    }
+    return out;
+}
+
+Result<Step> callStep(const KernelModule& km, const KernelNode& top, bool walker) {
+    Step st;
+    if (top.math == MathOp::MatMul) {
+        if (top.bufferA >= km.buffers.size() || top.bufferB >= km.buffers.size() ||
+            top.bufferOut >= km.buffers.size()) {
+            return err(ErrorCode::InvalidGraph, "matmul buffer id out of range");
+        }
+        const auto& da = km.buffers[top.bufferA].dims;
+        const auto& db = km.buffers[top.bufferB].dims;
+        const auto& dc = km.buffers[top.bufferOut].dims;
+        if (da.size() != 2 || db.size() != 2 || dc.size() != 2) {
+            return err(ErrorCode::InvalidGraph, "matmul requires rank-2 buffer dims");
+        }
+        const int64_t m = da[0], k = da[1];
+        const int64_t n = walker ? dc[1] : db[1];
+        if (db[0] != k || dc[0] != m || dc[1] != n) return err(ErrorCode::InvalidGraph, "matmul operand shapes incompatible");
+        if (walker && db[1] != n) {
+            return err(ErrorCode::UnsupportedCapability, "matmul with B columns != C columns");
+        }
+        st.kind = StepKind::Gemm;
+        st.what = "gemm-call";
+        st.a = top.bufferA;
+        st.b = top.bufferB;
+        st.c = top.bufferOut;
+        st.m = m;
+        st.n = n;
+        st.k = k;
+        st.lda = k;
+        st.ldb = n;
+        st.ldc = n;
+        st.accumulate = true;  // gemmRowBlock accumulates into C (:406-432)
+        return st;
+    }
+    if (top.math == MathOp::Softmax || top.math == MathOp::ReduceSum) {
+        const bool soft = top.math == MathOp::Softmax;
+        if (top.bufferA >= km.buffers.size() || top.bufferOut >= km.buffers.size()) {
+            return err(ErrorCode::InvalidGraph, soft ? "softmax buffer id out of range" : "reducesum buffer id out of range");
+        }
+        const auto& da = km.buffers[top.bufferA].dims;
+        const auto& dy = km.buffers[top.bufferOut].dims;
+        if (da.size() != 2 || dy.size() != (soft ? 2u : 1u)) {
+            return err(ErrorCode::InvalidGraph, soft ? "softmax requires rank-2 operand and output"
+                                                     : "reducesum requires rank-2 input over rank-1 output");
+        }
+        const int64_t m = da[0], k = da[1];
+        if (dy[0] != m || (soft && dy[1] != k) || k <= 0 || m <= 0) {
+            return err(ErrorCode::InvalidGraph, soft ? "softmax operand shapes incompatible" : "reducesum operand shapes incompatible");
+        }
+        st.kind = soft ? StepKind::Softmax : StepKind::RowSum;
+        st.what = soft ? "softmax-call" : "reducesum-call";
+        st.x = top.bufferA;
+        st.y = top.bufferOut;
+        st.rows = m;
+        st.cols = k;
+        return st;
+    }
+    return err(ErrorCode::UnsupportedCapability, "no executor for call target");
+}
+
+// ---------------------------------------------------------- patterns ----
+const KernelNode* node(const KernelModule& km, uint32_t id) {
+    return id < km.nodes.size() ? &km.nodes[id] : nullptr;
+}
+
+bool isLoop0(const KernelNode* n, int64_t& extent) {
+    if (n == nullptr || n->op != KernelOp::Loop || n->step != 1 || n->begin != 0 ||
+        !n->beginCoeffs.empty() || !n->endCoeffs.empty() || n->end <= 0) {
+        return false;
+    }
+    extent = n->end;
+    return true;
+}
+
+bool isConstStore(const KernelNode* c, double value) {
+    if (c == nullptr || c->op != KernelOp::Compute || c->exprs.size() != 1) return false;
+    const KernelExpr& e = c->exprs[0];
+    if (e.op != MathOp::Add || e.a.kind != K::Const || e.b.kind != K::Const || e.b.constValue != 0.0) return false;
+    if (std::isinf(value)) return std::isinf(e.a.constValue) && (e.a.constValue < 0) == (value < 0);
+    return e.a.constValue == value;
+}
+
+bool elemIs(const KernelOperand& o, uint32_t buf, std::initializer_list<int64_t> coeffs) {
+    if (o.kind != K::ElemIdx || o.index != static_cast<int64_t>(buf) || o.idxOffset != 0) return false;
+    if (o.idxCoeffs.size() != coeffs.size()) return false;
+    size_t i = 0;
+    for (const int64_t c : coeffs) {
+        if (o.idxCoeffs[i++] != c) return false;
+    }
+    return true;
+}
+
+bool storeIs(const KernelNode* s, uint32_t buf, std::initializer_list<int64_t> coeffs, AccumMode acc) {
+    if (s == nullptr || s->op != KernelOp::Store || s->bufferOut != buf || s->outIndexOffset != 0 || s->accum != acc) {
+        return false;
+    }
+    if (s->outIndexCoeffs.size() != coeffs.size()) return false;
+    size_t i = 0;
+    for (const int64_t c : coeffs) {
+        if (s->outIndexCoeffs[i++] != c) return false;
+    }
+    return true;
+}
+
+bool isPassThrough(const KernelExpr& e, uint32_t buf, std::initializer_list<int64_t> coeffs) {
+    // Sub(x, 0) is the exact passthrough of the softmax nest; Add(x, 0) the
+    // GEMM operand load (which maps -0.0 to +0.0, immaterial to a product).
+    return (e.op == MathOp::Sub || e.op == MathOp::Add) && e.b.kind == K::Const && e.b.constValue == 0.0 &&
+           elemIs(e.a, buf, coeffs);
+}
+
+/// poly.synth softmax nest (:363-523): m{ RM=-inf; k{RM max= x}; k{E=exp(x-RM)};
+/// S=0; k{S += E}; k{Y = E/S} }.
+bool matchSoftmaxNest(const KernelModule& km, uint32_t root, Step& st) {
+    const KernelNode* ml = node(km, root);
+    int64_t M = 0;
+    if (!isLoop0(ml, M) || ml->children.size() != 8) return false;
+    const auto& ch = ml->children;
+    const KernelNode* c0 = node(km, ch[0]);
+    const KernelNode* s0 = node(km, ch[1]);
+    const KernelNode* lRM = node(km, ch[2]);
+    const KernelNode* lE = node(km, ch[3]);
+    const KernelNode* c3 = node(km, ch[4]);
+    const KernelNode* s3 = node(km, ch[5]);
+    const KernelNode* lS = node(km, ch[6]);
+    const KernelNode* lD = node(km, ch[7]);
+    if (s0 == nullptr || s3 == nullptr) return false;
+    const uint32_t rm = s0->bufferOut, sm = s3->bufferOut;
+    if (!isConstStore(c0, -INFINITY) || !storeIs(s0, rm, {1}, AccumMode::None)) return false;
+    if (!isConstStore(c3, 0.0) || !storeIs(s3, sm, {1}, AccumMode::None)) return false;
+    int64_t K1 = 0, K2 = 0, K3 = 0, K4 = 0;
+    if (!isLoop0(lRM, K1) || !isLoop0(lE, K2) || !isLoop0(lS, K3) || !isLoop0(lD, K4)) return false;
+    if (K1 != K2 || K1 != K3 || K1 != K4) return false;
+    for (const KernelNode* l : {lRM, lE, lS, lD}) {
+        if (l->children.size() != 2) return false;
+    }
+    const KernelNode* c1 = node(km, lRM->children[0]);
+    const KernelNode* s1 = node(km, lRM->children[1]);
+    const KernelNode* c2 = node(km, lE->children[0]);
+    const KernelNode* s2 = node(km, lE->children[1]);
+    const KernelNode* c4 = node(km, lS->children[0]);
+    const KernelNode* s4 = node(km, lS->children[1]);
+    const KernelNode* c5 = node(km, lD->children[0]);
+    const KernelNode* s5 = node(km, lD->children[1]);
+    for (const KernelNode* c : {c1, c2, c4, c5}) {
+        if (c == nullptr || c->op != KernelOp::Compute) return false;
+    }
+    if (c1->exprs.size() != 1 || c2->exprs.size() != 2 || c4->exprs.size() != 1 || c5->exprs.size() != 1) return false;
+    const KernelOperand& xo = c1->exprs[0].a;
+    if (xo.kind != K::ElemIdx || xo.index < 0 || static_cast<size_t>(xo.index) >= km.buffers.size()) return false;
+    const uint32_t x = static_cast<uint32_t>(xo.index);
+    const int64_t K = K1;
+    if (!isPassThrough(c1->exprs[0], x, {K, 1}) || c1->exprs[0].op != MathOp::Sub) return false;
+    if (!storeIs(s1, rm, {1, 0}, AccumMode::Max)) return false;
+    const KernelExpr& e20 = c2->exprs[0];
+    const KernelExpr& e21 = c2->exprs[1];
+    if (e20.op != MathOp::Sub || !elemIs(e20.a, x, {K, 1}) || !elemIs(e20.b, rm, {1, 0})) return false;
+    if (e21.op != MathOp::Exp || e21.a.kind != K::Temp || e21.a.index != 0) return false;
+    if (s2 == nullptr || s2->op != KernelOp::Store) return false;
+    const uint32_t eb = s2->bufferOut;
+    if (!storeIs(s2, eb, {K, 1}, AccumMode::None)) return false;
+    if (!isPassThrough(c4->exprs[0], eb, {K, 1}) || c4->exprs[0].op != MathOp::Sub) return false;
+    if (!storeIs(s4, sm, {1, 0}, AccumMode::Add)) return false;
+    const KernelExpr& e5 = c5->exprs[0];
+    if (e5.op != MathOp::Div || !elemIs(e5.a, eb, {K, 1}) || !elemIs(e5.b, sm, {1, 0})) return false;
+    if (s5 == nullptr || s5->op != KernelOp::Store) return false;
+    const uint32_t y = s5->bufferOut;
+    if (!storeIs(s5, y, {K, 1}, AccumMode::None)) return false;
+    // The three scratch buffers must be temps private to this nest, sized as
+    // the statements address them; x and y must hold M*K elements.
+    for (const uint32_t t : {rm, eb, sm}) {
+        if (t >= km.buffers.size() || !km.buffers[t].isTemp) return false;
+    }
+    if (bufElems(km.buffers[rm]) < M || bufElems(km.buffers[sm]) < M || bufElems(km.buffers[eb]) < M * K) return false;
+    if (y >= km.buffers.size() || bufElems(km.buffers[x]) < M * K || bufElems(km.buffers[y]) < M * K) return false;
+    if (x == rm || x == eb || x == sm || y == rm || y == eb || y == sm) return false;
+    st.kind = StepKind::Softmax;
+    st.what = "softmax-nest";
+    st.x = x;
+    st.y = y;
+    st.rows = M;
+    st.cols = K;
+    return true;
+}
+
+/// poly.synth ReduceSum nest (:153-229): i{ Y=0; k{ Y += A } }.
+bool matchReduceSumNest(const KernelModule& km, uint32_t root, Step& st) {
+    const KernelNode* il = node(km, root);
+    int64_t M = 0, Kx = 0;
+    if (!isLoop0(il, M) || il->children.size() != 3) return false;
+    const KernelNode* c0 = node(km, il->children[0]);
+    const KernelNode* s0 = node(km, il->children[1]);
+    const KernelNode* kl = node(km, il->children[2]);
+    if (s0 == nullptr || !isConstStore(c0, 0.0)) return false;
+    const uint32_t y = s0->bufferOut;
+    if (!storeIs(s0, y, {1}, AccumMode::None)) return false;
+    if (!isLoop0(kl, Kx) || kl->children.size() != 2) return false;
+    const KernelNode* c1 = node(km, kl->children[0]);
+    const KernelNode* s1 = node(km, kl->children[1]);
+    if (c1 == nullptr || c1->op != KernelOp::Compute || c1->exprs.size() != 1) return false;
+    const KernelOperand& xo = c1->exprs[0].a;
+    if (xo.kind != K::ElemIdx || xo.index < 0 || static_cast<size_t>(xo.index) >= km.buffers.size()) return false;
+    const uint32_t x = static_cast<uint32_t>(xo.index);
+    if (c1->exprs[0].op != MathOp::Add || !isPassThrough(c1->exprs[0], x, {Kx, 1})) return false;
+    if (!storeIs(s1, y, {1, 0}, AccumMode::Add)) return false;
+    if (x == y || bufElems(km.buffers[x]) < M * Kx || y >= km.buffers.size() || bufElems(km.buffers[y]) < M) return false;
+    st.kind = StepKind::RowSum;
+    st.what = "reducesum-nest";
+    st.x = x;
+    st.y = y;
+    st.rows = M;
+    st.cols = Kx;
+    return true;
+}
+
+/// poly.synth GEMM nest (:58-147): i{ j{ C=0; k{ C += A[i,k]*B[k,j] } } }.
+bool matchGemmNest(const KernelModule& km, uint32_t root, Step& st) {
+    const KernelNode* il = node(km, root);
+    int64_t M = 0, N = 0, Kx = 0;
+    if (!isLoop0(il, M) || il->children.size() != 1) return false;
+    const KernelNode* jl = node(km, il->children[0]);
+    if (!isLoop0(jl, N) || jl->children.size() != 3) return false;
+    const KernelNode* c0 = node(km, jl->children[0]);
+    const KernelNode* s0 = node(km, jl->children[1]);
+    const KernelNode* kl = node(km, jl->children[2]);
+    if (s0 == nullptr || c0 == nullptr || c0->op != KernelOp::Compute || c0->exprs.size() != 1) return false;
+    const KernelExpr& z = c0->exprs[0];
+    if (z.op != MathOp::Add || z.a.kind != K::Const || z.a.constValue != 0.0 || z.b.kind != K::Const ||
+        z.b.constValue != 0.0) {
+        return false;
+    }
+    const uint32_t c = s0->bufferOut;
+    if (!storeIs(s0, c, {N, 1}, AccumMode::None)) return false;
+    if (!isLoop0(kl, Kx) || kl->children.size() != 2) return false;
+    const KernelNode* c1 = node(km, kl->children[0]);
+    const KernelNode* s1 = node(km, kl->children[1]);
+    if (c1 == nullptr || c1->op != KernelOp::Compute || c1->exprs.size() != 3) return false;
+    const KernelOperand& ao = c1->exprs[0].a;
+    const KernelOperand& bo = c1->exprs[1].a;
+    if (ao.kind != K::ElemIdx || bo.kind != K::ElemIdx || ao.index < 0 || bo.index < 0 ||
+        static_cast<size_t>(ao.index) >= km.buffers.size() || static_cast<size_t>(bo.index) >= km.buffers.size()) {
+        return false;
+    }
+    const uint32_t a = static_cast<uint32_t>(ao.index), b = static_cast<uint32_t>(bo.index);
+    if (!isPassThrough(c1->exprs[0], a, {Kx, 0, 1}) || c1->exprs[0].op != MathOp::Add) return false;
+    if (!isPassThrough(c1->exprs[1], b, {0, 1, N}) || c1->exprs[1].op != MathOp::Add) return false;
+    const KernelExpr& mul = c1->exprs[2];
+    if (mul.op != MathOp::Mul || mul.a.kind != K::Temp || mul.a.index != 0 || mul.b.kind != K::Temp || mul.b.index != 1) {
+        return false;
+    }
+    if (!storeIs(s1, c, {N, 1, 0}, AccumMode::Add)) return false;
+    if (c >= km.buffers.size() || c == a || c == b) return false;
+    if (bufElems(km.buffers[a]) < M * Kx || bufElems(km.buffers[b]) < Kx * N || bufElems(km.buffers[c]) < M * N) return false;
+    st.kind = StepKind::Gemm;
+    st.what = "gemm-nest";
+    st.a = a;
+    st.b = b;
+    st.c = c;
+    st.m = M;
+    st.n = N;
+    st.k = Kx;
+    st.lda = Kx;
+    st.ldb = N;
+    st.ldc = N;
+    st.accumulate = false;  // S0 zeroes C first
+    return true;
+}
+
+/// Batched score nest: b{ i{ j{ SC=0; k{ SC += Q[b,i,k]*K[b,j,k] } } } } over
+/// a temp SC[batch*seq, seq]; then r{ j{ SC = Add(Div(SC, c), bias[j]) } };
+/// then the softmax nest over SC rows into S. Fused into one launch.
+bool matchScoreSoftmax(const KernelModule& km, const std::vector<uint32_t>& roots, size_t at, Step& st) {
+    if (at + 2 >= roots.size()) return false;
+    const KernelNode* bl = node(km, roots[at]);
+    int64_t B = 0, S = 0, S2 = 0, D = 0;
+    if (!isLoop0(bl, B) || bl->children.size() != 1) return false;
+    const KernelNode* il = node(km, bl->children[0]);
+    if (!isLoop0(il, S) || il->children.size() != 1) return false;
+    const KernelNode* jl = node(km, il->children[0]);
+    if (!isLoop0(jl, S2) || S2 != S || jl->children.size() != 3) return false;
+    const KernelNode* c0 = node(km, jl->children[0]);
+    const KernelNode* s0 = node(km, jl->children[1]);
+    const KernelNode* kl = node(km, jl->children[2]);
+    if (s0 == nullptr || c0 == nullptr || c0->op != KernelOp::Compute || c0->exprs.size() != 1) return false;
+    const KernelExpr& z = c0->exprs[0];
+    if (z.op != MathOp::Add || z.a.kind != K::Const || z.a.constValue != 0.0 || z.b.kind != K::Const ||
+        z.b.constValue != 0.0) {
+        return false;
+    }
+    const uint32_t sc = s0->bufferOut;
+    if (!storeIs(s0, sc, {S * S, S, 1}, AccumMode::None)) return false;
+    if (!isLoop0(kl, D) || kl->children.size() != 2) return false;
+    const KernelNode* c1 = node(km, kl->children[0]);
+    const KernelNode* s1 = node(km, kl->children[1]);
+    if (c1 == nullptr || c1->op != KernelOp::Compute || c1->exprs.size() != 3) return false;
+    const KernelOperand& qo = c1->exprs[0].a;
+    const KernelOperand& ko = c1->exprs[1].a;
+    if (qo.kind != K::ElemIdx || ko.kind != K::ElemIdx || qo.index < 0 || ko.index < 0 ||
+        static_cast<size_t>(qo.index) >= km.buffers.size() || static_cast<size_t>(ko.index) >= km.buffers.size()) {
+        return false;
+    }
+    const uint32_t q = static_cast<uint32_t>(qo.index), kb = static_cast<uint32_t>(ko.index);
+    if (!isPassThrough(c1->exprs[0], q, {S * D, D, 0, 1}) || c1->exprs[0].op != MathOp::Add) return false;
+    if (!isPassThrough(c1->exprs[1], kb, {S * D, 0, D, 1}) || c1->exprs[1].op != MathOp::Add) return false;
+    const KernelExpr& mul = c1->exprs[2];
+    if (mul.op != MathOp::Mul || mul.a.kind != K::Temp || mul.a.index != 0 || mul.b.kind != K::Temp || mul.b.index != 1) {
+        return false;
+    }
+    if (!storeIs(s1, sc, {S * S, S, 1, 0}, AccumMode::Add)) return false;
+    if (sc >= km.buffers.size() || !km.buffers[sc].isTemp) return false;
+    // Root 2: r{ j{ SC = Add(Div(SC, c), bias[j]) } }.
+    NestInfo ni;
+    if (!perfectNest(km, roots[at + 1], ni) || ni.depth != 2 || ni.begin[0] != 0 || ni.begin[1] != 0 ||
+        ni.extent[0] != B * S || ni.extent[1] != S) {
+        return false;
+    }
+    const KernelNode& ec = *ni.compute;
+    if (ec.exprs.size() != 2 || !storeIs(ni.store, sc, {S, 1}, AccumMode::None)) return false;
+    const KernelExpr& dv = ec.exprs[0];
+    const KernelExpr& ad = ec.exprs[1];
+    if (dv.op != MathOp::Div || !elemIs(dv.a, sc, {S, 1}) || dv.b.kind != K::Const || dv.b.constValue == 0.0) return false;
+    if (ad.op != MathOp::Add || ad.a.kind != K::Temp || ad.a.index != 0 || ad.b.kind != K::ElemIdx) return false;
+    if (ad.b.index < 0 || static_cast<size_t>(ad.b.index) >= km.buffers.size()) return false;
+    const uint32_t bias = static_cast<uint32_t>(ad.b.index);
+    if (!elemIs(ad.b, bias, {0, 1})) return false;
+    // Root 3: softmax over SC rows.
+    Step soft;
+    if (!matchSoftmaxNest(km, roots[at + 2], soft) || soft.x != sc || soft.rows != B * S || soft.cols != S) return false;
+    // SC must not be read anywhere else in the module.
+    if (bufElems(km.buffers[q]) < B * S * D || bufElems(km.buffers[kb]) < B * S * D ||
+        bufElems(km.buffers[bias]) < S || bufElems(km.buffers[soft.y]) < B * S * S) {
+        return false;
+    }
+    st.kind = StepKind::ScoreSoftmax;
+    st.what = "score-softmax";
+    st.q = q;
+    st.kk = kb;
+    st.bias = bias;
+    st.s = soft.y;
+    st.batch = B;
+    st.seq = S;
+    st.dim = D;
+    st.div = dv.b.constValue;
+    return true;
+}
+
+void markTemps(const KernelModule& km, const Step& st, std::vector<bool>& need) {
+    auto mark = [&](uint32_t b) {
+        if (b < km.buffers.size() && km.buffers[b].isTemp) need[b] = true;
+    };
+    switch (st.kind) {
+        case StepKind::Elementwise:
+            for (const StreamRef& s : st.inputs) mark(s.buffer);
+            mark(st.out.buffer);
+            break;
+        case StepKind::Softmax:
+        case StepKind::RowSum:
+            mark(st.x);
+            mark(st.y);
+            break;
+        case StepKind::Gemm:
+            mark(st.a);
+            mark(st.b);
+            mark(st.c);
+            break;
+        case StepKind::ScoreSoftmax:
+            mark(st.q);
+            mark(st.kk);
+            mark(st.bias);
+            mark(st.s);
+            break;
+        case StepKind::Fail:
+            break;
+    }
+}
+
+std::string policyFor(const KernelModule& km, const std::vector<Step>& steps) {
+    bool transcend = false, gemm16 = false, gemm32 = false, soft = false, p7out = false, score = false;
+    for (const Step& st : steps) {
+        switch (st.kind) {
+            case StepKind::Elementwise:
+                if (st.chainBody.find("mlk_p7_sin_f32out") != std::string::npos) p7out = true;
+                for (const char* f : {"exp(", "log(", "sin(", "cos(", "tan(", "tanh(", "erf(", "pow("}) {
+                    if (st.chainBody.find(std::string(" ") + f) != std::string::npos ||
+                        st.chainBody.find(std::string("(") + f) != std::string::npos) {
+                        transcend = true;
+                    }
+                }
+                break;
+            case StepKind::Softmax: soft = true; break;
+            case StepKind::RowSum: soft = true; break;
+            case StepKind::Gemm:
+                if (km.buffers[st.a].dtype == Dtype::F16 || km.buffers[st.b].dtype == Dtype::F16) gemm16 = true;
+                else gemm32 = true;
+                break;
+            case StepKind::ScoreSoftmax: score = true; break;
+            case StepKind::Fail: break;
+        }
+    }
+    if (score || gemm16) return "tol-rel1e-2-gfx950-v1";
+    if (gemm32) return "tol-rel1e-5sqrtk-gfx950-v1";
+    if (soft || transcend) return "tol-rel1e-6-gfx950-v1";
+    if (p7out) return "tol-4ulp-f32-gfx950-v1";
+    return "bitexact-rne-gfx950-v1";
+}
+
+}  // namespace
+
+int64_t bufferElements(const KernelBuffer& b, int64_t dynamicElements) {
+    if (!b.dims.empty()) {
+        int64_t n = 1;
+        for (const int64_t d : b.dims) {
+            if (d < 0) return -1;
+            n *= d;
+        }
+        return n;
+    }
+    if (b.elements >= 0) return b.elements;
+    return dynamicElements;
+}
+
+Result<Plan> planModule(const KernelModule& km) {
+    Plan plan;
+    plan.tempNeeded.assign(km.buffers.size(), false);
+    if (km.nodes.empty()) return err(ErrorCode::InvalidGraph, "kernel module has no nodes");
+    for (const KernelBuffer& b : km.buffers) {
+        if (b.dtype == Dtype::Other && (b.isInput || b.isOutput || b.isTemp)) {
+            return err(ErrorCode::UnsupportedCapability, "buffer dtype outside f16/f32/f64: " + b.name);
+        }
+    }
+    plan.multiDim = isMultiDimModule(km);
+    if (!plan.multiDim) {
+        for (const KernelNode& top : km.nodes) {
+            if (top.op == KernelOp::Loop) {
+                auto steps = tier1Loop(km, top);
+                if (!steps.has_value()) return err(steps.error().code, steps.error().message);
+                for (Step& s : *steps) plan.steps.push_back(std::move(s));
+            } else if (top.op == KernelOp::Call) {
+                auto st = callStep(km, top, false);
+                if (!st.has_value()) return err(st.error().code, st.error().message);
+                plan.steps.push_back(std::move(*st));
+            }
+        }
+    } else {
+        const std::vector<uint32_t> roots = forestRoots(km);
+        for (size_t i = 0; i < roots.size(); ++i) {
+            const KernelNode& r = km.nodes[roots[i]];
+            Step st;
+            if (r.op == KernelOp::Call) {
+                auto cs = callStep(km, r, true);
+                if (!cs.has_value()) return err(cs.error().code, cs.error().message);
+                plan.steps.push_back(std::move(*cs));
+                continue;
+            }
+            if (r.op != KernelOp::Loop) {
+                if (r.op == KernelOp::Guard && r.hasAffineGuard()) {
+                    return err(ErrorCode::UnsupportedCapability, "guarded root: no HIP class (generic nest path)");
+                }
+                continue;  // Compute/Store/etc. at root carry no semantics for the walker
+            }
+            if (matchScoreSoftmax(km, roots, i, st)) {
+                plan.steps.push_back(std::move(st));
+                i += 2;
+                continue;
+            }
+            if (matchSoftmaxNest(km, roots[i], st) || matchGemmNest(km, roots[i], st) ||
+                matchReduceSumNest(km, roots[i], st)) {
+                plan.steps.push_back(std::move(st));
+                continue;
+            }
+            NestInfo ni;
+            if (perfectNest(km, roots[i], ni)) {
+                auto es = elementwiseNest(km, ni);
+                if (!es.has_value()) return err(es.error().code, es.error().message);
+                plan.steps.push_back(std::move(*es));
+                continue;
+            }
+            return err(ErrorCode::UnsupportedCapability,
+                       "loop nest rooted at node " + std::to_string(roots[i]) +
+                           " matches no HIP class (tiled/guarded/affine-bound nests need the generic path)");
+        }
+    }
+    for (const Step& st : plan.steps) markTemps(km, st, plan.tempNeeded);
+    for (size_t b = 0; b < km.buffers.size(); ++b) {
+        if (!plan.tempNeeded[b]) continue;
+        const int64_t n = bufElems(km.buffers[b]);
+        if (n <= 0 || n > kTempElementsLimit) {
+            return err(ErrorCode::InvalidGraph, "temp buffer element count out of range");
+        }
+    }
+    std::string cls;
+    for (const Step& st : plan.steps) {
+        if (!cls.empty()) cls += "+";
+        cls += st.what;
+    }
+    plan.className = cls.empty() ? "empty" : cls;
+    plan.policy = policyFor(km, plan.steps);
+    return plan;
+}
+
+}  // namespace mlk::hip

@@ -1,0 +1,80 @@
+// Class recognition: turns a KernelModule into a plan of launches of the
+// hand-written gfx950 kernels, with every address proved in bounds on the
+// host before anything runs on the device.
+#pragma once
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "kernel_ir.h"
+
+namespace mlk::hip {
+
+enum class StepKind : uint8_t { Elementwise, Softmax, Gemm, RowSum, ScoreSoftmax, Fail };
+
+/// One read or write of a buffer over an R-dim box: element (v0..vR-1),
+/// v_d in [0, extent_d), touches buffer[offset + sum coeff[d] * v_d].
+struct StreamRef {
+    uint32_t buffer{kInvalidId};
+    int64_t offset{0};
+    int64_t coeff[4]{0, 0, 0, 0};
+};
+
+struct Step {
+    StepKind kind{StepKind::Fail};
+    std::string what;                 // class name for reports
+
+    // Elementwise (JIT instance of elementwise_template.hip).
+    int rank{1};
+    int64_t extent[4]{1, 1, 1, 1};
+    bool dynamicExtent{false};        // 1-D loop bound = io.elements
+    int64_t dynBegin{0};              // dynamic form: first index
+    std::vector<StreamRef> inputs;
+    StreamRef out;
+    AccumMode accum{AccumMode::None};
+    std::string chainBody;
+    std::string source;
+    void* fn{nullptr};
+
+    // Softmax / RowSum: rows x cols from buffer x into y.
+    uint32_t x{kInvalidId}, y{kInvalidId};
+    int64_t rows{0}, cols{0};
+
+    // Gemm: C[M,N] (+)= A[M,K] B[K,N] (batched with per-batch strides).
+    uint32_t a{kInvalidId}, b{kInvalidId}, c{kInvalidId};
+    int64_t m{0}, n{0}, k{0};
+    int64_t lda{0}, ldb{0}, ldc{0};
+    bool accumulate{false};
+
+    // ScoreSoftmax: S = softmax(Q K^T / div + bias) per batch.
+    uint32_t q{kInvalidId}, kk{kInvalidId}, bias{kInvalidId}, s{kInvalidId};
+    int64_t batch{0}, seq{0}, dim{0};
+    double div{1.0};
+
+    // Fail: the step reports this ABI code at run time (1 = negative store
+    // address, as the reference walker's InvalidGraph at execution).
+    int failCode{0};
+};
+
+struct Plan {
+    std::string className;            // joined step classes
+    std::string policy;               // tolerance policy id
+    bool multiDim{false};
+    std::vector<Step> steps;
+    std::vector<bool> tempNeeded;     // per buffer id: device scratch needed
+};
+
+/// Recognizes every root of `km` (or every top-level node of a 1-D module)
+/// as a supported class. Refuses honestly (UnsupportedCapability) what no
+/// hand-written kernel covers.
+Result<Plan> planModule(const KernelModule& km);
+
+/// Full hipRTC source of an elementwise step (prelude + template).
+std::string elementwiseSource(const KernelModule& km, const Step& st);
+
+/// Buffer element count as the executors size it (dims product, else
+/// `elements`; dynamic buffers take the run's element count).
+int64_t bufferElements(const KernelBuffer& b, int64_t dynamicElements);
+
+}  // namespace mlk::hip

@@ -1,0 +1,302 @@
+"""Parity of the HIP backend against the CPU oracle, through the C ABI.
+
+Tolerances: poly7 sin chain <= 4 f32 ULP;
+softmax <= 1e-6 relative; f32 GEMM <= 1e-5*sqrt(K) relative; f16 GEMM
+<= 1e-2 relative; score+softmax <= 1e-2 relative; "relative" is
+|got-ref|/max(|ref|,1) (bench/math/math_bench.cpp:172-181). Chains of
+IEEE add/sub/mul/div over f64 buffers are bit-exact.
+"""
+import math
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from mlk2_amd import fixtures as fx
+from mlk2_amd import inputs
+from mlk2_amd.backend import DeviceBuffer, MlkHipError
+from mlk2_amd.kernel_ir import KernelExpr, const, elem_a, elem_b, scalar, temp
+from mlk2_amd.parity import max_rel, ulp_distance_f32
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(f"[gpu] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+# ------------------------------------------------------------------ C1 ----
+@pytest.mark.parametrize("n", [1, 1000, 1 << 20, 1 << 24])
+def test_c1_sin_chain_ulp(hip, n):
+    say(f"c1 sin(x^2+3x) poly7 n={n}")
+    km = fx.config1_module(n=n)
+    x = inputs.config_inputs("c1", {"n": n})["x"]
+    art = hip.build(km)
+    assert art.class_name == "elementwise-1d"
+    got = art.run({0: x})[1].astype(np.float32)
+    ref = oracle.run(km, {0: x}, hw_threads=4)[1]
+    d = ulp_distance_f32(got, ref)
+    say(f"c1 n={n} max_ulp={d.max()} mean_ulp={d.mean():.3f}")
+    assert d.max() <= 4.0
+
+
+def test_c1_quadrant_edges_and_specials(hip):
+    say("c1 quadrant edges / specials")
+    xs = []
+    for q in range(-6, 7):
+        # x with x^2+3x near (2q+1)*pi/4: solve, then take f32 neighbours.
+        t = (2 * q + 1) * math.pi / 4
+        disc = 9 + 4 * t
+        if disc < 0:
+            continue
+        r = (-3 + math.sqrt(disc)) / 2
+        f = np.float32(r)
+        xs += [np.nextafter(f, np.float32(-np.inf)), f, np.nextafter(f, np.float32(np.inf))]
+    xs += [0.0, -0.0, -3.0, 2.0, 4.0, -4.0, np.inf, -np.inf, np.nan]
+    x = np.array(xs, dtype=np.float32)
+    km = fx.config1_module(n=x.size)
+    got = hip.build(km).run({0: x})[1].astype(np.float32)
+    ref = oracle.run(km, {0: x})[1]
+    assert ulp_distance_f32(got, ref).max() <= 4.0
+
+
+def test_c1_f64_buffers_bit_exact(hip):
+    # Every op of the chain (mul, add, the poly7 reduction and polynomial) is
+    # an IEEE f64 operation evaluated in the reference's order.
+    say("c1 f64 bit-exact")
+    n = 100000
+    x = inputs.uniform(inputs.SEEDS["c1_x"], n, -40.0, 40.0, "f64")
+    km = fx.config1_module(n=n, dtype="f64")
+    art = hip.build(km)
+    assert art.policy == "bitexact-rne-gfx950-v1"
+    got = art.run({0: x})[1]
+    ref = oracle.run(km, {0: x})[1]
+    assert np.array_equal(got.view(np.int64), ref.view(np.int64))
+
+
+def test_c1_dynamic_bound_legacy_form(hip):
+    # loop end = kKernelLoopDynamicBound: the extent comes from io.elements
+    # (kernel_buffers.cpp:966-969), through the legacy 1-D ABI.
+    say("c1 dynamic bound, legacy ABI")
+    km = fx.config1_module(n=1)
+    km.nodes[2].end = -1
+    km.buffers[0].elements = -1
+    km.buffers[0].dims = []
+    km.buffers[1].elements = -1
+    km.buffers[1].dims = []
+    n = 3001
+    x = inputs.uniform(5, n, -4.0, 4.0)
+    art = hip.build(km)
+    got = art.run({0: x}, elements=n, legacy=True)[1].astype(np.float32)
+    ref = oracle.run(km, {0: x}, elements=n)[1]
+    assert ulp_distance_f32(got, ref).max() <= 4.0
+
+
+def test_scalar_param_and_two_inputs_1d(hip):
+    # y = (x * s0 - y) / s1 with ScalarParams (lower.to_kernel_ir.cpp:295-307)
+    say("1-D chain with scalar params, f64 bit-exact")
+    n = 5000
+    chain = [KernelExpr("mul", elem_a(), scalar(0)), KernelExpr("sub", temp(0), elem_b()),
+             KernelExpr("div", temp(1), scalar(1))]
+    km = fx.lower_elementwise([("x", [n], "f64"), ("z", [n], "f64")], chain, [n], "f64")
+    a = inputs.uniform(1, n, -3, 3, "f64")
+    b = inputs.uniform(2, n, -3, 3, "f64")
+    art = hip.build(km)
+    for sc in ([1.5, 0.25], [2.0, 0.0], [-1.0]):
+        got = art.run({0: a, 1: b}, scalars=sc)[2]
+        ref = oracle.run(km, {0: a, 1: b}, scalars=sc)[2]
+        assert np.array_equal(got.view(np.int64), ref.view(np.int64)), sc
+
+
+# ------------------------------------------------------------------ C2 ----
+@pytest.mark.parametrize("shape,tier", [((8192, 4096), 1), ((512, 4096), 2), ((33, 100), 1),
+                                        ((7, 9000), 1), ((64, 256), 2)])
+def test_c2_softmax(hip, shape, tier):
+    m, k = shape
+    say(f"c2 softmax {m}x{k} tier{tier}")
+    x = inputs.normal(inputs.SEEDS["c2_x"], m * k, 0.0, 2.0).reshape(m, k)
+    km = fx.config2_module(m, k, tier)
+    art = hip.build(km)
+    got = art.run({0: x})[1]
+    ref = oracle.run(fx.config2_module(m, k, 1), {0: x})[1]
+    e = max_rel(got, ref)
+    say(f"c2 {m}x{k} max_rel={e:.3e}")
+    assert e <= 1e-6
+    rows = got.reshape(m, k).sum(axis=1)
+    assert np.abs(rows - 1.0).max() < 1e-5
+
+
+def test_softmax_adversarial_rows(hip):
+    # unit_poly.cpp:3820-3835: NaN row, +/-0 rows, K=1.
+    say("softmax adversarial rows")
+    M, K = 24, 16
+    x = np.array([((i * 13) % 19) * 0.25 - 2.0 for i in range(M * K)])
+    x[9 * K + 2] = np.nan
+    x[10 * K:11 * K] = [(-0.0 if k % 2 == 0 else 0.0) for k in range(K)]
+    x[11 * K:11 * K + 4] = [-1.0, -0.0, 0.0, -2.0]
+    for tier in (1, 2):
+        km = fx.config2_module(M, K, tier)
+        got = hip.build(km).run({0: x})[1]
+        ref = oracle.run(fx.config2_module(M, K, 1), {0: x})[1]
+        assert np.array_equal(np.isnan(got), np.isnan(ref))
+        assert max_rel(got[~np.isnan(ref)], ref[~np.isnan(ref)]) <= 1e-6
+    km = fx.softmax_call_module(5, 1)
+    got = hip.build(km).run({0: np.array([-3.0, 0.0, 7.5, 1e30, -1e30])})[1]
+    assert np.array_equal(got, np.ones(5))
+
+
+# ------------------------------------------------------------------ C3 ----
+@pytest.mark.parametrize("rows,cols", [(4096, 4096), (37, 100), (3, 5)])
+def test_c3_broadcast_chain(hip, rows, cols):
+    say(f"c3 exp(a*x+b)*x {rows}x{cols}")
+    d = inputs.config_inputs("c3", {"rows": rows, "cols": cols})
+    km = fx.config3_module(rows, cols, tier=2)
+    art = hip.build(km)
+    assert art.class_name == "elementwise-nd"
+    got = art.run({0: d["x"], 1: d["b"]})[2]
+    ref = oracle.run(km, {0: d["x"], 1: d["b"]}, hw_threads=4)[2]
+    e = max_rel(got, ref)
+    u = ulp_distance_f32(got.astype(np.float32), ref)
+    say(f"c3 max_rel={e:.3e} max_ulp={u.max()}")
+    assert e <= 1e-6
+
+
+def test_c3_tier1_form_refused(hip):
+    # The Tier-1 1-D path reads b[i] (kernel_buffers.cpp:110-113): with
+    # b[4096] under a 4096^2 loop that is out of bounds; the backend refuses.
+    km = fx.config3_module(64, 128, tier=1)
+    with pytest.raises(MlkHipError) as ei:
+        hip.build(km)
+    assert ei.value.code == 7
+
+
+def test_c3_scalar_param_a(hip):
+    say("c3 with a as ScalarParam")
+    rows, cols = 64, 256
+    d = inputs.config_inputs("c3", {"rows": rows, "cols": cols})
+    km = fx.config3_module(rows, cols, tier=2, a_operand=scalar(0))
+    art = hip.build(km)
+    for a in (0.5, -1.25):
+        got = art.run({0: d["x"], 1: d["b"]}, scalars=[a])[2]
+        ref = oracle.run(km, {0: d["x"], 1: d["b"]}, scalars=[a])[2]
+        assert max_rel(got, ref) <= 1e-6
+
+
+# ------------------------------------------------------------------ C4 ----
+def _gemm_ref(A, B):
+    m, k = A.shape
+    n = B.shape[1]
+    call = fx.matmul_call_module(m, k, n, "f64", "f64")
+    return oracle.run(call, {0: A, 1: B}, hw_threads=8)[2].reshape(m, n)
+
+
+@pytest.mark.parametrize("m,k,n,tier", [(1024, 1024, 1024, 2), (1024, 1024, 1024, 1),
+                                        (64, 32, 64, 2), (100, 70, 33, 2)])
+def test_c4a_gemm_f32(hip, m, k, n, tier):
+    say(f"c4a gemm f32 {m}x{k}x{n} tier{tier}")
+    d = inputs.config_inputs("c4a", {"m": m, "k": k, "n": n})
+    km = fx.config4_module(m, k, n, "f32", tier)
+    art = hip.build(km)
+    got = art.run({0: d["A"], 1: d["B"]})[2].reshape(m, n)
+    ref = _gemm_ref(d["A"].astype(np.float64), d["B"].astype(np.float64))
+    e = max_rel(got, ref)
+    say(f"c4a max_rel={e:.3e} (tol {1e-5 * math.sqrt(k):.3e})")
+    assert e <= 1e-5 * math.sqrt(k)
+
+
+@pytest.mark.parametrize("m,k,n", [(512, 4096, 512), (256, 64, 256), (300, 50, 70)])
+def test_c4b_gemm_f16(hip, m, k, n):
+    say(f"c4b gemm f16 {m}x{k}x{n}")
+    d = inputs.config_inputs("c4b", {"m": m, "k": k, "n": n})
+    km = fx.config4_module(m, k, n, "f16", 2)
+    art = hip.build(km)
+    got = art.run({0: d["A"], 1: d["B"]})[2].reshape(m, n)
+    ref = _gemm_ref(d["A"].astype(np.float64), d["B"].astype(np.float64))
+    e = max_rel(got, ref)
+    say(f"c4b max_rel={e:.3e}")
+    assert e <= 1e-2
+
+
+def test_c4b_full_size_sampled_rows(hip):
+    # 4096^3 on the device; 32 sampled rows recomputed by the oracle's GEMM.
+    m = k = n = 4096
+    say("c4b gemm f16 4096^3, sampled rows")
+    d = inputs.config_inputs("c4b", {"m": m, "k": k, "n": n})
+    km = fx.config4_module(m, k, n, "f16", 2)
+    art = hip.build(km)
+    bufs = {0: DeviceBuffer.from_array(d["A"], "f16"), 1: DeviceBuffer.from_array(d["B"], "f16"),
+            2: DeviceBuffer(m * n, "f32")}
+    art.run_device(bufs)
+    got = bufs[2].to_numpy().reshape(m, n)
+    rows = np.random.default_rng(4).choice(m, 32, replace=False)
+    ref = _gemm_ref(d["A"][rows].astype(np.float64), d["B"].astype(np.float64))
+    e = max_rel(got[rows], ref)
+    say(f"c4b full max_rel(sampled)={e:.3e}")
+    assert e <= 1e-2
+
+
+def test_matmul_call_accumulates_into_c(hip):
+    # Call(MatMul) adds into C (kernel_buffers.cpp:406-432); the nest form
+    # initializes it (poly.synth.cpp:75-95).
+    say("matmul call accumulates")
+    m, k, n = 256, 64, 256
+    d = inputs.config_inputs("c4a", {"m": m, "k": k, "n": n})
+    c0 = inputs.uniform(9, m * n, -1, 1)
+    call = fx.config4_module(m, k, n, "f32", 1)
+    got = hip.build(call).run({0: d["A"], 1: d["B"], 2: c0})[2]
+    ref = oracle.run(call, {0: d["A"], 1: d["B"]}, init={2: c0})[2]
+    assert max_rel(got, ref) <= 1e-5 * math.sqrt(k)
+
+
+# ------------------------------------------------------------------ C5 ----
+@pytest.mark.parametrize("b,s,dm", [(2, 128, 128), (1, 24, 8)])
+def test_c5_score_softmax(hip, b, s, dm):
+    say(f"c5 score softmax b={b} s={s} d={dm}")
+    d = inputs.config_inputs("c5", {"batch": b, "seq": s, "dim": dm})
+    km = fx.score_softmax_module(b, s, dm)
+    art = hip.build(km)
+    assert art.class_name == "score-softmax"
+    got = art.run({0: d["Q"], 1: d["K"], 2: d["bias"]})[3]
+    ref = oracle.run(km, {0: d["Q"], 1: d["K"], 2: d["bias"]}, hw_threads=8)[3]
+    e = max_rel(got, ref)
+    say(f"c5 max_rel={e:.3e}")
+    assert e <= 1e-2
+
+
+# ------------------------------------------------------------- entries ----
+def test_device_entry_matches_host_entry(hip):
+    say("device entry vs host entry")
+    n = 1 << 18
+    x = inputs.config_inputs("c1", {"n": n})["x"]
+    km = fx.config1_module(n=n)
+    art = hip.build(km)
+    host = art.run({0: x})[1].astype(np.float32)
+    bufs = {0: DeviceBuffer.from_array(x, "f32"), 1: DeviceBuffer(n, "f32")}
+    art.run_device(bufs)
+    dev = bufs[1].to_numpy()
+    assert np.array_equal(host.view(np.int32), dev.view(np.int32))
+
+
+def test_bad_binding_rejected(hip):
+    km = fx.config1_module(n=1024)
+    art = hip.build(km)
+    bufs = {0: DeviceBuffer(100, "f32"), 1: DeviceBuffer(1024, "f32")}
+    with pytest.raises(MlkHipError) as ei:
+        art.run_device(bufs)
+    assert ei.value.code == 6
+    bufs = {0: DeviceBuffer(1024, "f16"), 1: DeviceBuffer(1024, "f32")}
+    with pytest.raises(MlkHipError) as ei:
+        art.run_device(bufs)
+    assert ei.value.code == 6
+
+
+def test_reducesum_call_and_nest(hip):
+    say("reducesum")
+    M, K = 300, 1000
+    x = inputs.normal(3, M * K)
+    for km in (fx.reducesum_call_module(M, K), fx.synth_reducesum(fx.reducesum_call_module(M, K))):
+        got = hip.build(km).run({0: x})[1]
+        ref = oracle.run(fx.reducesum_call_module(M, K), {0: x})[1]
+        assert max_rel(got, ref) <= 1e-6
