@@ -53,7 +53,16 @@ def bench_config(be, name: str, steps: int, warmup: int) -> dict:
     from mlk2_amd import inputs
     from mlk2_amd.backend import DeviceBuffer
 
-    if name == "c1":
+    if name == "copy":
+        # Calibration for the PMC counters: y = x + 0 over 2^26 f32 (a plain
+        # streaming copy through the elementwise template, 512 MiB moved).
+        from mlk2_amd.kernel_ir import KernelExpr, const, elem_a
+        n = 1 << 26
+        km = fx.lower_elementwise([("x", [n], "f32")], [KernelExpr("add", elem_a(), const(0.0))], [n])
+        bufs = {0: DeviceBuffer.from_array(np.zeros(n, np.float32), "f32"), 1: DeviceBuffer(n, "f32")}
+        work, unit, peak, bound = 8 * n, "GB/s", PEAK_HBM_GBS, "hbm"
+        wl = "copy y = x + 0, f32, 2^26"
+    elif name == "c1":
         n = 1 << 24
         km = fx.config1_module(n=n)
         d = inputs.config_inputs("c1")
@@ -184,7 +193,8 @@ def main() -> int:
     achieved = bytes_alg / (kernel_ms * 1e-3) / 1e9
 
     configs = {}
-    names = [n for n in ("c1", "c3", "c4a", "c4b", "c5") if not args.only or n in args.only.split(",")]
+    names = [n for n in ("copy", "c1", "c3", "c4a", "c4b", "c5")
+             if (not args.only and n != "copy") or n in args.only.split(",")]
     for name in names:
         try:
             configs[name] = bench_config(be, name, max(10, args.steps // 2), 5)
