@@ -11,11 +11,14 @@
 // Without a prelude the file compiles standalone with a sample instance (the
 // C1 chain), which is how the build checks it.
 //
-// Mapping: lane c owns kPer consecutive elements of one innermost row of the
-// box (row = c / chunksPerRow). A stream with innermost coefficient 1 is read
-// with 16-byte loads when the lane's run is 16-byte aligned, coefficient 0 is
-// one broadcast load per lane, any other coefficient is a gather. The output
-// is written the same way. Index arithmetic divides by compile-time extents.
+// Mapping: a wave owns a segment of 64*kPer consecutive elements of one
+// innermost row of the box; lane l holds the 4-element groups at columns
+// seg*64*kPer + g*256 + 4*l (g < kPer/4), so each vector load or store of the
+// wave covers one contiguous 256-element span (1 KiB of f32). A stream with
+// innermost coefficient 1 is read with one vector access per group when
+// aligned (16 B for f32/f64 pairs, 8 B for f16), coefficient 0 is one
+// broadcast load per lane, any other coefficient is a gather. The output is
+// written the same way. Index arithmetic divides by compile-time extents.
 // Compiled with -ffp-contract=off: f64 mul/add round separately, as on the
 // reference's x86-64 build; the only fused multiply-adds are the explicit
 // ones of the f32 residual polynomial in mlk_p7_sin_f32out.
@@ -45,7 +48,7 @@ constexpr int kAccum = 0;
 
 typedef float mlk_f32x4 __attribute__((ext_vector_type(4)));
 typedef double mlk_f64x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 mlk_f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 mlk_f16x4 __attribute__((ext_vector_type(4)));
 
 namespace mlk {
 
@@ -161,69 +164,58 @@ __device__ __forceinline__ void storeOne(void* p, long long i, double v) {
 template <int DT>
 constexpr int kBytes = DT == 0 ? 4 : (DT == 1 ? 2 : 8);
 
-/// kPer consecutive elements from a 16-byte aligned run.
+/// Alignment (bytes) a 4-element group needs for its vector access.
 template <int DT>
-__device__ __forceinline__ void loadRunVec(const void* p, long long i, double (&v)[kPer]) {
+constexpr unsigned long long kGroupAlign = DT == 1 ? 8ull : 16ull;
+
+constexpr int kGroups = kPer / 4;  // 4-element groups per lane
+constexpr int kSeg = 64 * kPer;    // elements per wave segment of a row
+
+/// Four consecutive elements at flat index i (group-aligned).
+template <int DT>
+__device__ __forceinline__ void loadGroup(const void* p, long long i, double* v) {
     if constexpr (DT == 0) {
-        const mlk_f32x4* q = reinterpret_cast<const mlk_f32x4*>(static_cast<const float*>(p) + i);
-        mlk_f32x4 f[kPer / 4];
+        const mlk_f32x4 f =
+            __builtin_nontemporal_load(reinterpret_cast<const mlk_f32x4*>(static_cast<const float*>(p) + i));
 #pragma unroll
-        for (int c = 0; c < kPer / 4; ++c) f[c] = __builtin_nontemporal_load(q + c);
-#pragma unroll
-        for (int c = 0; c < kPer / 4; ++c) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[4 * c + e] = static_cast<double>(f[c][e]);
-        }
+        for (int e = 0; e < 4; ++e) v[e] = static_cast<double>(f[e]);
     } else if constexpr (DT == 1) {
-        const mlk_f16x8* q = reinterpret_cast<const mlk_f16x8*>(static_cast<const _Float16*>(p) + i);
-        mlk_f16x8 h[kPer / 8];
+        const mlk_f16x4 h = __builtin_nontemporal_load(
+            reinterpret_cast<const mlk_f16x4*>(static_cast<const _Float16*>(p) + i));
 #pragma unroll
-        for (int c = 0; c < kPer / 8; ++c) h[c] = __builtin_nontemporal_load(q + c);
-#pragma unroll
-        for (int c = 0; c < kPer / 8; ++c) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) v[8 * c + e] = static_cast<double>(static_cast<float>(h[c][e]));
-        }
+        for (int e = 0; e < 4; ++e) v[e] = static_cast<double>(static_cast<float>(h[e]));
     } else {
         const mlk_f64x2* q = reinterpret_cast<const mlk_f64x2*>(static_cast<const double*>(p) + i);
-#pragma unroll
-        for (int c = 0; c < kPer / 2; ++c) {
-            const mlk_f64x2 d = __builtin_nontemporal_load(q + c);
-            v[2 * c] = d[0];
-            v[2 * c + 1] = d[1];
-        }
+        const mlk_f64x2 a = __builtin_nontemporal_load(q);
+        const mlk_f64x2 b = __builtin_nontemporal_load(q + 1);
+        v[0] = a[0];
+        v[1] = a[1];
+        v[2] = b[0];
+        v[3] = b[1];
     }
 }
 
 template <int DT>
-__device__ __forceinline__ void storeRunVec(void* p, long long i, const double (&v)[kPer]) {
+__device__ __forceinline__ void storeGroup(void* p, long long i, const double* v) {
     if constexpr (DT == 0) {
-        mlk_f32x4* q = reinterpret_cast<mlk_f32x4*>(static_cast<float*>(p) + i);
+        mlk_f32x4 f;
 #pragma unroll
-        for (int c = 0; c < kPer / 4; ++c) {
-            mlk_f32x4 f;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) f[e] = static_cast<float>(v[4 * c + e]);
-            __builtin_nontemporal_store(f, q + c);
-        }
+        for (int e = 0; e < 4; ++e) f[e] = static_cast<float>(v[e]);
+        __builtin_nontemporal_store(f, reinterpret_cast<mlk_f32x4*>(static_cast<float*>(p) + i));
     } else if constexpr (DT == 1) {
-        mlk_f16x8* q = reinterpret_cast<mlk_f16x8*>(static_cast<_Float16*>(p) + i);
+        mlk_f16x4 h;
 #pragma unroll
-        for (int c = 0; c < kPer / 8; ++c) {
-            mlk_f16x8 h;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) h[e] = toHalf(v[8 * c + e]);
-            __builtin_nontemporal_store(h, q + c);
-        }
+        for (int e = 0; e < 4; ++e) h[e] = toHalf(v[e]);
+        __builtin_nontemporal_store(h, reinterpret_cast<mlk_f16x4*>(static_cast<_Float16*>(p) + i));
     } else {
         mlk_f64x2* q = reinterpret_cast<mlk_f64x2*>(static_cast<double*>(p) + i);
-#pragma unroll
-        for (int c = 0; c < kPer / 2; ++c) {
-            mlk_f64x2 d;
-            d[0] = v[2 * c];
-            d[1] = v[2 * c + 1];
-            __builtin_nontemporal_store(d, q + c);
-        }
+        mlk_f64x2 a, b;
+        a[0] = v[0];
+        a[1] = v[1];
+        b[0] = v[2];
+        b[1] = v[3];
+        __builtin_nontemporal_store(a, q);
+        __builtin_nontemporal_store(b, q + 1);
     }
 }
 
@@ -233,8 +225,11 @@ constexpr long long outerRows() {
     return r;
 }
 
+/// Element g*4+e of a lane sits at column lane0 + g*256 + e, lane0 =
+/// seg*kSeg + 4*lane: each vector instruction of a wave covers one
+/// contiguous 64x4-element span.
 template <int K>
-__device__ __forceinline__ void loadStream(const void* p, const long long (&var)[4], long long col0,
+__device__ __forceinline__ void loadStream(const void* p, const long long (&var)[4], long long lane0,
                                            bool full, long long W, double (&v)[kPer]) {
     constexpr int DT = kInDt[K];
     long long base = kInOff[K];
@@ -246,15 +241,20 @@ __device__ __forceinline__ void loadStream(const void* p, const long long (&var)
 #pragma unroll
         for (int e = 0; e < kPer; ++e) v[e] = x;
     } else {
-        const long long first = base + ci * col0;
         const bool vec = ci == 1 && full &&
-                         ((reinterpret_cast<unsigned long long>(p) + first * kBytes<DT>) & 15ull) == 0;
+                         ((reinterpret_cast<unsigned long long>(p) + (base + lane0) * kBytes<DT>) &
+                          (kGroupAlign<DT> - 1)) == 0;
         if (vec) {
-            loadRunVec<DT>(p, first, v);
+#pragma unroll
+            for (int g = 0; g < kGroups; ++g) loadGroup<DT>(p, base + lane0 + g * 256, &v[4 * g]);
         } else {
 #pragma unroll
-            for (int e = 0; e < kPer; ++e) {
-                v[e] = (col0 + e < W) ? loadOne<DT>(p, first + ci * e) : 0.0;
+            for (int g = 0; g < kGroups; ++g) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const long long col = lane0 + g * 256 + e;
+                    v[4 * g + e] = col < W ? loadOne<DT>(p, base + ci * col) : 0.0;
+                }
             }
         }
     }
@@ -262,11 +262,11 @@ __device__ __forceinline__ void loadStream(const void* p, const long long (&var)
 
 template <int K>
 __device__ __forceinline__ void loadAll(const void* const (&ptr)[4], const long long (&var)[4],
-                                        long long col0, bool full, long long W,
+                                        long long lane0, bool full, long long W,
                                         double (&in)[MLK_NIN][kPer]) {
     if constexpr (K < MLK_NIN) {
-        loadStream<K>(ptr[K], var, col0, full, W, in[K]);
-        loadAll<K + 1>(ptr, var, col0, full, W, in);
+        loadStream<K>(ptr[K], var, lane0, full, W, in[K]);
+        loadAll<K + 1>(ptr, var, lane0, full, W, in);
     }
 }
 
@@ -280,16 +280,18 @@ extern "C" __global__ __launch_bounds__(256) void mlk_elementwise(const void* p0
     // The 1-D dynamic form (loop end = the run's element count) takes its
     // extent at launch; every other extent is a compile-time constant.
     const long long W = kDynamicExtent ? dynExtent : kExt[kRank - 1];
-    const long long chunksPerRow = (W + kPer - 1) / kPer;
+    const long long segsPerRow = (W + kSeg - 1) / kSeg;
     constexpr long long rows = outerRows();
-    const long long total = rows * chunksPerRow;
+    const long long total = rows * segsPerRow;
     const void* const ptr[4] = {p0, p1, p2, p3};
-    const long long stride = static_cast<long long>(gridDim.x) * kThreads;
-    for (long long c = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x; c < total;
-         c += stride) {
-        const long long row = c / chunksPerRow;
-        const long long col0 = (c - row * chunksPerRow) * kPer;
-        const bool full = col0 + kPer <= W;
+    const int lane = threadIdx.x & 63;
+    const long long waves = static_cast<long long>(gridDim.x) * (kThreads / 64);
+    for (long long w = static_cast<long long>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
+         w < total; w += waves) {
+        const long long row = w / segsPerRow;
+        const long long seg = w - row * segsPerRow;
+        const long long lane0 = seg * kSeg + 4 * lane;
+        const bool full = (seg + 1) * kSeg <= W;
         long long var[4] = {0, 0, 0, 0};
         {
             long long rem = row;
@@ -300,7 +302,7 @@ extern "C" __global__ __launch_bounds__(256) void mlk_elementwise(const void* p0
             }
         }
         double in[MLK_NIN][kPer];
-        loadAll<0>(ptr, var, col0, full, W, in);
+        loadAll<0>(ptr, var, lane0, full, W, in);
         double res[kPer];
 #pragma unroll
         for (int e = 0; e < kPer; ++e) {
@@ -313,26 +315,35 @@ extern "C" __global__ __launch_bounds__(256) void mlk_elementwise(const void* p0
 #pragma unroll
         for (int d = 0; d < kRank - 1; ++d) obase += kOutC[d] * var[d];
         constexpr long long oc = kOutC[kRank - 1];
-        const long long ofirst = obase + oc * col0;
         if constexpr (kAccum != 0) {
 #pragma unroll
-            for (int e = 0; e < kPer; ++e) {
-                if (col0 + e < W) {
-                    const long long at = ofirst + oc * e;
-                    const double old = loadOne<kOutDt>(out, at);
-                    const double v = kAccum == 1 ? old + res[e] : ((res[e] > old) ? res[e] : old);
-                    storeOne<kOutDt>(out, at, v);
+            for (int g = 0; g < kGroups; ++g) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const long long col = lane0 + g * 256 + e;
+                    if (col < W) {
+                        const long long at = obase + oc * col;
+                        const double old = loadOne<kOutDt>(out, at);
+                        const double r = res[4 * g + e];
+                        storeOne<kOutDt>(out, at, kAccum == 1 ? old + r : ((r > old) ? r : old));
+                    }
                 }
             }
         } else {
             const bool vec = oc == 1 && full &&
-                             ((reinterpret_cast<unsigned long long>(out) + ofirst * kBytes<kOutDt>) & 15ull) == 0;
+                             ((reinterpret_cast<unsigned long long>(out) + (obase + lane0) * kBytes<kOutDt>) &
+                              (kGroupAlign<kOutDt> - 1)) == 0;
             if (vec) {
-                storeRunVec<kOutDt>(out, ofirst, res);
+#pragma unroll
+                for (int g = 0; g < kGroups; ++g) storeGroup<kOutDt>(out, obase + lane0 + g * 256, &res[4 * g]);
             } else {
 #pragma unroll
-                for (int e = 0; e < kPer; ++e) {
-                    if (col0 + e < W) storeOne<kOutDt>(out, ofirst + oc * e, res[e]);
+                for (int g = 0; g < kGroups; ++g) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const long long col = lane0 + g * 256 + e;
+                        if (col < W) storeOne<kOutDt>(out, obase + oc * col, res[4 * g + e]);
+                    }
                 }
             }
         }

@@ -90,6 +90,65 @@ __global__ __launch_bounds__(256) void softmaxWaveRow(const float* x,
     }
 }
 
+/// Same arithmetic as softmaxWaveRow, with each wave walking several rows and
+/// the next row's loads issued before the current row's reductions, so HBM
+/// reads of row r+1 overlap the exp/sum/stores of row r.
+template <int CH>
+__global__ __launch_bounds__(256) void softmaxWaveRowPipelined(const float* x, float* y, int64_t rows,
+                                                               int64_t cols, int64_t xs, int64_t ys) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int64_t waves = static_cast<int64_t>(gridDim.x) * 4;
+    f32x4 cur[CH], nxt[CH];
+    auto load = [&](int64_t row, f32x4 (&v)[CH]) {
+        const float* xr = x + row * xs;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int64_t col = (static_cast<int64_t>(c) * 64 + lane) * 4;
+            v[c] = col < cols ? __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(xr + col))
+                              : f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        }
+    };
+    if (wave < rows) load(wave, cur);
+    for (int64_t row = wave; row < rows; row += waves) {
+        const int64_t nrow = row + waves;
+        if (nrow < rows) load(nrow, nxt);
+        float m = -INFINITY;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) m = fmaxf(m, cur[c][e]);
+        }
+        m = waveMax(m);
+        double s = 0.0;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int64_t col = (static_cast<int64_t>(c) * 64 + lane) * 4;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float ex = expf(cur[c][e] - m);
+                cur[c][e] = ex;
+                if (col < cols) s += static_cast<double>(ex);
+            }
+        }
+        s = waveSum(s);
+        const float inv = s != 0.0 ? static_cast<float>(1.0 / s) : 0.0f;
+        float* yr = y + row * ys;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int64_t col = (static_cast<int64_t>(c) * 64 + lane) * 4;
+            if (col < cols) {
+                f32x4 o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[e] = s != 0.0 ? cur[c][e] * inv : 0.0f;
+                __builtin_nontemporal_store(o, reinterpret_cast<f32x4*>(yr + col));
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < CH; ++c) cur[c] = nxt[c];
+    }
+}
+
 template <typename T>
 __device__ __forceinline__ double ld(const void* p, int64_t i) {
     return static_cast<double>(static_cast<const T*>(p)[i]);
@@ -153,9 +212,25 @@ __global__ __launch_bounds__(256) void softmaxBlockRow(mlkd_softmax p) {
     }
 }
 
+// Launch variant of the wave-per-row path (0: one row per wave; 1: rows
+// pipelined over a grid of `gSoftmaxWaves` waves). Set by the variant search
+// (mlkd_softmax_set_variant); the defaults are the measured best on gfx950.
+int gSoftmaxVariant = 0;
+int64_t gSoftmaxWaves = 0;
+
 template <int CH>
 int launchWave(const mlkd_softmax& p, hipStream_t st) {
+    if (gSoftmaxVariant == 1) {
+        int64_t waves = gSoftmaxWaves > 0 ? gSoftmaxWaves : 2048;
+        if (waves > p.rows) waves = p.rows;
+        const int64_t blocks = (waves + 3) / 4;
+        hipLaunchKernelGGL(softmaxWaveRowPipelined<CH>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st,
+                           static_cast<const float*>(p.x), static_cast<float*>(p.y), p.rows, p.cols,
+                           p.x_row_stride, p.y_row_stride);
+        return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
+    }
     int64_t blocks = (p.rows + 3) / 4;
+    if (gSoftmaxWaves > 0 && blocks > (gSoftmaxWaves + 3) / 4) blocks = (gSoftmaxWaves + 3) / 4;
     if (blocks > 8192) blocks = 8192;
     hipLaunchKernelGGL(softmaxWaveRow<CH>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st,
                        static_cast<const float*>(p.x), static_cast<float*>(p.y), p.rows, p.cols,
@@ -164,6 +239,11 @@ int launchWave(const mlkd_softmax& p, hipStream_t st) {
 }
 
 }  // namespace
+
+extern "C" void mlkd_softmax_set_variant(int variant, int64_t waves) {
+    gSoftmaxVariant = variant;
+    gSoftmaxWaves = waves;
+}
 
 extern "C" int mlkd_launch_softmax(const mlkd_softmax* p, void* stream) {
     if (p == nullptr || p->rows < 0 || p->cols < 0) return MLKD_RT_LAUNCH;

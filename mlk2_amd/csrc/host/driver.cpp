@@ -14,8 +14,8 @@ namespace {
 
 int dtypeCode(Dtype d) { return d == Dtype::F32 ? MLKD_F32 : (d == Dtype::F16 ? MLKD_F16 : MLKD_F64); }
 
-unsigned gridFor(int64_t chunks) {
-    int64_t blocks = (chunks + 255) / 256;
+unsigned gridFor(int64_t threads) {
+    int64_t blocks = (threads + 255) / 256;
     // Grid-stride beyond 64 workgroups of 4 waves per CU on 256 CUs.
     if (blocks > 16384) blocks = 16384;
     if (blocks < 1) blocks = 1;
@@ -196,8 +196,9 @@ int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* 
                 int64_t rows = 1;
                 for (int d = 0; d < st.rank - 1; ++d) rows *= st.extent[d];
                 const int64_t w = st.rank == 1 ? ext0 : st.extent[st.rank - 1];
-                const int64_t chunks = rows * ((w + 15) / 16);
-                rc = mlkd_jit_launch_elementwise(st.fn, gridFor(chunks), in, out, &sc, ext0, stream);
+                // One wave per 1024-element row segment (the template's kSeg).
+                const int64_t threads = rows * ((w + 1023) / 1024) * 64;
+                rc = mlkd_jit_launch_elementwise(st.fn, gridFor(threads), in, out, &sc, ext0, stream);
                 break;
             }
             case StepKind::Softmax:
