@@ -61,11 +61,12 @@ __device__ __forceinline__ void xcdTile(int tilesM, int tilesN, int& tm, int& tn
     tn = id % tilesN;
 }
 
+template <bool ACC>
 __global__ __launch_bounds__(512) void gemmF16Mfma(const _Float16* __restrict__ A,
                                                    const _Float16* __restrict__ B,
                                                    float* __restrict__ C, int M, int N, int K,
                                                    int64_t lda, int64_t ldb, int64_t ldc,
-                                                   int accumulate) {
+                                                   int /*accumulate: template ACC*/) {
     extern __shared__ __align__(16) _Float16 lds[];
     _Float16* As = lds;                      // [2][256][kPadK]
     _Float16* Bs = lds + 2 * kTileHalves;    // [2][256][kPadK]
@@ -84,8 +85,10 @@ __global__ __launch_bounds__(512) void gemmF16Mfma(const _Float16* __restrict__ 
     // 8 (k) x 8 (n) block of B each.
     const bool loadsA = tid < 256;
     const int t = tid & 255;
-    const int bk = t >> 5;     // B block: k rows bk*8 .. +7
-    const int bn = t & 31;     // B block: n cols bn*8 .. +7
+    // k-block fastest across lanes: the 8 lanes that share an n-block
+    // write one LDS row's 8 chunks, so transposed writes are conflict-free.
+    const int bk = t & 7;      // B block: k rows bk*8 .. +7
+    const int bn = t >> 3;     // B block: n cols bn*8 .. +7
     u32x4 reg[8];
 
     auto globalLoad = [&](int k0) {
@@ -187,7 +190,400 @@ __global__ __launch_bounds__(512) void gemmF16Mfma(const _Float16* __restrict__ 
                 const int64_t row = row0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                 float* dst = C + row * ldc + cBase;
                 const float v = acc[i][j][r];
-                *dst = accumulate ? *dst + v : v;
+                *dst = ACC ? *dst + v : v;
+            }
+        }
+    }
+}
+
+/// 4-wave variant: the same 256x256x64 workgroup tile with each wave owning a
+/// 128x128 quadrant (4x4 MFMA tiles, 256 accumulators in AGPRs), so every
+/// kk step issues 8 LDS operand reads for 16 MFMAs. Thread t loads 8 A chunks
+/// and one 8x8 B block per K step.
+template <bool ACC>
+__global__ __launch_bounds__(256) void gemmF16Mfma4w(const _Float16* __restrict__ A,
+                                                     const _Float16* __restrict__ B,
+                                                     float* __restrict__ C, int M, int N, int K,
+                                                     int64_t lda, int64_t ldb, int64_t ldc,
+                                                     int /*accumulate: template ACC*/) {
+    extern __shared__ __align__(16) _Float16 lds[];
+    _Float16* As = lds;
+    _Float16* Bs = lds + 2 * kTileHalves;
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int wm = wave >> 1;   // 0..1
+    const int wn = wave & 1;    // 0..1
+    int tm, tn;
+    xcdTile(M / kBM, N / kBN, tm, tn);
+    const int64_t row0 = static_cast<int64_t>(tm) * kBM;
+    const int64_t col0 = static_cast<int64_t>(tn) * kBN;
+    const int bk = t & 7;
+    const int bn = t >> 3;
+    u32x4 ra[8], rb[8];
+    auto globalLoad = [&](int k0) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int c = j * 256 + t;
+            ra[j] = *reinterpret_cast<const u32x4*>(A + (row0 + (c >> 3)) * lda + k0 + (c & 7) * 8);
+        }
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            rb[r] = *reinterpret_cast<const u32x4*>(B + static_cast<int64_t>(k0 + bk * 8 + r) * ldb + col0 + bn * 8);
+        }
+    };
+    auto ldsStore = [&](int buf) {
+        _Float16* da = As + buf * kTileHalves;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int c = j * 256 + t;
+            *reinterpret_cast<u32x4*>(da + (c >> 3) * kPadK + (c & 7) * 8) = ra[j];
+        }
+        _Float16* db = Bs + buf * kTileHalves;
+#pragma unroll
+        for (int n = 0; n < 8; ++n) {
+            const int p = n >> 1;
+            const uint32_t sel = (n & 1) ? 0x07060302u : 0x05040100u;
+            u32x4 o;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) o[j] = __builtin_amdgcn_perm(rb[2 * j + 1][p], rb[2 * j][p], sel);
+            *reinterpret_cast<u32x4*>(db + (bn * 8 + n) * kPadK + bk * 8) = o;
+        }
+    };
+    f32x16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+        }
+    }
+    const int steps = K / kBK;
+    globalLoad(0);
+    ldsStore(0);
+    __syncthreads();
+    const int lrow = lane & 31;
+    const int lk = (lane >> 5) * 8;
+    for (int s = 0; s < steps; ++s) {
+        const int buf = s & 1;
+        if (s + 1 < steps) globalLoad((s + 1) * kBK);
+        const _Float16* as = As + buf * kTileHalves + (wm * 128 + lrow) * kPadK + lk;
+        const _Float16* bs = Bs + buf * kTileHalves + (wn * 128 + lrow) * kPadK + lk;
+#pragma unroll
+        for (int kk = 0; kk < kBK; kk += 16) {
+            f16x8 a[4], b[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const f16x8*>(as + i * 32 * kPadK + kk);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const f16x8*>(bs + j * 32 * kPadK + kk);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+                }
+            }
+        }
+        if (s + 1 < steps) ldsStore(buf ^ 1);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t cBase = col0 + wn * 128 + j * 32 + (lane & 31);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int64_t row = row0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                float* dst = C + row * ldc + cBase;
+                const float v = acc[i][j][r];
+                *dst = ACC ? *dst + v : v;
+            }
+        }
+    }
+}
+
+/// 4-wave variant with A moved by the gfx950 direct global->LDS path
+/// (global_load_lds_dwordx4): A never occupies VGPRs, which leaves room for
+/// the 256 accumulators plus B's register staging without spills. A's LDS
+/// tile is unpadded [256][64] with 16-byte chunks XOR-swizzled by
+/// (row >> 1) & 7, so the 16 rows one quarter-wave reads hit 16 distinct
+/// chunk slots. Each direct-load instruction writes 64 consecutive 16-byte
+/// slots (lane i -> slot i); the lane chooses the global chunk that belongs
+/// in that slot.
+constexpr int kTileA = 256 * kBK;  // halves, unpadded
+
+__device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
+
+template <bool ACC>
+__global__ __launch_bounds__(256) void gemmF16Mfma4wDirect(const _Float16* __restrict__ A,
+                                                           const _Float16* __restrict__ B,
+                                                           float* __restrict__ C, int M, int N, int K,
+                                                           int64_t lda, int64_t ldb, int64_t ldc,
+                                                           int /*accumulate: template ACC*/) {
+    extern __shared__ __align__(16) _Float16 lds[];
+    _Float16* As = lds;                    // [2][256][64] swizzled
+    _Float16* Bs = lds + 2 * kTileA;       // [2][256][kPadK]
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int wm = wave >> 1;
+    const int wn = wave & 1;
+    int tm, tn;
+    xcdTile(M / kBM, N / kBN, tm, tn);
+    const int64_t row0 = static_cast<int64_t>(tm) * kBM;
+    const int64_t col0 = static_cast<int64_t>(tn) * kBN;
+    const int bk = t & 7;
+    const int bn = t >> 3;
+    u32x4 rb[8];
+    auto directA = [&](int k0, int buf) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int slot0 = (wave * 8 + j) * 64;          // first slot of this instruction
+            const int q = slot0 + lane;
+            const int row = q >> 3;
+            const int c = (q & 7) ^ swz(row);               // logical chunk stored in slot q
+            const _Float16* src = A + (row0 + row) * lda + k0 + c * 8;
+            _Float16* dst = As + buf * kTileA + slot0 * 8;  // wave-uniform
+            __builtin_amdgcn_global_load_lds(src, reinterpret_cast<__attribute__((address_space(3))) void*>(
+                                                       reinterpret_cast<uintptr_t>(dst)),
+                                             16, 0, 0);
+        }
+    };
+    auto loadB = [&](int k0) {
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            rb[r] = *reinterpret_cast<const u32x4*>(B + static_cast<int64_t>(k0 + bk * 8 + r) * ldb + col0 + bn * 8);
+        }
+    };
+    auto storeB = [&](int buf) {
+        _Float16* db = Bs + buf * kTileHalves;
+#pragma unroll
+        for (int n = 0; n < 8; ++n) {
+            const int p = n >> 1;
+            const uint32_t sel = (n & 1) ? 0x07060302u : 0x05040100u;
+            u32x4 o;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) o[j] = __builtin_amdgcn_perm(rb[2 * j + 1][p], rb[2 * j][p], sel);
+            *reinterpret_cast<u32x4*>(db + (bn * 8 + n) * kPadK + bk * 8) = o;
+        }
+    };
+    f32x16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+        }
+    }
+    const int steps = K / kBK;
+    directA(0, 0);
+    loadB(0);
+    storeB(0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    const int lrow = lane & 31;
+    const int lhalf = lane >> 5;
+    for (int s = 0; s < steps; ++s) {
+        const int buf = s & 1;
+        if (s + 1 < steps) {
+            directA((s + 1) * kBK, buf ^ 1);
+            loadB((s + 1) * kBK);
+        }
+        const _Float16* as = As + buf * kTileA;
+        const _Float16* bs = Bs + buf * kTileHalves + (wn * 128 + lrow) * kPadK + lhalf * 8;
+#pragma unroll
+        for (int kk = 0; kk < kBK; kk += 16) {
+            f16x8 a[4], b[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = wm * 128 + i * 32 + lrow;
+                const int c = (kk >> 3) + lhalf;
+                a[i] = *reinterpret_cast<const f16x8*>(as + row * kBK + ((c ^ swz(row)) * 8));
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const f16x8*>(bs + j * 32 * kPadK + kk);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+                }
+            }
+        }
+        if (s + 1 < steps) storeB(buf ^ 1);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t cBase = col0 + wn * 128 + j * 32 + (lane & 31);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int64_t row = row0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                float* dst = C + row * ldc + cBase;
+                const float v = acc[i][j][r];
+                *dst = ACC ? *dst + v : v;
+            }
+        }
+    }
+}
+
+/// Variant 3: variant 2's data movement with an explicit software pipeline
+/// inside the K step. Operand fragments are double buffered in registers:
+/// the 8 LDS reads for kk+1 are issued while the 16 MFMAs of kk run, and
+/// sched_group_barrier pins the interleave (1 DS read per 2 MFMAs; the next
+/// step's global loads spread over the first kk; the B transpose and its LDS
+/// writes over the last kk), so the MFMA pipe never waits on LDS latency
+/// except once after each barrier.
+template <bool ACC>
+__global__ __launch_bounds__(256) void gemmF16Mfma4wPipe(const _Float16* __restrict__ A,
+                                                         const _Float16* __restrict__ B,
+                                                         float* __restrict__ C, int M, int N, int K,
+                                                         int64_t lda, int64_t ldb, int64_t ldc) {
+    extern __shared__ __align__(16) _Float16 lds[];
+    _Float16* As = lds;
+    _Float16* Bs = lds + 2 * kTileA;
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int wm = wave >> 1;
+    const int wn = wave & 1;
+    int tm, tn;
+    xcdTile(M / kBM, N / kBN, tm, tn);
+    const int64_t row0 = static_cast<int64_t>(tm) * kBM;
+    const int64_t col0 = static_cast<int64_t>(tn) * kBN;
+    const int bk = t & 7;
+    const int bn = t >> 3;
+    const int lrow = lane & 31;
+    const int lhalf = lane >> 5;
+    u32x4 rb[8];
+    auto directA = [&](int k0, int buf) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int slot0 = (wave * 8 + j) * 64;
+            const int q = slot0 + lane;
+            const int row = q >> 3;
+            const int c = (q & 7) ^ swz(row);
+            const _Float16* src = A + (row0 + row) * lda + k0 + c * 8;
+            _Float16* dst = As + buf * kTileA + slot0 * 8;
+            __builtin_amdgcn_global_load_lds(src, reinterpret_cast<__attribute__((address_space(3))) void*>(
+                                                       reinterpret_cast<uintptr_t>(dst)),
+                                             16, 0, 0);
+        }
+    };
+    auto loadB = [&](int k0) {
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            rb[r] = *reinterpret_cast<const u32x4*>(B + static_cast<int64_t>(k0 + bk * 8 + r) * ldb + col0 + bn * 8);
+        }
+    };
+    auto storeB = [&](int buf) {
+        _Float16* db = Bs + buf * kTileHalves;
+#pragma unroll
+        for (int n = 0; n < 8; ++n) {
+            const int p = n >> 1;
+            const uint32_t sel = (n & 1) ? 0x07060302u : 0x05040100u;
+            u32x4 o;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) o[j] = __builtin_amdgcn_perm(rb[2 * j + 1][p], rb[2 * j][p], sel);
+            *reinterpret_cast<u32x4*>(db + (bn * 8 + n) * kPadK + bk * 8) = o;
+        }
+    };
+    f16x8 fa[2][4], fb[2][4];
+    auto readFrags = [&](int buf, int kk, int slot) {
+        const _Float16* as = As + buf * kTileA;
+        const _Float16* bs = Bs + buf * kTileHalves + (wn * 128 + lrow) * kPadK + lhalf * 8 + kk;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = wm * 128 + i * 32 + lrow;
+            const int c = (kk >> 3) + lhalf;
+            fa[slot][i] = *reinterpret_cast<const f16x8*>(as + row * kBK + ((c ^ swz(row)) * 8));
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) fb[slot][j] = *reinterpret_cast<const f16x8*>(bs + j * 32 * kPadK);
+    };
+    f32x16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+        }
+    }
+    auto mfmas = [&](int slot) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[slot][i], fb[slot][j], acc[i][j], 0, 0, 0);
+            }
+        }
+    };
+    const int steps = K / kBK;
+    directA(0, 0);
+    loadB(0);
+    storeB(0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    for (int s = 0; s < steps; ++s) {
+        const int buf = s & 1;
+        // Branch-free step body (one scheduling region): the last step
+        // re-loads its own, in-bounds K slice into the idle buffer.
+        const int kNext = (s + 1 < steps ? s + 1 : s) * kBK;
+        readFrags(buf, 0, 0);
+        directA(kNext, buf ^ 1);
+        loadB(kNext);
+        // kk = 0: next fragments + the next step's global loads.
+        readFrags(buf, 16, 1);
+        mfmas(0);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // 1 DS read
+            __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);   // 2 VMEM reads
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);   // 2 MFMA
+        }
+        readFrags(buf, 32, 0);
+        mfmas(1);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        }
+        readFrags(buf, 48, 1);
+        mfmas(0);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        }
+        mfmas(1);
+        storeB(buf ^ 1);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // 4 VALU (transpose)
+            __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);   // 1 DS write
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);   // 2 MFMA
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t cBase = col0 + wn * 128 + j * 32 + (lane & 31);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int64_t row = row0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                float* dst = C + row * ldc + cBase;
+                const float v = acc[i][j][r];
+                *dst = ACC ? *dst + v : v;
             }
         }
     }
@@ -196,11 +592,12 @@ __global__ __launch_bounds__(512) void gemmF16Mfma(const _Float16* __restrict__ 
 // ---------------------------------------------------------------- f32 ----
 constexpr int kFM = 64, kFN = 64, kFK = 32;
 
+template <bool ACC>
 __global__ __launch_bounds__(256) void gemmF32Mfma(const float* __restrict__ A,
                                                    const float* __restrict__ B,
                                                    float* __restrict__ C, int M, int N, int K,
                                                    int64_t lda, int64_t ldb, int64_t ldc,
-                                                   int accumulate) {
+                                                   int /*accumulate: template ACC*/) {
     __shared__ float At[2][kFK][kFM + 4];   // transposed: [k][m]
     __shared__ float Bs[2][kFK][kFN + 4];   // as loaded: [k][n]
     const int tid = threadIdx.x;
@@ -260,7 +657,7 @@ __global__ __launch_bounds__(256) void gemmF32Mfma(const float* __restrict__ A,
     for (int r = 0; r < 16; ++r) {
         const int64_t row = row0 + wm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         float* dst = C + row * ldc + cBase;
-        *dst = accumulate ? *dst + acc[r] : acc[r];
+        *dst = ACC ? *dst + acc[r] : acc[r];
     }
 }
 
@@ -339,7 +736,13 @@ __global__ __launch_bounds__(256) void gemmGeneral(mlkd_gemm p) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// f16 GEMM launch variant (0: 8 waves of 128x64; 1: 4 waves of 128x128),
+// set by the variant search through mlkd_gemm_set_variant.
+int gGemmF16Variant = 0;
+
 }  // namespace
+
+extern "C" void mlkd_gemm_set_variant(int variant) { gGemmF16Variant = variant; }
 
 extern "C" int mlkd_launch_gemm(const mlkd_gemm* p, void* stream) {
     if (p == nullptr || p->m < 0 || p->n < 0 || p->k < 0) return MLKD_RT_LAUNCH;
@@ -353,14 +756,71 @@ extern "C" int mlkd_launch_gemm(const mlkd_gemm* p, void* stream) {
         const size_t ldsBytes = 4 * kTileHalves * sizeof(_Float16);
         static bool ldsRaised = false;
         if (!ldsRaised) {
-            if (hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF16Mfma),
+            if (hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF16Mfma<true>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    static_cast<int>(ldsBytes)) != hipSuccess ||
+                hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF16Mfma<false>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    static_cast<int>(ldsBytes)) != hipSuccess ||
+                hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF16Mfma4w<true>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    static_cast<int>(ldsBytes)) != hipSuccess ||
+                hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF16Mfma4w<false>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize,
                                     static_cast<int>(ldsBytes)) != hipSuccess) {
                 return MLKD_RT_LAUNCH;
             }
             ldsRaised = true;
         }
-        hipLaunchKernelGGL(gemmF16Mfma, dim3(tiles), dim3(512), ldsBytes, st,
+        if (gGemmF16Variant == 3) {
+            const size_t ldsDirect = (2 * kTileA + 2 * kTileHalves) * sizeof(_Float16);
+            static bool raised3 = false;
+            if (!raised3) {
+                if (hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF16Mfma4wPipe<true>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        static_cast<int>(ldsDirect)) != hipSuccess ||
+                    hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF16Mfma4wPipe<false>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        static_cast<int>(ldsDirect)) != hipSuccess) {
+                    return MLKD_RT_LAUNCH;
+                }
+                raised3 = true;
+            }
+            hipLaunchKernelGGL((p->accumulate ? gemmF16Mfma4wPipe<true> : gemmF16Mfma4wPipe<false>), dim3(tiles),
+                               dim3(256), ldsDirect, st, static_cast<const _Float16*>(p->a),
+                               static_cast<const _Float16*>(p->b), static_cast<float*>(p->c),
+                               static_cast<int>(p->m), static_cast<int>(p->n), static_cast<int>(p->k), p->lda,
+                               p->ldb, p->ldc);
+            return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
+        }
+        if (gGemmF16Variant == 2) {
+            const size_t ldsDirect = (2 * kTileA + 2 * kTileHalves) * sizeof(_Float16);
+            static bool raised2 = false;
+            if (!raised2) {
+                if (hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF16Mfma4wDirect<true>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    static_cast<int>(ldsDirect)) != hipSuccess ||
+                hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF16Mfma4wDirect<false>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        static_cast<int>(ldsDirect)) != hipSuccess) {
+                    return MLKD_RT_LAUNCH;
+                }
+                raised2 = true;
+            }
+            hipLaunchKernelGGL((p->accumulate ? gemmF16Mfma4wDirect<true> : gemmF16Mfma4wDirect<false>), dim3(tiles), dim3(256), ldsDirect, st,
+                               static_cast<const _Float16*>(p->a), static_cast<const _Float16*>(p->b),
+                               static_cast<float*>(p->c), static_cast<int>(p->m), static_cast<int>(p->n),
+                               static_cast<int>(p->k), p->lda, p->ldb, p->ldc, p->accumulate);
+            return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
+        }
+        if (gGemmF16Variant == 1) {
+            hipLaunchKernelGGL((p->accumulate ? gemmF16Mfma4w<true> : gemmF16Mfma4w<false>), dim3(tiles), dim3(256), ldsBytes, st,
+                               static_cast<const _Float16*>(p->a), static_cast<const _Float16*>(p->b),
+                               static_cast<float*>(p->c), static_cast<int>(p->m), static_cast<int>(p->n),
+                               static_cast<int>(p->k), p->lda, p->ldb, p->ldc, p->accumulate);
+            return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
+        }
+        hipLaunchKernelGGL((p->accumulate ? gemmF16Mfma<true> : gemmF16Mfma<false>), dim3(tiles), dim3(512), ldsBytes, st,
                            static_cast<const _Float16*>(p->a), static_cast<const _Float16*>(p->b),
                            static_cast<float*>(p->c), static_cast<int>(p->m), static_cast<int>(p->n),
                            static_cast<int>(p->k), p->lda, p->ldb, p->ldc, p->accumulate);
@@ -370,7 +830,7 @@ extern "C" int mlkd_launch_gemm(const mlkd_gemm* p, void* stream) {
         p->c_dtype == MLKD_F32 && p->m % kFM == 0 && p->n % kFN == 0 && p->k % kFK == 0 &&
         p->lda % 4 == 0 && p->ldb % 4 == 0 && aligned16(p->a) && aligned16(p->b)) {
         const int tiles = static_cast<int>((p->m / kFM) * (p->n / kFN));
-        hipLaunchKernelGGL(gemmF32Mfma, dim3(tiles), dim3(256), 0, st,
+        hipLaunchKernelGGL((p->accumulate ? gemmF32Mfma<true> : gemmF32Mfma<false>), dim3(tiles), dim3(256), 0, st,
                            static_cast<const float*>(p->a), static_cast<const float*>(p->b),
                            static_cast<float*>(p->c), static_cast<int>(p->m), static_cast<int>(p->n),
                            static_cast<int>(p->k), p->lda, p->ldb, p->ldc, p->accumulate);

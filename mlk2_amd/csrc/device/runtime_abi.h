@@ -58,7 +58,11 @@ int mlkd_launch_softmax(const mlkd_softmax* p, void* stream);
 /// rows over `waves` waves; waves <= 0 keeps the default grid).
 void mlkd_softmax_set_variant(int variant, int64_t waves);
 int mlkd_launch_gemm(const mlkd_gemm* p, void* stream);
+/// Variant-space hook for the f16 GEMM (0: 8 waves x 128x64, 1: 4 waves x 128x128).
+void mlkd_gemm_set_variant(int variant);
 int mlkd_launch_score_softmax(const mlkd_score_softmax* p, void* stream);
+/// Variant-space hook for score-softmax (0: fused single pass, 1: two phase).
+void mlkd_score_set_variant(int variant);
 
 #ifdef __cplusplus
 }

@@ -62,6 +62,118 @@ __global__ __launch_bounds__(256) void scoresF16(const _Float16* __restrict__ Q,
     }
 }
 
+/// Fused single pass (seq <= 2048, seq % 128 == 0, dim % 16 == 0,
+/// dim <= 256): a workgroup owns 32 query rows of one batch and all seq key
+/// columns. Wave w computes the 32 x (seq/4) score block of columns
+/// [w*seq/4, (w+1)*seq/4) with v_mfma_f32_32x32x16_f16, keeping it in
+/// accumulators (seq/128 tiles of 32x32, at most 16 tiles = 256 AGPRs).
+/// Scale and bias are applied in registers, the row max and row sum are
+/// reduced across the 32 lanes of a half-wave (shuffles) and across the 4
+/// waves (LDS), and each normalized score is written to HBM exactly once:
+/// the kernel's HBM traffic is Q, K (L2-resident per batch) and one write
+/// of S.
+template <int NT>
+__global__ __launch_bounds__(256) void scoreSoftmaxFused(const _Float16* __restrict__ Q,
+                                                         const _Float16* __restrict__ K,
+                                                         const float* __restrict__ bias,
+                                                         float* __restrict__ S, int seq, int dim,
+                                                         float div) {
+    __shared__ float redMax[4][32];
+    __shared__ float redSum[4][32];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int rowsPerBatch = seq / 32;
+    const int64_t b = blockIdx.x / rowsPerBatch;
+    const int i0 = (blockIdx.x % rowsPerBatch) * 32;
+    const int j0 = wave * (NT * 32);
+    const int l32 = lane & 31;
+    const int half = lane >> 5;
+    const _Float16* q = Q + (b * seq + i0 + l32) * dim + half * 8;
+    const _Float16* kbase = K + (b * seq + j0 + l32) * dim + half * 8;
+    f32x16 acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[t][r] = 0.0f;
+    }
+    for (int kk = 0; kk < dim; kk += 16) {
+        const f16x8 a = *reinterpret_cast<const f16x8*>(q + kk);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const f16x8 x = *reinterpret_cast<const f16x8*>(kbase + static_cast<int64_t>(t) * 32 * dim + kk);
+            acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, x, acc[t], 0, 0, 0);
+        }
+    }
+    // Scale + bias; per-lane row maxima (register r holds row
+    // 8*(r/4) + 4*half + r%4 of the tile, column l32).
+    float rmax[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) rmax[r] = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const float bj = bias[j0 + t * 32 + l32];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float v = acc[t][r] / div + bj;
+            acc[t][r] = v;
+            rmax[r] = fmaxf(rmax[r], v);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+#pragma unroll
+        for (int off = 16; off >= 1; off >>= 1) rmax[r] = fmaxf(rmax[r], __shfl_xor(rmax[r], off, 64));
+    }
+    if (l32 == 0) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) redMax[wave][8 * (r >> 2) + 4 * half + (r & 3)] = rmax[r];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int row = 8 * (r >> 2) + 4 * half + (r & 3);
+        rmax[r] = fmaxf(fmaxf(redMax[0][row], redMax[1][row]), fmaxf(redMax[2][row], redMax[3][row]));
+    }
+    float rsum[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) rsum[r] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float e = __expf(acc[t][r] - rmax[r]);
+            acc[t][r] = e;
+            rsum[r] += e;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+#pragma unroll
+        for (int off = 16; off >= 1; off >>= 1) rsum[r] += __shfl_xor(rsum[r], off, 64);
+    }
+    if (l32 == 0) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) redSum[wave][8 * (r >> 2) + 4 * half + (r & 3)] = rsum[r];
+    }
+    __syncthreads();
+    float inv[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int row = 8 * (r >> 2) + 4 * half + (r & 3);
+        const float sum = (redSum[0][row] + redSum[1][row]) + (redSum[2][row] + redSum[3][row]);
+        inv[r] = sum != 0.0f ? 1.0f / sum : 0.0f;
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        float* dst = S + (b * seq + i0) * static_cast<int64_t>(seq) + j0 + t * 32 + l32;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = 8 * (r >> 2) + 4 * half + (r & 3);
+            __builtin_nontemporal_store(acc[t][r] * inv[r], dst + static_cast<int64_t>(row) * seq);
+        }
+    }
+}
+
 template <typename T>
 __device__ __forceinline__ double ldAny(const void* p, int dt, int64_t i) {
     if (dt == MLKD_F32) return static_cast<const float*>(p)[i];
@@ -92,7 +204,12 @@ __global__ __launch_bounds__(256) void scoresGeneral(mlkd_score_softmax p) {
     }
 }
 
+// 0: fused single pass where the shape allows it; 1: scores then softmax.
+int gScoreVariant = 0;
+
 }  // namespace
+
+extern "C" void mlkd_score_set_variant(int variant) { gScoreVariant = variant; }
 
 extern "C" int mlkd_launch_score_softmax(const mlkd_score_softmax* p, void* stream) {
     if (p == nullptr || p->batch < 0 || p->seq < 0 || p->dim < 0) return MLKD_RT_LAUNCH;
@@ -102,6 +219,37 @@ extern "C" int mlkd_launch_score_softmax(const mlkd_score_softmax* p, void* stre
                       p->seq % 128 == 0 && p->dim % 16 == 0 && p->dim > 0 && p->seq < (1 << 20) &&
                       (reinterpret_cast<uintptr_t>(p->q) & 15u) == 0 &&
                       (reinterpret_cast<uintptr_t>(p->k) & 15u) == 0 && p->dim % 8 == 0;
+    const bool fused = fast && p->seq <= 2048 && p->dim <= 256 && gScoreVariant == 0;
+    if (fused) {
+        const int64_t blocks = p->batch * (p->seq / 32);
+        if (blocks > 0x7FFFFFFF) return MLKD_RT_LAUNCH;
+        const int nt = static_cast<int>(p->seq / 128);
+        auto launch = [&](auto kern) {
+            hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st,
+                               static_cast<const _Float16*>(p->q), static_cast<const _Float16*>(p->k),
+                               static_cast<const float*>(p->bias), static_cast<float*>(p->s),
+                               static_cast<int>(p->seq), static_cast<int>(p->dim), static_cast<float>(p->div));
+        };
+        switch (nt) {
+            case 1: launch(scoreSoftmaxFused<1>); break;
+            case 2: launch(scoreSoftmaxFused<2>); break;
+            case 3: launch(scoreSoftmaxFused<3>); break;
+            case 4: launch(scoreSoftmaxFused<4>); break;
+            case 5: launch(scoreSoftmaxFused<5>); break;
+            case 6: launch(scoreSoftmaxFused<6>); break;
+            case 7: launch(scoreSoftmaxFused<7>); break;
+            case 8: launch(scoreSoftmaxFused<8>); break;
+            case 9: launch(scoreSoftmaxFused<9>); break;
+            case 10: launch(scoreSoftmaxFused<10>); break;
+            case 11: launch(scoreSoftmaxFused<11>); break;
+            case 12: launch(scoreSoftmaxFused<12>); break;
+            case 13: launch(scoreSoftmaxFused<13>); break;
+            case 14: launch(scoreSoftmaxFused<14>); break;
+            case 15: launch(scoreSoftmaxFused<15>); break;
+            default: launch(scoreSoftmaxFused<16>); break;
+        }
+        return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
+    }
     if (fast) {
         const int64_t blocks = p->batch * (p->seq / 64) * (p->seq / 128);
         if (blocks > 0x7FFFFFFF) return MLKD_RT_LAUNCH;

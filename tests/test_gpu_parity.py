@@ -265,6 +265,56 @@ def test_c5_score_softmax(hip, b, s, dm):
     assert e <= 1e-2
 
 
+def _score_ref(Q, K, bias, rows=None):
+    """Config-5 reference composed from oracle pieces: k-ascending f64 GEMM
+    Q_b K_b^T (Call(MatMul) with K^T materialized, as Transpose is rank-2),
+    then Div by the f64 constant sqrt(dim) and Add bias[j] (IEEE f64, the
+    walker's operations), then Call(Softmax)."""
+    B, S, D = Q.shape
+    out = []
+    for b in range(B):
+        q = Q[b].astype(np.float64) if rows is None else Q[b][rows].astype(np.float64)
+        sc = _gemm_ref(q, np.ascontiguousarray(K[b].astype(np.float64).T))
+        sc = sc / math.sqrt(D) + bias.astype(np.float64)
+        m = sc.shape[0]
+        km = fx.softmax_call_module(m, S, "f64")
+        out.append(oracle.run(km, {0: sc})[1].reshape(m, S))
+    return np.concatenate(out)
+
+
+@pytest.mark.parametrize("b,s,dm", [(1, 2048, 128), (2, 512, 64), (1, 384, 16)])
+def test_c5_fused_shapes(hip, b, s, dm):
+    say(f"c5 fused b={b} s={s} d={dm}")
+    d = inputs.config_inputs("c5", {"batch": b, "seq": s, "dim": dm})
+    km = fx.score_softmax_module(b, s, dm)
+    art = hip.build(km)
+    got = art.run({0: d["Q"], 1: d["K"], 2: d["bias"]})[3].reshape(b * s, s)
+    ref = _score_ref(d["Q"], d["K"], d["bias"])
+    e = max_rel(got, ref)
+    say(f"c5 fused max_rel={e:.3e}")
+    assert e <= 1e-2
+
+
+def test_c5_full_size_sampled_rows(hip):
+    b, s, dm = 16, 2048, 128
+    say("c5 full size 16x2048x2048, sampled rows")
+    d = inputs.config_inputs("c5")
+    km = fx.score_softmax_module(b, s, dm)
+    art = hip.build(km)
+    bufs = {0: DeviceBuffer.from_array(d["Q"], "f16"), 1: DeviceBuffer.from_array(d["K"], "f16"),
+            2: DeviceBuffer.from_array(d["bias"], "f32"), 3: DeviceBuffer(b * s * s, "f32")}
+    art.run_device(bufs)
+    got = bufs[3].to_numpy().reshape(b, s, s)
+    rows = np.random.default_rng(5).choice(s, 24, replace=False)
+    for bb in (0, 15):
+        ref = _score_ref(d["Q"][bb:bb + 1], d["K"][bb:bb + 1], d["bias"], rows=rows)
+        e = max_rel(got[bb][rows], ref)
+        say(f"c5 full batch {bb} max_rel={e:.3e}")
+        assert e <= 1e-2
+    sums = got.reshape(b * s, s)[::97].astype(np.float64).sum(axis=1)
+    assert np.abs(sums - 1.0).max() < 1e-3
+
+
 # ------------------------------------------------------------- entries ----
 def test_device_entry_matches_host_entry(hip):
     say("device entry vs host entry")
