@@ -20,6 +20,7 @@ namespace {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __global__ __launch_bounds__(256) void scoresF16(const _Float16* __restrict__ Q,
                                                  const _Float16* __restrict__ K,
@@ -174,6 +175,153 @@ __global__ __launch_bounds__(256) void scoreSoftmaxFused(const _Float16* __restr
     }
 }
 
+/// Fused single pass, second form (dim = 16*KS with KS in {4, 8}, seq =
+/// 32*NT*WAVES): WAVES waves per workgroup split the seq columns, each wave
+/// keeps NT 32x32 score tiles in accumulators. The dim loop is unrolled at
+/// compile time; Q fragments load once, and tile t+1's K fragments are
+/// loaded while tile t's MFMAs run. With WAVES = 8 and NT = 8 a wave needs
+/// 128 AGPRs, so two waves share each SIMD and one wave's stores overlap
+/// another's MFMAs. Workgroups of one batch are placed on one XCD
+/// (logical id = (id % 8) * (total / 8) + id / 8), so each batch's K is
+/// fetched into a single L2.
+template <int WAVES, int NT, int KS>
+__global__ __launch_bounds__(WAVES * 64) void scoreSoftmaxFusedT(const _Float16* __restrict__ Q,
+                                                                const _Float16* __restrict__ K,
+                                                                const float* __restrict__ bias,
+                                                                float* __restrict__ S, int seq,
+                                                                float div) {
+    constexpr int kDim = KS * 16;
+    __shared__ float redMax[WAVES][32];
+    __shared__ float redSum[WAVES][32];
+    // Output staging: 16 rows x (NT*32 + 4) floats per wave, so each global
+    // store writes one contiguous row span of the wave (NT*128 bytes).
+    constexpr int kStageW = NT * 32 + 4;
+    __shared__ __align__(16) float stage[WAVES][16 * kStageW];
+    const float rdiv = 1.0f / div;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int rowsPerBatch = seq / 32;
+    const int total = static_cast<int>(gridDim.x);
+    int id = static_cast<int>(blockIdx.x);
+    if (total % 8 == 0) id = (id % 8) * (total / 8) + id / 8;
+    const int64_t b = id / rowsPerBatch;
+    const int i0 = (id % rowsPerBatch) * 32;
+    const int j0 = wave * (NT * 32);
+    const int l32 = lane & 31;
+    const int half = lane >> 5;
+    const _Float16* q = Q + (b * seq + i0 + l32) * kDim + half * 8;
+    const _Float16* kbase = K + (b * seq + j0 + l32) * kDim + half * 8;
+    f16x8 a[KS];
+#pragma unroll
+    for (int k = 0; k < KS; ++k) a[k] = *reinterpret_cast<const f16x8*>(q + k * 16);
+    f16x8 xb[2][KS];
+#pragma unroll
+    for (int k = 0; k < KS; ++k) xb[0][k] = *reinterpret_cast<const f16x8*>(kbase + k * 16);
+    f32x16 acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        if (t + 1 < NT) {
+#pragma unroll
+            for (int k = 0; k < KS; ++k) {
+                xb[(t + 1) & 1][k] =
+                    *reinterpret_cast<const f16x8*>(kbase + static_cast<int64_t>(t + 1) * 32 * kDim + k * 16);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[t][r] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < KS; ++k) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[k], xb[t & 1][k], acc[t], 0, 0, 0);
+    }
+    float rmax[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) rmax[r] = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const float bj = bias[j0 + t * 32 + l32];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float v = acc[t][r] * rdiv + bj;
+            acc[t][r] = v;
+            rmax[r] = fmaxf(rmax[r], v);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+#pragma unroll
+        for (int off = 16; off >= 1; off >>= 1) rmax[r] = fmaxf(rmax[r], __shfl_xor(rmax[r], off, 64));
+    }
+    if (l32 == 0) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) redMax[wave][8 * (r >> 2) + 4 * half + (r & 3)] = rmax[r];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int row = 8 * (r >> 2) + 4 * half + (r & 3);
+        float m = redMax[0][row];
+#pragma unroll
+        for (int w = 1; w < WAVES; ++w) m = fmaxf(m, redMax[w][row]);
+        rmax[r] = m;
+    }
+    float rsum[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) rsum[r] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float e = __expf(acc[t][r] - rmax[r]);
+            acc[t][r] = e;
+            rsum[r] += e;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+#pragma unroll
+        for (int off = 16; off >= 1; off >>= 1) rsum[r] += __shfl_xor(rsum[r], off, 64);
+    }
+    if (l32 == 0) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) redSum[wave][8 * (r >> 2) + 4 * half + (r & 3)] = rsum[r];
+    }
+    __syncthreads();
+    float inv[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int row = 8 * (r >> 2) + 4 * half + (r & 3);
+        float sum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) sum += redSum[w][row];
+        inv[r] = sum != 0.0f ? 1.0f / sum : 0.0f;
+    }
+    float* stg = stage[wave];
+    float* rowBase = S + (b * seq + i0) * static_cast<int64_t>(seq) + j0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        // Registers 8h..8h+7 hold rows 16h..16h+15 of every tile.
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+#pragma unroll
+            for (int rr = 0; rr < 8; ++rr) {
+                const int r = 8 * h + rr;
+                const int rowLocal = 8 * (rr >> 2) + 4 * half + (rr & 3);
+                stg[rowLocal * kStageW + t * 32 + l32] = acc[t][r] * inv[r];
+            }
+        }
+        __syncthreads();
+        // Each row of the wave's span is NT*32 floats = NT*8 float4.
+#pragma unroll
+        for (int q = lane; q < 16 * NT * 8; q += 64) {
+            const int rowLocal = q / (NT * 8);
+            const int c4 = q - rowLocal * (NT * 8);
+            const f32x4 v = *reinterpret_cast<const f32x4*>(stg + rowLocal * kStageW + c4 * 4);
+            __builtin_nontemporal_store(
+                v, reinterpret_cast<f32x4*>(rowBase + static_cast<int64_t>(16 * h + rowLocal) * seq + c4 * 4));
+        }
+        __syncthreads();
+    }
+}
+
 template <typename T>
 __device__ __forceinline__ double ldAny(const void* p, int dt, int64_t i) {
     if (dt == MLKD_F32) return static_cast<const float*>(p)[i];
@@ -220,6 +368,43 @@ extern "C" int mlkd_launch_score_softmax(const mlkd_score_softmax* p, void* stre
                       (reinterpret_cast<uintptr_t>(p->q) & 15u) == 0 &&
                       (reinterpret_cast<uintptr_t>(p->k) & 15u) == 0 && p->dim % 8 == 0;
     const bool fused = fast && p->seq <= 2048 && p->dim <= 256 && gScoreVariant == 0;
+    // Second fused form for dim 64/128 and seq a multiple of 256 (8 waves of
+    // seq/256 tiles, at most 8 tiles per wave).
+    if (fused && (p->dim == 128 || p->dim == 64) && p->seq % 256 == 0) {
+        const int64_t blocks = p->batch * (p->seq / 32);
+        if (blocks > 0x7FFFFFFF) return MLKD_RT_LAUNCH;
+        const int nt = static_cast<int>(p->seq / 256);
+        auto launch = [&](auto kern) {
+            hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(blocks)), dim3(512), 0, st,
+                               static_cast<const _Float16*>(p->q), static_cast<const _Float16*>(p->k),
+                               static_cast<const float*>(p->bias), static_cast<float*>(p->s),
+                               static_cast<int>(p->seq), static_cast<float>(p->div));
+        };
+        if (p->dim == 128) {
+            switch (nt) {
+                case 1: launch(scoreSoftmaxFusedT<8, 1, 8>); break;
+                case 2: launch(scoreSoftmaxFusedT<8, 2, 8>); break;
+                case 3: launch(scoreSoftmaxFusedT<8, 3, 8>); break;
+                case 4: launch(scoreSoftmaxFusedT<8, 4, 8>); break;
+                case 5: launch(scoreSoftmaxFusedT<8, 5, 8>); break;
+                case 6: launch(scoreSoftmaxFusedT<8, 6, 8>); break;
+                case 7: launch(scoreSoftmaxFusedT<8, 7, 8>); break;
+                default: launch(scoreSoftmaxFusedT<8, 8, 8>); break;
+            }
+        } else {
+            switch (nt) {
+                case 1: launch(scoreSoftmaxFusedT<8, 1, 4>); break;
+                case 2: launch(scoreSoftmaxFusedT<8, 2, 4>); break;
+                case 3: launch(scoreSoftmaxFusedT<8, 3, 4>); break;
+                case 4: launch(scoreSoftmaxFusedT<8, 4, 4>); break;
+                case 5: launch(scoreSoftmaxFusedT<8, 5, 4>); break;
+                case 6: launch(scoreSoftmaxFusedT<8, 6, 4>); break;
+                case 7: launch(scoreSoftmaxFusedT<8, 7, 4>); break;
+                default: launch(scoreSoftmaxFusedT<8, 8, 4>); break;
+            }
+        }
+        return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
+    }
     if (fused) {
         const int64_t blocks = p->batch * (p->seq / 32);
         if (blocks > 0x7FFFFFFF) return MLKD_RT_LAUNCH;
