@@ -128,6 +128,13 @@ int mlkhip_time_device(const mlkhip_artifact* a, const mlkhip_binding* binds, in
                        const double* scalars, int64_t n_scalars, int64_t elements, void* stream,
                        int warmup, int reps, float* ms_out);
 
+/* Times `reps` back-to-back launches with one HIP event pair around the
+ * whole span on `stream` (after `warmup` untimed launches) and writes the
+ * average milliseconds per launch into `avg_ms`. */
+int mlkhip_time_device_span(const mlkhip_artifact* a, const mlkhip_binding* binds, int n_binds,
+                            const double* scalars, int64_t n_scalars, int64_t elements, void* stream,
+                            int warmup, int reps, float* avg_ms);
+
 /* ---- device memory plumbing for hosts without another HIP runtime ----- */
 int mlkhip_malloc(void** p, size_t bytes);
 int mlkhip_free(void* p);

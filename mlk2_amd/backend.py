@@ -80,6 +80,9 @@ def lib():
     L.mlkhip_time_device.argtypes = [c.c_void_p, c.POINTER(Binding), c.c_int, _PD, c.c_int64,
                                      c.c_int64, c.c_void_p, c.c_int, c.c_int,
                                      c.POINTER(c.c_float)]
+    L.mlkhip_time_device_span.argtypes = [c.c_void_p, c.POINTER(Binding), c.c_int, _PD, c.c_int64,
+                                          c.c_int64, c.c_void_p, c.c_int, c.c_int,
+                                          c.POINTER(c.c_float)]
     L.mlkhip_malloc.argtypes = [c.POINTER(c.c_void_p), c.c_size_t]
     L.mlkhip_free.argtypes = [c.c_void_p]
     L.mlkhip_memcpy_h2d.argtypes = [c.c_void_p, c.c_void_p, c.c_size_t]
@@ -270,6 +273,19 @@ class LoadedKernel:
         _check(lib().mlkhip_time_device(self._h, arr, n, sc.ctypes.data_as(_PD), nsc,
                                         int(elements), stream, warmup, reps, ms))
         return np.array(ms[:reps], dtype=np.float64)
+
+
+    def time_device_span(self, bufs: Dict[int, DeviceBuffer], reps: int, warmup: int = 5,
+                         scalars: Sequence[float] = (), elements: int = 0,
+                         stream: Optional[int] = None) -> float:
+        """Average ms per launch over `reps` back-to-back launches, one event
+        pair around the span."""
+        arr, n = self._bindings(bufs)
+        sc, nsc = self._scalars(scalars)
+        ms = ctypes.c_float(0.0)
+        _check(lib().mlkhip_time_device_span(self._h, arr, n, sc.ctypes.data_as(_PD), nsc,
+                                             int(elements), stream, warmup, reps, ctypes.byref(ms)))
+        return float(ms.value)
 
 
 def _numel(b, elements: int) -> int:

@@ -536,6 +536,30 @@ int mlkhip_time_device(const mlkhip_artifact* a, const mlkhip_binding* binds, in
     return rc;
 }
 
+int mlkhip_time_device_span(const mlkhip_artifact* a, const mlkhip_binding* binds, int n_binds,
+                            const double* scalars, int64_t n_scalars, int64_t elements, void* stream,
+                            int warmup, int reps, float* avg_ms) {
+    for (int w = 0; w < warmup; ++w) {
+        const int rc = mlkhip_run_device(a, binds, n_binds, scalars, n_scalars, elements, stream);
+        if (rc != MLKHIP_OK) return rc;
+    }
+    void* e0 = nullptr;
+    void* e1 = nullptr;
+    if (mlkd_rt_event_create(&e0) != 0 || mlkd_rt_event_create(&e1) != 0) return setError(MLKHIP_LAUNCH, "event create");
+    int rc = mlkd_rt_event_record(e0, stream) == 0 ? MLKHIP_OK : MLKHIP_LAUNCH;
+    for (int r = 0; r < reps && rc == MLKHIP_OK; ++r) {
+        rc = mlkhip_run_device(a, binds, n_binds, scalars, n_scalars, elements, stream);
+    }
+    float ms = 0.0f;
+    if (rc == MLKHIP_OK && (mlkd_rt_event_record(e1, stream) != 0 || mlkd_rt_event_elapsed_ms(e0, e1, &ms) != 0)) {
+        rc = setError(MLKHIP_LAUNCH, "event timing");
+    }
+    if (avg_ms != nullptr) *avg_ms = reps > 0 ? ms / static_cast<float>(reps) : 0.0f;
+    mlkd_rt_event_destroy(e0);
+    mlkd_rt_event_destroy(e1);
+    return rc;
+}
+
 int mlkhip_malloc(void** p, size_t bytes) { return mlkd_rt_malloc(p, bytes); }
 int mlkhip_free(void* p) { return mlkd_rt_free(p); }
 int mlkhip_memcpy_h2d(void* dst, const void* src, size_t bytes) {
