@@ -175,19 +175,17 @@ constexpr int kSeg = 64 * kPer;    // elements per wave segment of a row
 template <int DT>
 __device__ __forceinline__ void loadGroup(const void* p, long long i, double* v) {
     if constexpr (DT == 0) {
-        const mlk_f32x4 f =
-            __builtin_nontemporal_load(reinterpret_cast<const mlk_f32x4*>(static_cast<const float*>(p) + i));
+        const mlk_f32x4 f = *reinterpret_cast<const mlk_f32x4*>(static_cast<const float*>(p) + i);
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = static_cast<double>(f[e]);
     } else if constexpr (DT == 1) {
-        const mlk_f16x4 h = __builtin_nontemporal_load(
-            reinterpret_cast<const mlk_f16x4*>(static_cast<const _Float16*>(p) + i));
+        const mlk_f16x4 h = *reinterpret_cast<const mlk_f16x4*>(static_cast<const _Float16*>(p) + i);
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = static_cast<double>(static_cast<float>(h[e]));
     } else {
         const mlk_f64x2* q = reinterpret_cast<const mlk_f64x2*>(static_cast<const double*>(p) + i);
-        const mlk_f64x2 a = __builtin_nontemporal_load(q);
-        const mlk_f64x2 b = __builtin_nontemporal_load(q + 1);
+        const mlk_f64x2 a = q[0];
+        const mlk_f64x2 b = q[1];
         v[0] = a[0];
         v[1] = a[1];
         v[2] = b[0];

@@ -52,7 +52,7 @@ __global__ __launch_bounds__(256) void softmaxWaveRow(const float* x,
         for (int c = 0; c < CH; ++c) {
             const int64_t col = (static_cast<int64_t>(c) * 64 + lane) * 4;
             if (col < cols) {
-                v[c] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(xr + col));
+                v[c] = *reinterpret_cast<const f32x4*>(xr + col);
             } else {
                 v[c] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
             }
@@ -105,7 +105,7 @@ __global__ __launch_bounds__(256) void softmaxWaveRowPipelined(const float* x, f
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
             const int64_t col = (static_cast<int64_t>(c) * 64 + lane) * 4;
-            v[c] = col < cols ? __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(xr + col))
+            v[c] = col < cols ? *reinterpret_cast<const f32x4*>(xr + col)
                               : f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
         }
     };
