@@ -77,9 +77,10 @@ int mlkhip_build(const char* module_json, size_t len, const char* arch, const ch
 int mlkhip_plan(const char* module_json, size_t len, char* class_name, size_t class_cap,
                 char* policy, size_t policy_cap, int* n_steps);
 
-/* Instantiates the template source of step `step` (elementwise steps) and
- * compiles it for `arch` without loading; returns the code-object size, 0
- * for steps that use precompiled kernels, or -1. `source` may be NULL. */
+/* Instantiates the hipRTC source of step `step` (elementwise and generic
+ * loop-nest steps) and compiles it for `arch` without loading; returns the
+ * code-object size, 0 for steps that use precompiled kernels, or -1.
+ * `source` may be NULL. */
 long long mlkhip_compile_check(const char* module_json, size_t len, int step, const char* arch,
                                char* source, size_t source_cap);
 

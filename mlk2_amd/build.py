@@ -30,7 +30,7 @@ HIPCC = os.path.join(ROCM, "bin", "hipcc")
 CLANG = os.path.join(ROCM, "llvm", "bin", "clang++")
 
 DEVICE_SOURCES = ["runtime.hip", "jit.hip", "softmax.hip", "gemm.hip", "score_softmax.hip"]
-HOST_SOURCES = ["kernel_ir.cpp", "planner.cpp", "codegen.cpp", "driver.cpp"]
+HOST_SOURCES = ["kernel_ir.cpp", "planner.cpp", "codegen.cpp", "nestgen.cpp", "driver.cpp"]
 
 HIP_FLAGS = [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
              "-Wall", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
@@ -46,15 +46,22 @@ def _run(cmd):
     return out
 
 
-def _embed_template(gen_dir: str) -> None:
-    src = open(os.path.join(CSRC, "device", "elementwise_template.hip")).read()
+def _embed(gen_dir: str, source: str, symbol: str, inc: str) -> None:
+    src = open(os.path.join(CSRC, "device", source)).read()
     if ")MLKTPL" in src:
-        raise RuntimeError("template text contains the raw-string delimiter")
-    text = 'static const char kElementwiseTemplate[] = R"MLKTPL(' + src + ')MLKTPL";\n'
-    path = os.path.join(gen_dir, "elementwise_template.inc")
+        raise RuntimeError(f"{source} contains the raw-string delimiter")
+    text = f'static const char {symbol}[] = R"MLKTPL(' + src + ')MLKTPL";\n'
+    path = os.path.join(gen_dir, inc)
     if not os.path.exists(path) or open(path).read() != text:
         with open(path, "w") as f:
             f.write(text)
+
+
+def _embed_template(gen_dir: str) -> None:
+    """The hipRTC sources the host code instantiates: the device math header
+    (prepended to every instance) and the elementwise template."""
+    _embed(gen_dir, "mlk_device_math.h", "kDeviceMathHeader", "device_math.inc")
+    _embed(gen_dir, "elementwise_template.hip", "kElementwiseTemplate", "elementwise_template.inc")
 
 
 def build(verbose: bool = False) -> str:

@@ -200,4 +200,16 @@ int mlkd_jit_launch_elementwise(void* fn, unsigned grid, const void* const* in, 
     return e == hipSuccess ? 0 : MLKD_RT_LAUNCH;
 }
 
+/// Launches a generic loop-nest instance, 256 threads per workgroup.
+int mlkd_jit_launch_nest(void* fn, unsigned grid, const mlkd_nest_args* args,
+                         const mlkd_scalars* scalars, long long total, void* stream) {
+    mlkd_nest_args a = *args;
+    mlkd_scalars sc = *scalars;
+    long long t = total;
+    void* kargs[] = {&a, &sc, &t};
+    const hipError_t e = hipModuleLaunchKernel(static_cast<hipFunction_t>(fn), grid, 1, 1, 256, 1, 1, 0,
+                                               static_cast<hipStream_t>(stream), kargs, nullptr);
+    return e == hipSuccess ? 0 : MLKD_RT_LAUNCH;
+}
+
 }  // extern "C"

@@ -49,6 +49,20 @@ long long mlkd_jit_compile_only(const char* src, size_t len, const char* arch, c
                                 size_t cap);
 int mlkd_jit_launch_elementwise(void* fn, unsigned grid, const void* const* in, void* out,
                                 const mlkd_scalars* scalars, long long dyn_extent, void* stream);
+
+/// Kernel argument block of a generic loop-nest instance (the generated
+/// kernel declares the same layout): buffer slots, their element counts, the
+/// status word of run-time bounds checks, the run's element count.
+typedef struct {
+    void* p[16];
+    long long n[16];
+    int* status;
+    long long elements;
+} mlkd_nest_args;
+
+/// Launches a loop-nest instance: (mlkd_nest_args, scalars, long long total).
+int mlkd_jit_launch_nest(void* fn, unsigned grid, const mlkd_nest_args* args,
+                         const mlkd_scalars* scalars, long long total, void* stream);
 int mlkd_launch_rowsum(const mlkd_softmax* p, void* stream);
 
 /// Kernel launchers (device/*.hip). Each validates nothing beyond launch

@@ -10,6 +10,7 @@
 namespace mlk::hip {
 
 namespace {
+#include "device_math.inc"           // kDeviceMathHeader (generated at build)
 #include "elementwise_template.inc"  // kElementwiseTemplate (generated at build)
 
 int dtypeCode(Dtype d) { return d == Dtype::F32 ? 0 : (d == Dtype::F16 ? 1 : 2); }
@@ -69,7 +70,9 @@ std::string elementwiseSource(const KernelModule& km, const Step& st) {
         start = nl + 1;
     }
     p += joined + "\n";
-    return p + kElementwiseTemplate;
+    return p + kDeviceMathHeader + kElementwiseTemplate;
 }
+
+const char* deviceMathHeader() { return kDeviceMathHeader; }
 
 }  // namespace mlk::hip

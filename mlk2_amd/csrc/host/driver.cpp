@@ -54,10 +54,10 @@ Result<std::unique_ptr<HipLoadedKernel>> buildHipKernelArtifact(const KernelModu
     if (!validArch(config.arch)) {
         return err(ErrorCode::InvalidArgument, "invalid HIP target '" + config.arch + "' (want gfx<hex>)");
     }
-    auto plan = planModule(km);
-    if (!plan.has_value()) return err(plan.error().code, plan.error().message);
     std::unique_ptr<HipLoadedKernel> k(new HipLoadedKernel());
-    k->km_ = km;
+    k->km_ = deviceModule(km);
+    auto plan = planModule(k->km_);
+    if (!plan.has_value()) return err(plan.error().code, plan.error().message);
     k->plan_ = std::move(*plan);
     k->arch_ = config.arch;
     k->bindIndex_.assign(km.buffers.size(), -1);
@@ -80,6 +80,11 @@ Result<std::unique_ptr<HipLoadedKernel>> buildHipKernelArtifact(const KernelModu
                 return err(ErrorCode::InvalidGraph, "operand buffer is not bindable");
             }
         }
+        for (const uint32_t b : st.nestBufs) {
+            if (b >= km.buffers.size() || k->bindIndex_[b] < 0) {
+                return err(ErrorCode::InvalidGraph, "loop-nest buffer is not bindable");
+            }
+        }
     }
     const int devices = mlkd_rt_device_count();
     if (devices <= 0) return err(ErrorCode::UnsupportedCapability, "no HIP device visible");
@@ -90,20 +95,31 @@ Result<std::unique_ptr<HipLoadedKernel>> buildHipKernelArtifact(const KernelModu
                    "declared target " + config.arch + " does not match device " + devArch);
     }
     for (Step& st : k->plan_.steps) {
-        if (st.kind != StepKind::Elementwise) continue;
-        st.source = elementwiseSource(km, st);
+        if (st.kind != StepKind::Elementwise && st.kind != StepKind::Nest) continue;
+        const bool nest = st.kind == StepKind::Nest;
+        if (!nest) st.source = elementwiseSource(k->km_, st);
         char log[4096] = {0};
         void* fn = nullptr;
         uint64_t fp = 0;
-        const int rc = mlkd_jit_build(st.source.data(), st.source.size(), "mlk_elementwise",
+        const int rc = mlkd_jit_build(st.source.data(), st.source.size(), nest ? "mlk_nest" : "mlk_elementwise",
                                       config.arch.c_str(), config.cacheDir.c_str(), &fn, &fp, log,
                                       sizeof(log));
-        if (rc != 0) return err(ErrorCode::UnsupportedCapability, std::string("template instance: ") + log);
+        if (rc != 0) {
+            return err(ErrorCode::UnsupportedCapability,
+                       std::string(nest ? "loop-nest instance: " : "template instance: ") + log);
+        }
         st.fn = fn;
     }
     k->scratch_.assign(km.buffers.size(), nullptr);
     k->scratchElems_.assign(km.buffers.size(), 0);
     return k;
+}
+
+HipLoadedKernel::~HipLoadedKernel() {
+    for (void* p : scratch_) {
+        if (p != nullptr) mlkd_rt_free(p);
+    }
+    if (status_ != nullptr) mlkd_rt_free(status_);
 }
 
 int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* scalars,
@@ -233,6 +249,46 @@ int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* 
                 rc = mlkd_launch_gemm(&p, stream);
                 break;
             }
+            case StepKind::Nest: {
+                mlkd_nest_args na;
+                std::memset(&na, 0, sizeof(na));
+                for (size_t sl = 0; sl < st.nestBufs.size(); ++sl) {
+                    const uint32_t b = st.nestBufs[sl];
+                    na.p[sl] = ptr[b];
+                    const int bi = bindIndex_[b];
+                    na.n[sl] = km_.buffers[b].isTemp && binds[bi].ptr == nullptr
+                                   ? bufferElements(km_.buffers[b], elements)
+                                   : binds[bi].elements;
+                }
+                na.elements = elements;
+                if (st.checked) {
+                    std::lock_guard<std::mutex> g(scratchLock_);
+                    if (status_ == nullptr && mlkd_rt_malloc(&status_, 256) != 0) {
+                        status_ = nullptr;
+                        why = "status word allocation failed";
+                        return MLKHIP_RUNTIME;
+                    }
+                    if (mlkd_rt_fill32(status_, 0u, 4, stream) != 0) {
+                        why = "status word clear failed";
+                        return MLKHIP_LAUNCH;
+                    }
+                    na.status = static_cast<int*>(status_);
+                }
+                rc = mlkd_jit_launch_nest(st.fn, gridFor(st.threads), &na, &sc, st.threads, stream);
+                if (rc == 0 && st.checked) {
+                    int status = 0;
+                    if (mlkd_rt_d2h(&status, status_, sizeof(status), stream) != 0 || mlkd_rt_sync(stream) != 0) {
+                        why = "status word read-back failed";
+                        return MLKHIP_LAUNCH;
+                    }
+                    if (status != 0) {
+                        why = status == MLKHIP_NEG_STORE ? "walker: negative store address"
+                                                         : "loop nest reaches outside a bound buffer";
+                        return status;
+                    }
+                }
+                break;
+            }
             case StepKind::ScoreSoftmax: {
                 mlkd_score_softmax p;
                 p.q = ptr[st.q];
@@ -276,6 +332,9 @@ int HipLoadedKernel::runHost(double* const* ptrs, int n, const double* scalars, 
         const uint32_t w[] = {st.out.buffer, st.y, st.c, st.s};
         for (const uint32_t b : w) {
             if (b != kInvalidId && b < written.size()) written[b] = true;
+        }
+        for (const uint32_t b : st.nestWrites) {
+            if (b < written.size()) written[b] = true;
         }
     }
     std::vector<DeviceBinding> binds(bindables_.size());
@@ -429,7 +488,7 @@ int mlkhip_plan(const char* module_json, size_t len, char* class_name, size_t cl
                 size_t policy_cap, int* n_steps) {
     auto km = mlk::hip::parseKernelModule(module_json, len);
     if (!km.has_value()) return setError(MLKHIP_REFUSED, km.error().message);
-    auto plan = mlk::hip::planModule(*km);
+    auto plan = mlk::hip::planModule(mlk::hip::deviceModule(*km));
     if (!plan.has_value()) return setError(MLKHIP_REFUSED, plan.error().message);
     copyOut(class_name, class_cap, plan->className);
     copyOut(policy, policy_cap, plan->policy);
@@ -441,12 +500,13 @@ long long mlkhip_compile_check(const char* module_json, size_t len, int step, co
                                char* source, size_t source_cap) {
     auto km = mlk::hip::parseKernelModule(module_json, len);
     if (!km.has_value()) return setError(-1, km.error().message);
-    auto plan = mlk::hip::planModule(*km);
+    const mlk::hip::KernelModule dm = mlk::hip::deviceModule(*km);
+    auto plan = mlk::hip::planModule(dm);
     if (!plan.has_value()) return setError(-1, plan.error().message);
     if (step < 0 || static_cast<size_t>(step) >= plan->steps.size()) return setError(-1, "step out of range");
     const mlk::hip::Step& st = plan->steps[static_cast<size_t>(step)];
-    if (st.kind != mlk::hip::StepKind::Elementwise) return 0;
-    const std::string src = mlk::hip::elementwiseSource(*km, st);
+    if (st.kind != mlk::hip::StepKind::Elementwise && st.kind != mlk::hip::StepKind::Nest) return 0;
+    const std::string src = st.kind == mlk::hip::StepKind::Nest ? st.source : mlk::hip::elementwiseSource(dm, st);
     copyOut(source, source_cap, src);
     if (arch == nullptr || !mlk::hip::validArch(arch)) return setError(-1, "invalid arch");
     char log[4096] = {0};

@@ -34,6 +34,8 @@ struct DeviceBinding {
 
 class HipLoadedKernel {
 public:
+    ~HipLoadedKernel();  // frees the artifact-owned scratch (temps, status word)
+
     const KernelModule& module() const { return km_; }
     const Plan& plan() const { return plan_; }
     const std::vector<uint32_t>& bindables() const { return bindables_; }
@@ -61,6 +63,8 @@ private:
     mutable std::mutex scratchLock_;
     mutable std::vector<void*> scratch_;
     mutable std::vector<int64_t> scratchElems_;
+    // Status word of loop-nest steps with run-time bounds checks.
+    mutable void* status_{nullptr};
 };
 
 /// Plans, instantiates and loads (buildGpuKernelArtifact analogue).

@@ -19,6 +19,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <functional>
 
 #include "../device_abi.h"
 
@@ -78,6 +79,17 @@ bool sameMap(const StreamRef& a, const StreamRef& b, int rank) {
     return true;
 }
 
+/// Adapts a stream-index lookup to chainCode's operand callback.
+template <class StreamOf>
+std::function<std::string(const KernelOperand&)> streamCode(StreamOf& streamOf) {
+    return [&streamOf](const KernelOperand& o) -> std::string {
+        const int s = streamOf(o);
+        return s < 0 ? std::string() : "in[" + std::to_string(s) + "]";
+    };
+}
+
+}  // namespace
+
 std::string literal(double v) {
     if (std::isnan(v)) return "__builtin_nan(\"\")";
     if (std::isinf(v)) return v > 0 ? "__builtin_inf()" : "(-__builtin_inf())";
@@ -86,13 +98,13 @@ std::string literal(double v) {
     return std::string("(") + buf + ")";
 }
 
-/// Builds the f64 chain body; stream(o) returns the stream index of an
-/// element operand. The reference evaluation (kernel_buffers.cpp:106-178):
-/// unary ops ignore b, Temp reads earlier results, ScalarParam past the
-/// table reads 0.0.
-template <class StreamOf>
+/// Builds the f64 chain body; elemCode(o) returns the device expression of an
+/// element operand (empty when it cannot be realized). The reference
+/// evaluation (kernel_buffers.cpp:106-178): unary ops ignore b, Temp reads
+/// earlier results, ScalarParam past the table reads 0.0.
 Result<std::string> chainCode(const std::vector<KernelExpr>& exprs, bool poly7, bool f32Out,
-                              StreamOf streamOf) {
+                              const std::function<std::string(const KernelOperand&)>& elemCode,
+                              const std::string& sink) {
     if (exprs.empty() || exprs.size() > 64) {
         return err(ErrorCode::UnsupportedCapability, "chain length outside 1..64");
     }
@@ -102,12 +114,9 @@ Result<std::string> chainCode(const std::vector<KernelExpr>& exprs, bool poly7, 
             case K::Const: out = literal(o.constValue); return true;
             case K::ElemA:
             case K::ElemB:
-            case K::ElemIdx: {
-                const int s = streamOf(o);
-                if (s < 0) return false;
-                out = "in[" + std::to_string(s) + "]";
-                return true;
-            }
+            case K::ElemIdx:
+                out = elemCode(o);
+                return !out.empty();
             case K::ScalarParam:
                 if (o.index < 0 || o.index >= MLKD_MAX_SCALARS) return false;
                 out = "sc.v[" + std::to_string(o.index) + "]";
@@ -166,9 +175,11 @@ Result<std::string> chainCode(const std::vector<KernelExpr>& exprs, bool poly7, 
         }
         body += "    const double t" + id + " = " + v + ";\n";
     }
-    body += "    return t" + std::to_string(exprs.size() - 1) + ";\n";
+    body += "    " + sink + "t" + std::to_string(exprs.size() - 1) + ";\n";
     return body;
 }
+
+namespace {
 
 struct NestInfo {
     int depth{0};
@@ -310,7 +321,7 @@ Result<Step> elementwiseNest(const KernelModule& km, const NestInfo& ni) {
     };
     const Dtype od = km.buffers[so.bufferOut].dtype;
     const bool f32Out = (od == Dtype::F32 || od == Dtype::F16) && so.accum == AccumMode::None;
-    auto body = chainCode(cp.exprs, cp.family == "poly7", f32Out, streamOf);
+    auto body = chainCode(cp.exprs, cp.family == "poly7", f32Out, streamCode(streamOf), "return ");
     if (!body.has_value()) return err(body.error().code, body.error().message);
     if (bad) return err(ErrorCode::UnsupportedCapability, "more than 4 distinct element streams");
     for (const StreamRef& s : ins) {
@@ -399,7 +410,8 @@ Result<std::vector<Step>> tier1Loop(const KernelModule& km, const KernelNode& lo
             return -1;  // ElemIdx is a multi-dim operand
         };
         const Dtype od = km.buffers[so.bufferOut].dtype;
-        auto body = chainCode(exprs, c.family == "poly7", od == Dtype::F32 || od == Dtype::F16, streamOf);
+        auto body = chainCode(exprs, c.family == "poly7", od == Dtype::F32 || od == Dtype::F16,
+                              streamCode(streamOf), "return ");
         if (!body.has_value()) return err(body.error().code, body.error().message);
         st.chainBody = *body;
         st.out = ref(so.bufferOut);
@@ -786,6 +798,9 @@ void markTemps(const KernelModule& km, const Step& st, std::vector<bool>& need) 
             mark(st.bias);
             mark(st.s);
             break;
+        case StepKind::Nest:
+            for (const uint32_t b : st.nestBufs) mark(b);
+            break;
         case StepKind::Fail:
             break;
     }
@@ -793,8 +808,16 @@ void markTemps(const KernelModule& km, const Step& st, std::vector<bool>& need) 
 
 std::string policyFor(const KernelModule& km, const std::vector<Step>& steps) {
     bool transcend = false, gemm16 = false, gemm32 = false, soft = false, p7out = false, score = false;
+    bool nestNarrow = false, nestF16 = false;
     for (const Step& st : steps) {
         switch (st.kind) {
+            case StepKind::Nest:
+                // f64 buffers and IEEE ops: bit-exact with the walker. A value
+                // re-read from an f32/f16 buffer carries that buffer's rounding.
+                if (st.transcendental) transcend = true;
+                if (st.narrowRoundTrip) nestNarrow = true;
+                if (st.touchesF16 && (st.narrowRoundTrip || st.transcendental)) nestF16 = true;
+                break;
             case StepKind::Elementwise:
                 if (st.chainBody.find("mlk_p7_sin_f32out") != std::string::npos) p7out = true;
                 for (const char* f : {"exp(", "log(", "sin(", "cos(", "tan(", "tanh(", "erf(", "pow("}) {
@@ -814,7 +837,8 @@ std::string policyFor(const KernelModule& km, const std::vector<Step>& steps) {
             case StepKind::Fail: break;
         }
     }
-    if (score || gemm16) return "tol-rel1e-2-gfx950-v1";
+    if (score || gemm16 || nestF16) return "tol-rel1e-2-gfx950-v1";
+    if (nestNarrow) return "tol-rel1e-6-gfx950-v1";
     if (gemm32) return "tol-rel1e-5sqrtk-gfx950-v1";
     if (soft || transcend) return "tol-rel1e-6-gfx950-v1";
     if (p7out) return "tol-4ulp-f32-gfx950-v1";
@@ -822,6 +846,14 @@ std::string policyFor(const KernelModule& km, const std::vector<Step>& steps) {
 }
 
 }  // namespace
+
+KernelModule deviceModule(const KernelModule& km) {
+    KernelModule d = km;
+    for (KernelBuffer& b : d.buffers) {
+        if (b.isTemp && !b.isInput && !b.isOutput) b.dtype = Dtype::F64;
+    }
+    return d;
+}
 
 int64_t bufferElements(const KernelBuffer& b, int64_t dynamicElements) {
     if (!b.dims.empty()) {
@@ -871,7 +903,9 @@ Result<Plan> planModule(const KernelModule& km) {
             }
             if (r.op != KernelOp::Loop) {
                 if (r.op == KernelOp::Guard && r.hasAffineGuard()) {
-                    return err(ErrorCode::UnsupportedCapability, "guarded root: no HIP class (generic nest path)");
+                    auto ns = planNest(km, roots[i]);
+                    if (!ns.has_value()) return err(ns.error().code, ns.error().message);
+                    plan.steps.push_back(std::move(*ns));
                 }
                 continue;  // Compute/Store/etc. at root carry no semantics for the walker
             }
@@ -888,13 +922,16 @@ Result<Plan> planModule(const KernelModule& km) {
             NestInfo ni;
             if (perfectNest(km, roots[i], ni)) {
                 auto es = elementwiseNest(km, ni);
-                if (!es.has_value()) return err(es.error().code, es.error().message);
-                plan.steps.push_back(std::move(*es));
-                continue;
+                if (es.has_value()) {
+                    plan.steps.push_back(std::move(*es));
+                    continue;
+                }
+                if (es.error().code != ErrorCode::UnsupportedCapability) return err(es.error().code, es.error().message);
             }
-            return err(ErrorCode::UnsupportedCapability,
-                       "loop nest rooted at node " + std::to_string(roots[i]) +
-                           " matches no HIP class (tiled/guarded/affine-bound nests need the generic path)");
+            // No hand-written class claims the root: the generic loop-nest kernel.
+            auto ns = planNest(km, roots[i]);
+            if (!ns.has_value()) return err(ns.error().code, ns.error().message);
+            plan.steps.push_back(std::move(*ns));
         }
     }
     for (const Step& st : plan.steps) markTemps(km, st, plan.tempNeeded);

@@ -4,6 +4,7 @@
 #pragma once
 
 #include <cstdint>
+#include <functional>
 #include <string>
 #include <vector>
 
@@ -11,7 +12,7 @@
 
 namespace mlk::hip {
 
-enum class StepKind : uint8_t { Elementwise, Softmax, Gemm, RowSum, ScoreSoftmax, Fail };
+enum class StepKind : uint8_t { Elementwise, Softmax, Gemm, RowSum, ScoreSoftmax, Nest, Fail };
 
 /// One read or write of a buffer over an R-dim box: element (v0..vR-1),
 /// v_d in [0, extent_d), touches buffer[offset + sum coeff[d] * v_d].
@@ -52,6 +53,21 @@ struct Step {
     int64_t batch{0}, seq{0}, dim{0};
     double div{1.0};
 
+    // Nest (generic loop nest, nestgen.cpp): one forest root as a hipRTC
+    // kernel; `nestBufs` maps kernel buffer slots to buffer ids; `threads` is
+    // the padded instance count of the collapsed parallel loops; `checked`
+    // means some access carries a run-time bounds check whose status word is
+    // read back after the launch.
+    uint32_t root{kInvalidId};
+    std::vector<uint32_t> nestBufs;
+    std::vector<uint32_t> nestWrites;
+    int64_t threads{0};
+    int collapsed{0};
+    bool checked{false};
+    bool transcendental{false};
+    bool narrowRoundTrip{false};
+    bool touchesF16{false};
+
     // Fail: the step reports this ABI code at run time (1 = negative store
     // address, as the reference walker's InvalidGraph at execution).
     int failCode{0};
@@ -72,6 +88,28 @@ Result<Plan> planModule(const KernelModule& km);
 
 /// Full hipRTC source of an elementwise step (prelude + template).
 std::string elementwiseSource(const KernelModule& km, const Step& st);
+
+/// The device math header text every hipRTC instance starts with.
+const char* deviceMathHeader();
+
+/// The module as the device holds it: temps in f64, as the reference
+/// executor holds every buffer (kernel_buffers.cpp:852-878).
+KernelModule deviceModule(const KernelModule& km);
+
+/// Generic loop-nest step for one forest root (nestgen.cpp): the root's
+/// subtree as straight-line f64 device code, the outermost parallel loops
+/// collapsed onto threads. The step's `source` holds the hipRTC text.
+Result<Step> planNest(const KernelModule& km, uint32_t root);
+
+/// Hex-float literal of an f64 constant (exact), or the non-finite builtins.
+std::string literal(double v);
+
+/// f64 chain body (kernel_buffers.cpp:106-178 semantics). `elemCode` gives the
+/// device expression of an ElemIdx/ElemA/ElemB operand ("" = unrealizable);
+/// the result is written as `<sink>tN;`.
+Result<std::string> chainCode(const std::vector<KernelExpr>& exprs, bool poly7, bool f32Out,
+                              const std::function<std::string(const KernelOperand&)>& elemCode,
+                              const std::string& sink);
 
 /// Buffer element count as the executors size it (dims product, else
 /// `elements`; dynamic buffers take the run's element count).

@@ -330,3 +330,196 @@ def _softmax_over(km: KernelModule, x: int, y: int, rows: int, cols: int) -> Ker
     view = KernelModule(buffers=list(km.buffers))
     view.nodes = [KernelNode(op="call", math="softmax", a=x, out=y)]
     return view
+
+
+# ------------------------------------------- poly.codegen tiled forms --
+def _stack_coeffs(depth: int, pos: dict, terms: dict) -> List[int]:
+    """Stack-position coefficient vector (codegen.cpp mapCoeffs): `terms` maps
+    a loop name to its coefficient, placed at that loop's stack position."""
+    c = [0] * depth
+    for name, v in terms.items():
+        c[pos[name]] = v
+    return c
+
+
+def _emit_tiled_levels(km: KernelModule, levels: Sequence[tuple], body, tile: int,
+                       depth: int = 0, pos: Optional[dict] = None) -> List[int]:
+    """Tiled band emission following poly codegen's emitLoop/emitPointBody
+    (polyhedral/src/codegen.cpp:296-420): per level a TILE loop over
+    [floor(lo/t), (hi+1)/t - 1] holding a POINT loop with the affine inclusive
+    bounds [t*ti, t*ti + t-1], plus a sibling partial tile whose point loop
+    ends at the constant hi when t does not divide hi+1; the inner levels are
+    replayed under each part. Tile and point loops carry the level's parallel
+    mark, the point loop its vector hint. ``levels`` are (name, lo, hi,
+    parallel, vector); ``body(pos, depth)`` returns the innermost children."""
+    pos = dict(pos or {})
+    if not levels:
+        return body(pos, depth)
+    name, lo, hi, par, vec = levels[0]
+    t = tile
+    first, full_last, last = lo // t, (hi + 1) // t - 1, hi // t
+    parts = []
+    if full_last >= first:
+        parts.append(("full", first, full_last))
+    if (hi + 1) % t != 0:
+        parts.append(("partial", last, last))
+    ids = []
+    for kind, t0, t1 in parts:
+        tile_id = km.add_node(KernelNode(op="loop", var=name + "_t", begin=t0, end=t1 + 1, parallel=par))
+        inner = dict(pos)
+        inner[name] = depth + 1
+        children = _emit_tiled_levels(km, levels[1:], body, tile, depth + 2, inner)
+        bc = [0] * (depth + 1)
+        bc[depth] = t
+        point = KernelNode(op="loop", var=name, begin_coeffs=bc, begin_offset=0, parallel=par,
+                           vector_hint=vec, children=children)
+        if kind == "full":
+            ec = [0] * (depth + 1)
+            ec[depth] = t
+            point.end_coeffs = ec
+            point.end_offset = t - 1
+        else:
+            point.end = hi + 1
+        km.nodes[tile_id].children.append(km.add_node(point))
+        ids.append(tile_id)
+    return ids
+
+
+def lift_1d(km: KernelModule) -> KernelModule:
+    """A Tier-1 1-D chain (Loop{Compute; Store} over ElemA/ElemB) written as
+    the one-level multi-dim nest the polyhedral scop models it as
+    (polyhedral/src/scop.cpp:107-149): each legacy operand becomes an ElemIdx
+    access with coefficient 1 on the loop, the store gets coefficient 1."""
+    root = km.nodes[km.roots()[0]]
+    compute = next(km.nodes[c] for c in root.children if km.nodes[c].op == "compute")
+    store = next(km.nodes[c] for c in root.children if km.nodes[c].op == "store")
+
+    def lift(o: KernelOperand) -> KernelOperand:
+        if o.kind == "elem_a":
+            return elem_idx(compute.a, [1])
+        if o.kind == "elem_b":
+            return elem_idx(compute.b, [1])
+        return o
+
+    out = KernelModule(buffers=list(km.buffers), name=km.name, schedule=dict(km.schedule))
+    c = out.add_node(KernelNode(op="compute", family=compute.family,
+                                exprs=[KernelExpr(e.op, lift(e.a), lift(e.b)) for e in compute.exprs]))
+    st = out.add_node(KernelNode(op="store", out=store.out, out_index_coeffs=[1]))
+    out.add_node(KernelNode(op="loop", var="i", begin=root.begin, end=root.end, children=[c, st]))
+    return out
+
+
+def tiled_elementwise_module(synth: KernelModule, tile: int = 32) -> KernelModule:
+    """A poly.synth broadcast elementwise nest (one perfect nest ending in
+    Compute+Store) re-emitted with every level tiled by ``tile`` and marked
+    parallel, the innermost point loop vector-hinted: the shape poly.codegen
+    gives a dependence-free band."""
+    root = synth.nodes[synth.roots()[0]]
+    dims = []
+    cur = root
+    while True:
+        dims.append(cur.end)
+        ch = [synth.nodes[c] for c in cur.children]
+        if len(ch) == 1 and ch[0].op == "loop":
+            cur = ch[0]
+            continue
+        compute, store = ch
+        break
+    rank = len(dims)
+    names = [f"e{d}" for d in range(rank)]
+    out = KernelModule(buffers=list(synth.buffers), name=synth.name, schedule=dict(synth.schedule))
+
+    def remap(o: KernelOperand, pos, depth) -> KernelOperand:
+        if o.kind != "elem_idx":
+            return o
+        return elem_idx(o.index, _stack_coeffs(depth, pos, {names[d]: c for d, c in enumerate(o.coeffs)
+                                                            if d < rank}), o.offset)
+
+    def body(pos, depth):
+        c = KernelNode(op="compute", family=compute.family, exprs=[
+            KernelExpr(e.op, remap(e.a, pos, depth), remap(e.b, pos, depth)) for e in compute.exprs])
+        s = KernelNode(op="store", out=store.out, accum=store.accum, out_index_offset=store.out_index_offset,
+                       out_index_coeffs=_stack_coeffs(depth, pos, {names[d]: c_ for d, c_ in
+                                                                   enumerate(store.out_index_coeffs)}))
+        return [out.add_node(c), out.add_node(s)]
+
+    levels = [(names[d], 0, dims[d] - 1, True, d == rank - 1) for d in range(rank)]
+    _emit_tiled_levels(out, levels, body, tile)
+    return out
+
+
+def tiled_gemm_module(m: int, k: int, n: int, dtype_in: str = "f32", tile: int = 32,
+                      init: str = "split", out_dtype: str = "f32") -> KernelModule:
+    """The poly.synth GEMM statements (S0: C[i,j] = 0 over (i,j); S1:
+    C[i,j] += A[i,k]*B[k,j] over (i,j,k), poly.synth.cpp:58-147) in the tiled
+    forms poly.codegen can give them, i and j parallel, k sequential. ``init``
+    places S0 as codegen's three strategies do (codegen.cpp:1-30, :440-530):
+    "hoist" emits it before the k band (its k value precedes the loop),
+    "guard" re-enters it in the k loop under the guard k == 0, and "split" cuts
+    the k range at 0 so S0 runs only in the singleton segment [0, 0] of the
+    first k tile, with constant point segments."""
+    km = KernelModule()
+    a = km.add_buffer(KernelBuffer("A", dtype_in, True, False, False, m * k, [m, k]))
+    b = km.add_buffer(KernelBuffer("B", dtype_in, True, False, False, k * n, [k, n]))
+    c = km.add_buffer(KernelBuffer("C", out_dtype, False, True, False, m * n, [m, n]))
+
+    def s0(pos, depth):
+        cp = KernelNode(op="compute", exprs=[KernelExpr("add", const(0.0), const(0.0))])
+        st = KernelNode(op="store", out=c, out_index_coeffs=_stack_coeffs(depth, pos, {"i": n, "j": 1}))
+        return [km.add_node(cp), km.add_node(st)]
+
+    def s1(pos, depth):
+        cp = KernelNode(op="compute", exprs=[
+            KernelExpr("add", elem_idx(a, _stack_coeffs(depth, pos, {"i": k, "k": 1})), const(0.0)),
+            KernelExpr("add", elem_idx(b, _stack_coeffs(depth, pos, {"k": n, "j": 1})), const(0.0)),
+            KernelExpr("mul", temp(0), temp(1))])
+        st = KernelNode(op="store", out=c, accum="add",
+                        out_index_coeffs=_stack_coeffs(depth, pos, {"i": n, "j": 1}))
+        return [km.add_node(cp), km.add_node(st)]
+
+    def k_band(pos, depth):
+        if init == "hoist":
+            return s0(pos, depth) + _emit_tiled_levels(km, [("k", 0, k - 1, False, False)], s1, tile, depth, pos)
+        if init == "guard":
+            def body(p, d):
+                g = KernelNode(op="guard", guard_coeffs=_stack_coeffs(d, p, {"k": 1}), guard_offset=0,
+                               children=s0(p, d))
+                return [km.add_node(g)] + s1(p, d)
+            return _emit_tiled_levels(km, [("k", 0, k - 1, False, False)], body, tile, depth, pos)
+        # split: tile 0 holds the singleton point segment [0,0] with S0 and S1,
+        # then [1, min(t,K)-1] with S1; later tiles as the standard parts.
+        ids = []
+        t0 = km.add_node(KernelNode(op="loop", var="k_t", begin=0, end=1))
+        p = dict(pos)
+        p["k"] = depth + 1
+        seg0 = KernelNode(op="loop", var="k", begin=0, end=1, children=s0(p, depth + 2) + s1(p, depth + 2))
+        km.nodes[t0].children.append(km.add_node(seg0))
+        hi0 = min(tile, k) - 1
+        if hi0 >= 1:
+            seg1 = KernelNode(op="loop", var="k", begin=1, end=hi0 + 1, children=s1(p, depth + 2))
+            km.nodes[t0].children.append(km.add_node(seg1))
+        ids.append(t0)
+        if k > tile:
+            full_last = k // tile - 1
+            if full_last >= 1:
+                tf = km.add_node(KernelNode(op="loop", var="k_t", begin=1, end=full_last + 1))
+                bc = [0] * (depth + 1)
+                bc[depth] = tile
+                ec = list(bc)
+                pt = KernelNode(op="loop", var="k", begin_coeffs=bc, begin_offset=0, end_coeffs=ec,
+                                end_offset=tile - 1, children=s1(p, depth + 2))
+                km.nodes[tf].children.append(km.add_node(pt))
+                ids.append(tf)
+            if k % tile != 0:
+                last = (k - 1) // tile
+                tp = km.add_node(KernelNode(op="loop", var="k_t", begin=last, end=last + 1))
+                bc = [0] * (depth + 1)
+                bc[depth] = tile
+                pt = KernelNode(op="loop", var="k", begin_coeffs=bc, begin_offset=0, end=k,
+                                children=s1(p, depth + 2))
+                km.nodes[tp].children.append(km.add_node(pt))
+                ids.append(tp)
+        return ids
+
+    _emit_tiled_levels(km, [("i", 0, m - 1, True, False), ("j", 0, n - 1, True, True)], k_band, tile)
+    return km

@@ -104,7 +104,7 @@ def run(km, arrays: Dict[int, np.ndarray], scalars: Sequence[float] = (),
         b = km.buffers[bid]
         n = b.elements if b.elements > 0 else int(elements)
         if init is not None and bid in init:
-            outs.append(np.ascontiguousarray(np.asarray(init[bid], dtype=np.float64).reshape(-1)))
+            outs.append(np.array(init[bid], dtype=np.float64).reshape(-1))  # a copy: init is not written
         else:
             outs.append(np.zeros(n, dtype=np.float64))
     execute(km.to_json(), ins, outs, scalars, elements, hw_threads)

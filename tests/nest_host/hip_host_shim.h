@@ -1,0 +1,38 @@
+// Host stand-ins for the HIP names a generated loop-nest kernel uses, so the
+// kernel text compiles as plain C++ for the CPU (under AddressSanitizer) and
+// its grid can be run one thread at a time. Test infrastructure only.
+#pragma once
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#define __HIPCC_RTC__ 1
+#define __device__
+#define __host__
+#define __global__
+#define __forceinline__ inline
+#define __launch_bounds__(...)
+
+struct mlk_dim3 {
+    unsigned x, y, z;
+};
+extern mlk_dim3 blockIdx, threadIdx, gridDim, blockDim;
+
+inline float __uint_as_float(unsigned u) {
+    float f;
+    memcpy(&f, &u, sizeof(f));
+    return f;
+}
+inline unsigned __float_as_uint(float f) {
+    unsigned u;
+    memcpy(&u, &f, sizeof(u));
+    return u;
+}
+/// f64 -> f32 rounded toward zero.
+inline float __double2float_rz(double d) {
+    float f = static_cast<float>(d);
+    if (f != f) return f;
+    if (isinf(f) && !isinf(d)) return nextafterf(f, 0.0f);
+    if ((d >= 0 && static_cast<double>(f) > d) || (d <= 0 && static_cast<double>(f) < d)) f = nextafterf(f, 0.0f);
+    return f;
+}

@@ -70,10 +70,14 @@ def test_tier1_broadcast_module_refused():
     assert "outside its buffer" in ei.value.message
 
 
-def test_unrecognized_nest_refused():
+def test_unrecognized_nest_takes_generic_path():
     km = fx.config3_module(8, 8, tier=2)
-    km.nodes[2].begin_coeffs = [0]          # affine bound: generic path only
+    km.nodes[2].begin_coeffs = [0]          # affine bound: no hand-written class
     km.nodes[2].end_coeffs = [1]
+    cls, policy, steps = be.plan(km)
+    assert (cls, steps) == ("loop-nest", 1)
+    # A loop with a non-unit step has no walker semantics: refused.
+    km.nodes[2].step = 2
     with pytest.raises(be.MlkHipError):
         be.plan(km)
 
@@ -92,9 +96,9 @@ def test_reference_writer_quirks_parse():
     pol = ctypes.create_string_buffer(64)
     n = ctypes.c_int()
     rc = be.lib().mlkhip_plan(text, len(text), cls, 256, pol, 64, ctypes.byref(n))
-    # -1e308 is not -inf: the softmax pattern needs the exact init, so the
-    # module falls through to the general nest check and is refused.
-    assert rc in (0, be.REFUSED)
+    # -1e308 is not -inf: the softmax class needs the exact init, so the
+    # module runs on the generic loop-nest path with the walker's semantics.
+    assert rc == 0 and cls.value.decode() == "loop-nest"
 
 
 @pytest.mark.parametrize("km", [fx.config1_module(1 << 24), fx.config3_module(4096, 4096, 2),

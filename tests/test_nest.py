@@ -1,0 +1,307 @@
+"""The generic loop-nest path (mlk2_amd/csrc/host/nestgen.cpp).
+
+Any multi-dim forest root no hand-written class claims (poly.codegen's tiled,
+guarded and split forms, triangular bounds, recurrences) runs as one generated
+kernel with the reference walker's semantics
+(runtime/src/execution/kernel_buffers.cpp:453-835).
+
+CPU tests compile each generated kernel for the host under AddressSanitizer
+and UndefinedBehaviorSanitizer and run its whole grid one thread at a time, in
+reverse order (``tests/nesthost.py``), against the oracle. That checks every
+address the kernel forms, and the host's parallelization proof, before the
+kernel runs on a GPU. GPU tests run the same modules through the C ABI.
+
+Bar: f64 buffers with IEEE operations are bit-exact with the walker (any NaN
+matches any NaN). f32 outputs of a register-held accumulation equal the
+walker's f64 value rounded once (round to nearest even), so they are
+bit-exact against the oracle's result rounded to f32. Chains with exp use
+the elementwise tolerance of 1e-6 relative.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import nest_fuzz as nf
+import nesthost
+import oracle
+from mlk2_amd import backend
+from mlk2_amd import fixtures as fx
+from mlk2_amd import inputs
+from mlk2_amd.kernel_ir import (KernelBuffer, KernelExpr, KernelModule, KernelNode, const, elem_idx)
+from mlk2_amd.parity import max_rel
+
+
+def say(msg):
+    print(f"[nest] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def gemm_inputs(m, k, n, seed=7):
+    rng = np.random.default_rng(seed)
+    a = rng.uniform(-1, 1, m * k).astype(np.float32).astype(np.float64)
+    b = rng.uniform(-1, 1, k * n).astype(np.float32).astype(np.float64)
+    return a, b
+
+
+def expected(ref: np.ndarray, dtype: str) -> np.ndarray:
+    if dtype == "f32":
+        return ref.astype(np.float32).astype(np.float64)
+    return ref
+
+
+def collapsed(km, step=0) -> int:
+    _, src = backend.compile_check(km, step)
+    line = src.splitlines()[0]
+    return int(line.split(",")[1].split()[0])
+
+
+def neg_store_module() -> KernelModule:
+    """i in [0,4): y[i-2] = x[i]; z[i] = 2*x[i] (two statements: no perfect
+    nest, so the generic path runs it). The walker fails at i = 0."""
+    km = KernelModule()
+    x = km.add_buffer(KernelBuffer("x", "f64", True, False, False, 4, [4]))
+    y = km.add_buffer(KernelBuffer("y", "f64", False, True, False, 4, [4]))
+    z = km.add_buffer(KernelBuffer("z", "f64", False, True, False, 4, [4]))
+    c0 = km.add_node(KernelNode(op="compute", exprs=[KernelExpr("add", elem_idx(x, [1]), const(0.0))]))
+    s0 = km.add_node(KernelNode(op="store", out=y, out_index_coeffs=[1], out_index_offset=-2))
+    c1 = km.add_node(KernelNode(op="compute", exprs=[KernelExpr("mul", elem_idx(x, [1]), const(2.0))]))
+    s1 = km.add_node(KernelNode(op="store", out=z, out_index_coeffs=[1]))
+    km.add_node(KernelNode(op="loop", var="i", begin=0, end=4, children=[c0, s0, c1, s1]))
+    return km
+
+
+def dynamic_end_module(n=8) -> KernelModule:
+    """i in [0, elements): y[i] = x[i] + x[i+1]: the loop end is the run's
+    element count, so the addresses are bounded only at run time."""
+    km = KernelModule()
+    x = km.add_buffer(KernelBuffer("x", "f64", True, False, False, n, [n]))
+    y = km.add_buffer(KernelBuffer("y", "f64", False, True, False, n, [n]))
+    c0 = km.add_node(KernelNode(op="compute", exprs=[KernelExpr("add", elem_idx(x, [1]), elem_idx(x, [1], 1))]))
+    s0 = km.add_node(KernelNode(op="store", out=y, out_index_coeffs=[1]))
+    km.add_node(KernelNode(op="loop", var="i", begin=0, end=-1, children=[c0, s0]))
+    return km
+
+
+def prefix_sum_module(n=300) -> KernelModule:
+    """y[0] = x[0]; i in [1,n): y[i] = y[i-1] + x[i] -- a recurrence: no loop
+    is parallel, the whole root runs in one thread, in order."""
+    km = KernelModule()
+    x = km.add_buffer(KernelBuffer("x", "f64", True, False, False, n, [n]))
+    y = km.add_buffer(KernelBuffer("y", "f64", False, True, False, n, [n]))
+    c0 = km.add_node(KernelNode(op="compute", exprs=[KernelExpr("add", elem_idx(x, [0]), const(0.0))]))
+    s0 = km.add_node(KernelNode(op="store", out=y, out_index_coeffs=[0]))
+    c1 = km.add_node(KernelNode(op="compute", exprs=[KernelExpr("add", elem_idx(y, [0, 1], -1),
+                                                                 elem_idx(x, [0, 1]))]))
+    s1 = km.add_node(KernelNode(op="store", out=y, out_index_coeffs=[0, 1]))
+    l1 = km.add_node(KernelNode(op="loop", var="i", begin=1, end=n, children=[c1, s1]))
+    km.add_node(KernelNode(op="loop", var="z", begin=0, end=1, children=[c0, s0, l1]))
+    return km
+
+
+def triangular_module(n=37) -> KernelModule:
+    """i in [0,n): { y[i] = 0; j in [0, i]: y[i] += L[i,j] * x[j];
+    guard j == i: d[i] = L[i,i] } -- lower-triangular product."""
+    km = KernelModule()
+    L = km.add_buffer(KernelBuffer("L", "f64", True, False, False, n * n, [n, n]))
+    x = km.add_buffer(KernelBuffer("x", "f64", True, False, False, n, [n]))
+    y = km.add_buffer(KernelBuffer("y", "f64", False, True, False, n, [n]))
+    d = km.add_buffer(KernelBuffer("d", "f64", False, True, False, n, [n]))
+    c0 = km.add_node(KernelNode(op="compute", exprs=[KernelExpr("add", const(0.0), const(0.0))]))
+    s0 = km.add_node(KernelNode(op="store", out=y, out_index_coeffs=[1]))
+    c1 = km.add_node(KernelNode(op="compute", exprs=[KernelExpr("mul", elem_idx(L, [n, 1]), elem_idx(x, [0, 1]))]))
+    s1 = km.add_node(KernelNode(op="store", out=y, out_index_coeffs=[1, 0], accum="add"))
+    c2 = km.add_node(KernelNode(op="compute", exprs=[KernelExpr("add", elem_idx(L, [n, 1]), const(0.0))]))
+    s2 = km.add_node(KernelNode(op="store", out=d, out_index_coeffs=[1, 0]))
+    g = km.add_node(KernelNode(op="guard", guard_coeffs=[1, -1], guard_offset=0, children=[c2, s2]))
+    lj = km.add_node(KernelNode(op="loop", var="j", begin=0, end=-1, begin_coeffs=[0], begin_offset=0,
+                                end_coeffs=[1], end_offset=0, children=[c1, s1, g]))
+    km.add_node(KernelNode(op="loop", var="i", begin=0, end=n, children=[c0, s0, lj]))
+    return km
+
+
+def host_vs_oracle(km, arrays, scalars=(), elements=0):
+    st, cur = nesthost.run_module(km, arrays, scalars, elements, reverse=True)
+    ref = oracle.run(km, {i: arrays[i] for i in km.input_ids()}, scalars, elements,
+                     init={i: arrays[i] for i in km.output_ids() if i in arrays})
+    return st, cur, ref
+
+
+# ---------------------------------------------------------------- CPU ----
+@pytest.mark.parametrize("init", ["hoist", "guard", "split"])
+@pytest.mark.parametrize("dtype", ["f64", "f32"])
+def test_tiled_gemm_host(init, dtype):
+    m, k, n = 70, 45, 37
+    km = fx.tiled_gemm_module(m, k, n, dtype, tile=16, init=init, out_dtype=dtype)
+    cls, pol, _ = backend.plan(km)
+    assert set(cls.split("+")) == {"loop-nest"} and pol == "bitexact-rne-gfx950-v1"
+    a, b = gemm_inputs(m, k, n)
+    st, cur, ref = host_vs_oracle(km, {0: a, 1: b, 2: np.full(m * n, 7.0)})
+    assert st == 0
+    assert nf.same_bits(cur[2], expected(ref[2], dtype))
+
+
+def test_tiled_gemm_collapses_all_parallel_levels():
+    # Divisible sizes: one full tile part per level, i_t/i/j_t/j collapse.
+    km = fx.tiled_gemm_module(64, 32, 64, "f32", tile=16, init="split")
+    assert collapsed(km) == 4
+    _, src = backend.compile_check(km)
+    assert "double r0 = " in src  # C[i,j] held in an f64 register over the k band
+
+
+def test_tiled_elementwise_host():
+    km = fx.tiled_elementwise_module(fx.config3_module(37, 100, tier=2), tile=32)
+    d = inputs.config_inputs("c3", {"rows": 37, "cols": 100})
+    st, cur, ref = host_vs_oracle(km, {0: d["x"], 1: d["b"]})
+    assert st == 0
+    assert max_rel(cur[2], ref[2]) <= 1e-6
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_fuzz_host(seed):
+    km = nf.random_module(seed)
+    cls, _, _ = backend.plan(km)
+    if any(c not in ("loop-nest", "empty") for c in cls.split("+")):
+        pytest.skip(f"plan {cls} includes a template class the host harness does not run")
+    arrays, scalars = nf.random_inputs(km, seed)
+    st, cur, ref = host_vs_oracle(km, arrays, scalars)
+    assert st == 0
+    for i in km.output_ids():
+        assert nf.same_bits(cur[i], ref[i]), (seed, i)
+
+
+def test_recurrence_runs_serially_host():
+    km = prefix_sum_module()
+    assert collapsed(km) == 0
+    x = np.arange(300, dtype=np.float64) * 0.5 - 20
+    st, cur, ref = host_vs_oracle(km, {0: x})
+    assert st == 0 and nf.same_bits(cur[1], ref[1])
+
+
+def test_triangular_and_guard_host():
+    km = triangular_module()
+    assert collapsed(km) == 1  # i proven parallel: y[i], d[i] move with i only
+    rng = np.random.default_rng(3)
+    arrays = {0: rng.uniform(-1, 1, 37 * 37), 1: rng.uniform(-1, 1, 37)}
+    st, cur, ref = host_vs_oracle(km, arrays)
+    assert st == 0 and nf.same_bits(cur[2], ref[2]) and nf.same_bits(cur[3], ref[3])
+
+
+def test_negative_store_reports_status_host():
+    km = neg_store_module()
+    assert backend.plan(km)[0] == "loop-nest"
+    st, _ = nesthost.run_module(km, {0: np.arange(4.0)})
+    assert st == 1
+    with pytest.raises(oracle.OracleError):
+        oracle.run(km, {0: np.arange(4.0)})
+
+
+def test_dynamic_end_bounds_checked_host():
+    km = dynamic_end_module()
+    x = np.arange(8.0)
+    st, cur, ref = host_vs_oracle(km, {0: x}, elements=7)
+    assert st == 0 and nf.same_bits(cur[1], ref[1])
+    # elements past the buffers: every out-of-range access is caught by the
+    # kernel's own checks (AddressSanitizer sees none) and reported as 6.
+    st, _ = nesthost.run_module(km, {0: x}, elements=12)
+    assert st == 6
+
+
+def test_nest_refusals():
+    # A Call inside a loop nest has no walker semantics the kernel can mirror.
+    km = KernelModule()
+    a = km.add_buffer(KernelBuffer("A", "f32", True, False, False, 4, [2, 2]))
+    y = km.add_buffer(KernelBuffer("Y", "f32", False, True, False, 4, [2, 2]))
+    call = km.add_node(KernelNode(op="call", math="softmax", a=a, out=y))
+    c = km.add_node(KernelNode(op="compute", exprs=[KernelExpr("add", elem_idx(a, [1]), const(0.0))]))
+    s = km.add_node(KernelNode(op="store", out=y, out_index_coeffs=[1]))
+    km.add_node(KernelNode(op="loop", var="i", begin=0, end=2, children=[call, c, s]))
+    with pytest.raises(backend.MlkHipError):
+        backend.plan(km)
+
+
+# ---------------------------------------------------------------- GPU ----
+@pytest.mark.gpu
+@pytest.mark.parametrize("init", ["hoist", "guard", "split"])
+@pytest.mark.parametrize("shape", [(70, 45, 37, 16), (256, 160, 192, 32)])
+def test_tiled_gemm_gpu(hip, init, shape):
+    m, k, n, t = shape
+    say(f"tiled gemm {init} {m}x{k}x{n} tile {t}")
+    for dtype in ("f64", "f32"):
+        km = fx.tiled_gemm_module(m, k, n, dtype, tile=t, init=init, out_dtype=dtype)
+        a, b = gemm_inputs(m, k, n)
+        c0 = np.full(m * n, 7.0)
+        art = hip.build(km)
+        got = art.run({0: a, 1: b, 2: c0})[2]
+        ref = oracle.run(km, {0: a, 1: b}, init={2: c0})[2]
+        assert nf.same_bits(got, expected(ref, dtype)), dtype
+
+
+@pytest.mark.gpu
+def test_tiled_c1_gpu(hip):
+    say("tiled 1-D sin chain (poly7), 2^20")
+    n = 1 << 20
+    km = fx.tiled_elementwise_module(fx.lift_1d(fx.config1_module(n=n)), tile=32)
+    x = inputs.config_inputs("c1", {"n": n})["x"]
+    art = hip.build(km)
+    assert art.class_name == "loop-nest"
+    got = art.run({0: x})[1]
+    ref = oracle.run(km, {0: x})[1]
+    # Exact f64 poly7, one rounding to f32.
+    assert nf.same_bits(got, expected(ref, "f32"))
+
+
+@pytest.mark.gpu
+def test_tiled_c3_gpu(hip):
+    say("tiled broadcast exp chain 4096x4096")
+    km = fx.tiled_elementwise_module(fx.config3_module(4096, 4096, tier=2), tile=32)
+    d = inputs.config_inputs("c3")
+    art = hip.build(km)
+    got = art.run({0: d["x"], 1: d["b"]})[2]
+    ref = oracle.run(km, {0: d["x"], 1: d["b"]})[2]
+    r = max_rel(got, ref)
+    say(f"tiled c3 max_rel={r:.3e}")
+    assert r <= 1e-6
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(60))
+def test_fuzz_gpu(hip, seed):
+    km = nf.random_module(seed)
+    say(f"fuzz seed {seed}: {backend.plan(km)[0]}")
+    arrays, scalars = nf.random_inputs(km, seed)
+    got = hip.build(km).run(arrays, scalars)
+    ref = oracle.run(km, {i: arrays[i] for i in km.input_ids()}, scalars,
+                     init={i: arrays[i] for i in km.output_ids()})
+    for i in km.output_ids():
+        assert nf.same_bits(got[i], ref[i]), (seed, i)
+
+
+@pytest.mark.gpu
+def test_serial_triangular_gpu(hip):
+    say("recurrence + triangular/guard nests")
+    km = prefix_sum_module()
+    x = np.arange(300, dtype=np.float64) * 0.5 - 20
+    assert nf.same_bits(hip.build(km).run({0: x})[1], oracle.run(km, {0: x})[1])
+    km = triangular_module()
+    rng = np.random.default_rng(3)
+    arrays = {0: rng.uniform(-1, 1, 37 * 37), 1: rng.uniform(-1, 1, 37)}
+    got = hip.build(km).run(arrays)
+    ref = oracle.run(km, arrays)
+    assert nf.same_bits(got[2], ref[2]) and nf.same_bits(got[3], ref[3])
+
+
+@pytest.mark.gpu
+def test_error_status_gpu(hip):
+    say("nest run-time checks: negative store, dynamic end past the buffers")
+    art = hip.build(neg_store_module())
+    with pytest.raises(backend.MlkHipError) as e:
+        art.run({0: np.arange(4.0)})
+    assert e.value.code == 1
+    art = hip.build(dynamic_end_module())
+    x = np.arange(8.0)
+    got = art.run({0: x}, elements=7)[1]
+    assert nf.same_bits(got, oracle.run(dynamic_end_module(), {0: x}, elements=7)[1])
+    with pytest.raises(backend.MlkHipError) as e:
+        art.run({0: x}, elements=12)
+    assert e.value.code == 6
