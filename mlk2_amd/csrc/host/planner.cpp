@@ -868,8 +868,19 @@ int64_t bufferElements(const KernelBuffer& b, int64_t dynamicElements) {
     return dynamicElements;
 }
 
-Result<Plan> planModule(const KernelModule& km) {
+Result<Plan> planModule(const KernelModule& input) {
+    // Multi-dim forests are recognized in canonical form (tiled, split and
+    // guarded bands folded back to their untiled shapes, canonical.cpp).
+    // Two schedule parameters select the path for tests and variant search:
+    // "hip_canonical" = 0 plans the module as written, "hip_generic" = 1 runs
+    // every multi-dim root on the generic loop-nest kernel.
+    const bool multiDim = isMultiDimModule(input);
+    const bool canon = input.param("hip_canonical", 1) != 0;
+    const bool genericOnly = input.param("hip_generic", 0) != 0;
+    int rewrites = 0;
+    const KernelModule km = multiDim && canon ? canonicalModule(input, &rewrites) : input;
     Plan plan;
+    plan.canonicalized = rewrites != 0;
     plan.tempNeeded.assign(km.buffers.size(), false);
     if (km.nodes.empty()) return err(ErrorCode::InvalidGraph, "kernel module has no nodes");
     for (const KernelBuffer& b : km.buffers) {
@@ -877,7 +888,7 @@ Result<Plan> planModule(const KernelModule& km) {
             return err(ErrorCode::UnsupportedCapability, "buffer dtype outside f16/f32/f64: " + b.name);
         }
     }
-    plan.multiDim = isMultiDimModule(km);
+    plan.multiDim = multiDim;
     if (!plan.multiDim) {
         for (const KernelNode& top : km.nodes) {
             if (top.op == KernelOp::Loop) {
@@ -908,6 +919,12 @@ Result<Plan> planModule(const KernelModule& km) {
                     plan.steps.push_back(std::move(*ns));
                 }
                 continue;  // Compute/Store/etc. at root carry no semantics for the walker
+            }
+            if (genericOnly) {
+                auto ns = planNest(km, roots[i]);
+                if (!ns.has_value()) return err(ns.error().code, ns.error().message);
+                plan.steps.push_back(std::move(*ns));
+                continue;
             }
             if (matchScoreSoftmax(km, roots, i, st)) {
                 plan.steps.push_back(std::move(st));

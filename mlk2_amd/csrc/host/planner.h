@@ -77,6 +77,7 @@ struct Plan {
     std::string className;            // joined step classes
     std::string policy;               // tolerance policy id
     bool multiDim{false};
+    bool canonicalized{false};        // planned on canonicalModule's rewrite
     std::vector<Step> steps;
     std::vector<bool> tempNeeded;     // per buffer id: device scratch needed
 };
@@ -95,6 +96,12 @@ const char* deviceMathHeader();
 /// The module as the device holds it: temps in f64, as the reference
 /// executor holds every buffer (kernel_buffers.cpp:852-878).
 KernelModule deviceModule(const KernelModule& km);
+
+/// Canonical form of a multi-dim module (canonical.cpp): poly.codegen's
+/// strip-mined, split and guarded bands rewritten to their untiled loop
+/// forms where the rewrite keeps the walker's order exactly. `rewrites` is
+/// set to 1 when anything changed. Buffers are unchanged.
+KernelModule canonicalModule(const KernelModule& km, int* rewrites);
 
 /// Generic loop-nest step for one forest root (nestgen.cpp): the root's
 /// subtree as straight-line f64 device code, the outermost parallel loops

@@ -176,3 +176,104 @@ def same_bits(a: np.ndarray, b: np.ndarray) -> bool:
     if not np.array_equal(na, nb):
         return False
     return np.array_equal(a[~na].view(np.uint64), b[~nb].view(np.uint64))
+
+
+def _insert_position(km: KernelModule, nid: int, p: int) -> None:
+    """Shifts stack positions >= p of every affine form in the subtree up by
+    one (a new loop level at position p encloses it)."""
+    n = km.nodes[nid]
+
+    def ins(c):
+        return c[:p] + [0] + c[p:] if len(c) > p else c
+
+    if n.begin_coeffs or n.end_coeffs:
+        if n.begin_coeffs:
+            n.begin_coeffs = ins(n.begin_coeffs)
+        if n.end_coeffs:
+            n.end_coeffs = ins(n.end_coeffs)
+    if n.out_index_coeffs:
+        n.out_index_coeffs = ins(n.out_index_coeffs)
+    if n.guard_coeffs:
+        n.guard_coeffs = ins(n.guard_coeffs)
+    for e in n.exprs:
+        for o in (e.a, e.b):
+            if o.kind == "elem_idx" and o.coeffs:
+                o.coeffs = ins(o.coeffs)
+    for c in n.children:
+        _insert_position(km, c, p)
+
+
+def _copy_subtree(km: KernelModule, nid: int) -> int:
+    import copy
+    n = copy.deepcopy(km.nodes[nid])
+    n.children = [_copy_subtree(km, c) for c in n.children]
+    return km.add_node(n)
+
+
+def _tile(km: KernelModule, nid: int, depth: int, t: int) -> List[int]:
+    """Replaces loop `nid` (stack position `depth`, constant bounds, begin a
+    multiple of t) by poly codegen's tile parts; returns the new node ids."""
+    n = km.nodes[nid]
+    lo, hi = n.begin, n.end - 1
+    first, full_last, last = lo // t, (hi + 1) // t - 1, hi // t
+    parts = []
+    if full_last >= first:
+        parts.append(("full", first, full_last))
+    if (hi + 1) % t != 0:
+        parts.append(("partial", last, last))
+    out = []
+    for kind, t0, t1 in parts:
+        kids = [_copy_subtree(km, c) for c in n.children]
+        for c in kids:
+            _insert_position(km, c, depth)
+        bc = [0] * (depth + 1)
+        bc[depth] = t
+        point = KernelNode(op="loop", var=(n.var or "v"), begin_coeffs=bc, begin_offset=0, children=kids)
+        if kind == "full":
+            point.end_coeffs, point.end_offset = list(bc), t - 1
+        else:
+            point.end = hi + 1
+        pid = km.add_node(point)
+        out.append(km.add_node(KernelNode(op="loop", var=(n.var or "v") + "_t", begin=t0, end=t1 + 1,
+                                          children=[pid])))
+    return out
+
+
+def tiled_random_module(seed: int) -> KernelModule:
+    """random_module(seed) with some constant-bound loops strip-mined the way
+    poly codegen tiles a band (full tiles with affine point bounds, a partial
+    tile with a constant end), nested tiles included."""
+    km = random_module(seed)
+    rng = np.random.default_rng(seed + 7)
+
+    def visit(ids: List[int], depth: int) -> List[int]:
+        out = []
+        for nid in ids:
+            n = km.nodes[nid]
+            if n.op == "loop":
+                n.children = visit(n.children, depth + 1)
+                const = not n.begin_coeffs and not n.end_coeffs and n.end >= 0
+                if const and n.end - n.begin >= 2 and rng.random() < 0.6:
+                    t = int(rng.choice([1, 2, 3]))
+                    if n.begin % t == 0:
+                        out.extend(_tile(km, nid, depth, t))
+                        continue
+            elif n.op == "guard":
+                n.children = visit(n.children, depth)
+            out.append(nid)
+        return out
+
+    roots = km.roots()
+    new_roots = visit(roots, 0)
+    # Rebuild so the roots run in their original order.
+    out = KernelModule(buffers=km.buffers, name=km.name, schedule=dict(km.schedule))
+
+    def emit(nid: int) -> int:
+        import copy
+        n = copy.deepcopy(km.nodes[nid])
+        n.children = [emit(c) for c in n.children]
+        return out.add_node(n)
+
+    for r in new_roots:
+        emit(r)
+    return out

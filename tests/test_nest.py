@@ -50,6 +50,18 @@ def expected(ref: np.ndarray, dtype: str) -> np.ndarray:
     return ref
 
 
+def generic(km, canonical: bool = True):
+    """The module with the schedule parameters that select the generic
+    loop-nest kernel for every root (and, with canonical=False, plan the
+    module as written, without the canonical rewrite)."""
+    out = fx.KernelModule(buffers=list(km.buffers), nodes=list(km.nodes), name=km.name,
+                          schedule=dict(km.schedule))
+    out.schedule["hip_generic"] = 1
+    if not canonical:
+        out.schedule["hip_canonical"] = 0
+    return out
+
+
 def collapsed(km, step=0) -> int:
     _, src = backend.compile_check(km, step)
     line = src.splitlines()[0]
@@ -130,44 +142,82 @@ def host_vs_oracle(km, arrays, scalars=(), elements=0):
 # ---------------------------------------------------------------- CPU ----
 @pytest.mark.parametrize("init", ["hoist", "guard", "split"])
 @pytest.mark.parametrize("dtype", ["f64", "f32"])
-def test_tiled_gemm_host(init, dtype):
+@pytest.mark.parametrize("canonical", [False, True])
+def test_tiled_gemm_generic_host(init, dtype, canonical):
+    # canonical=False: the tiled form itself on the generic kernel;
+    # canonical=True: its canonical rewrite on the generic kernel (checks
+    # that the rewrite keeps the walker's order: bit-exact in f64).
     m, k, n = 70, 45, 37
     km = fx.tiled_gemm_module(m, k, n, dtype, tile=16, init=init, out_dtype=dtype)
-    cls, pol, _ = backend.plan(km)
+    g = generic(km, canonical)
+    cls, pol, _ = backend.plan(g)
     assert set(cls.split("+")) == {"loop-nest"} and pol == "bitexact-rne-gfx950-v1"
     a, b = gemm_inputs(m, k, n)
-    st, cur, ref = host_vs_oracle(km, {0: a, 1: b, 2: np.full(m * n, 7.0)})
+    st, cur, ref = host_vs_oracle(g, {0: a, 1: b, 2: np.full(m * n, 7.0)})
     assert st == 0
     assert nf.same_bits(cur[2], expected(ref[2], dtype))
 
 
+@pytest.mark.parametrize("init", ["hoist", "guard", "split"])
+@pytest.mark.parametrize("shape", [(70, 45, 37, 16), (64, 32, 64, 16), (256, 160, 192, 32)])
+def test_tiled_gemm_canonicalizes_to_gemm_class(init, shape):
+    m, k, n, t = shape
+    km = fx.tiled_gemm_module(m, k, n, "f32", tile=t, init=init)
+    assert backend.plan(km) == ("gemm-nest", "tol-rel1e-5sqrtk-gfx950-v1", 1)
+    km16 = fx.tiled_gemm_module(m, k, n, "f16", tile=t, init=init)
+    assert backend.plan(km16)[0] == "gemm-nest"
+
+
+def test_tiled_elementwise_canonicalizes_to_template_class():
+    km = fx.tiled_elementwise_module(fx.config3_module(37, 100, tier=2), tile=32)
+    assert backend.plan(km)[0] == "elementwise-nd"
+    km = fx.tiled_elementwise_module(fx.lift_1d(fx.config1_module(n=1 << 20)), tile=32)
+    assert backend.plan(km)[:2] == ("elementwise-nd", "tol-4ulp-f32-gfx950-v1")
+
+
 def test_tiled_gemm_collapses_all_parallel_levels():
     # Divisible sizes: one full tile part per level, i_t/i/j_t/j collapse.
-    km = fx.tiled_gemm_module(64, 32, 64, "f32", tile=16, init="split")
+    km = generic(fx.tiled_gemm_module(64, 32, 64, "f32", tile=16, init="split"), canonical=False)
     assert collapsed(km) == 4
     _, src = backend.compile_check(km)
     assert "double r0 = " in src  # C[i,j] held in an f64 register over the k band
 
 
-def test_tiled_elementwise_host():
-    km = fx.tiled_elementwise_module(fx.config3_module(37, 100, tier=2), tile=32)
+@pytest.mark.parametrize("canonical", [False, True])
+def test_tiled_elementwise_generic_host(canonical):
+    km = generic(fx.tiled_elementwise_module(fx.config3_module(37, 100, tier=2), tile=32), canonical)
     d = inputs.config_inputs("c3", {"rows": 37, "cols": 100})
     st, cur, ref = host_vs_oracle(km, {0: d["x"], 1: d["b"]})
     assert st == 0
     assert max_rel(cur[2], ref[2]) <= 1e-6
 
 
+@pytest.mark.parametrize("canonical", [False, True])
 @pytest.mark.parametrize("seed", range(24))
-def test_fuzz_host(seed):
-    km = nf.random_module(seed)
-    cls, _, _ = backend.plan(km)
-    if any(c not in ("loop-nest", "empty") for c in cls.split("+")):
-        pytest.skip(f"plan {cls} includes a template class the host harness does not run")
+def test_fuzz_host(seed, canonical):
+    km = generic(nf.random_module(seed), canonical)
     arrays, scalars = nf.random_inputs(km, seed)
     st, cur, ref = host_vs_oracle(km, arrays, scalars)
     assert st == 0
     for i in km.output_ids():
         assert nf.same_bits(cur[i], ref[i]), (seed, i)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_tiled_fuzz_canonical_host(seed):
+    # A random forest and the same forest strip-mined as poly codegen tiles
+    # bands: the walker gives the same bits for both, the canonical rewrite
+    # of the tiled form runs bit-exact on the generic kernel, and in most
+    # seeds the canonical form plans to the untiled form's classes.
+    km0 = nf.random_module(seed)
+    km = nf.tiled_random_module(seed)
+    arrays, scalars = nf.random_inputs(km0, seed)
+    r0 = oracle.run(km0, {i: arrays[i] for i in km0.input_ids()}, scalars,
+                    init={i: arrays[i] for i in km0.output_ids()})
+    st, cur, ref = host_vs_oracle(generic(km, True), arrays, scalars)
+    assert st == 0
+    for i in km.output_ids():
+        assert nf.same_bits(ref[i], r0[i]) and nf.same_bits(cur[i], ref[i]), (seed, i)
 
 
 def test_recurrence_runs_serially_host():
@@ -227,14 +277,23 @@ def test_nest_refusals():
 def test_tiled_gemm_gpu(hip, init, shape):
     m, k, n, t = shape
     say(f"tiled gemm {init} {m}x{k}x{n} tile {t}")
+    a, b = gemm_inputs(m, k, n)
+    c0 = np.full(m * n, 7.0)
     for dtype in ("f64", "f32"):
         km = fx.tiled_gemm_module(m, k, n, dtype, tile=t, init=init, out_dtype=dtype)
-        a, b = gemm_inputs(m, k, n)
-        c0 = np.full(m * n, 7.0)
-        art = hip.build(km)
-        got = art.run({0: a, 1: b, 2: c0})[2]
         ref = oracle.run(km, {0: a, 1: b}, init={2: c0})[2]
-        assert nf.same_bits(got, expected(ref, dtype)), dtype
+        # The generic kernel on the tiled form and on its canonical rewrite:
+        # the walker's f64 sums, bit-exact (f32: rounded once).
+        for canonical in (False, True):
+            got = hip.build(generic(km, canonical)).run({0: a, 1: b, 2: c0})[2]
+            assert nf.same_bits(got, expected(ref, dtype)), (dtype, canonical)
+        # As planned: the canonical form on the GEMM class.
+        art = hip.build(km)
+        assert art.class_name == "gemm-nest"
+        got = art.run({0: a, 1: b, 2: c0})[2]
+        r = max_rel(got, ref)
+        say(f"  {dtype} gemm-nest max_rel={r:.3e}")
+        assert r <= 1e-5 * np.sqrt(k)
 
 
 @pytest.mark.gpu
@@ -243,12 +302,15 @@ def test_tiled_c1_gpu(hip):
     n = 1 << 20
     km = fx.tiled_elementwise_module(fx.lift_1d(fx.config1_module(n=n)), tile=32)
     x = inputs.config_inputs("c1", {"n": n})["x"]
-    art = hip.build(km)
-    assert art.class_name == "loop-nest"
-    got = art.run({0: x})[1]
     ref = oracle.run(km, {0: x})[1]
-    # Exact f64 poly7, one rounding to f32.
+    # Generic kernel: exact f64 poly7, one rounding to f32.
+    got = hip.build(generic(km, canonical=False)).run({0: x})[1]
     assert nf.same_bits(got, expected(ref, "f32"))
+    # As planned: the elementwise template (split-precision sin, <= 4 ULP).
+    from mlk2_amd.parity import ulp_distance_f32
+    art = hip.build(km)
+    assert art.class_name == "elementwise-nd"
+    assert ulp_distance_f32(art.run({0: x})[1].astype(np.float32), ref).max() <= 4.0
 
 
 @pytest.mark.gpu
@@ -256,12 +318,13 @@ def test_tiled_c3_gpu(hip):
     say("tiled broadcast exp chain 4096x4096")
     km = fx.tiled_elementwise_module(fx.config3_module(4096, 4096, tier=2), tile=32)
     d = inputs.config_inputs("c3")
-    art = hip.build(km)
-    got = art.run({0: d["x"], 1: d["b"]})[2]
     ref = oracle.run(km, {0: d["x"], 1: d["b"]})[2]
-    r = max_rel(got, ref)
-    say(f"tiled c3 max_rel={r:.3e}")
-    assert r <= 1e-6
+    for mod in (km, generic(km, canonical=False)):
+        art = hip.build(mod)
+        got = art.run({0: d["x"], 1: d["b"]})[2]
+        r = max_rel(got, ref)
+        say(f"tiled c3 {art.class_name} max_rel={r:.3e}")
+        assert r <= 1e-6
 
 
 @pytest.mark.gpu
@@ -270,9 +333,23 @@ def test_fuzz_gpu(hip, seed):
     km = nf.random_module(seed)
     say(f"fuzz seed {seed}: {backend.plan(km)[0]}")
     arrays, scalars = nf.random_inputs(km, seed)
-    got = hip.build(km).run(arrays, scalars)
     ref = oracle.run(km, {i: arrays[i] for i in km.input_ids()}, scalars,
                      init={i: arrays[i] for i in km.output_ids()})
+    for mod in (km, generic(km, canonical=False)):
+        got = hip.build(mod).run(arrays, scalars)
+        for i in km.output_ids():
+            assert nf.same_bits(got[i], ref[i]), (seed, i)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(24))
+def test_tiled_fuzz_gpu(hip, seed):
+    km = nf.tiled_random_module(seed)
+    say(f"tiled fuzz seed {seed}: {backend.plan(km)[0]}")
+    arrays, scalars = nf.random_inputs(km, seed)
+    ref = oracle.run(km, {i: arrays[i] for i in km.input_ids()}, scalars,
+                     init={i: arrays[i] for i in km.output_ids()})
+    got = hip.build(km).run(arrays, scalars)
     for i in km.output_ids():
         assert nf.same_bits(got[i], ref[i]), (seed, i)
 
