@@ -147,6 +147,88 @@ def cpu_baseline_softmax() -> dict:
             "host": platform.processor() or platform.machine(), "nproc": os.cpu_count()}
 
 
+def _time_cpu(fn, budget_s: float = 3.0, max_reps: int = 10):
+    fn()  # warm
+    reps = []
+    end = time.perf_counter() + budget_s
+    while time.perf_counter() < end and len(reps) < max_reps:
+        t0 = time.perf_counter()
+        fn()
+        reps.append(time.perf_counter() - t0)
+    return float(np.median(reps)), len(reps)
+
+
+def cpu_baseline_config(name: str) -> dict:
+    """The oracle's restatement of the reference CPU path for one config, on a
+    bounded sample, timed on this host: the Tier-1 1-D path and Call(MatMul)
+    with the executor's default thread count min(hardware threads, 4)
+    (kernel_buffers.cpp:183-199) and once with the module's "threads"
+    parameter at the host's thread count; the serial walker for the nests."""
+    import oracle
+    from mlk2_amd import fixtures as fx
+    from mlk2_amd import inputs
+    nproc = os.cpu_count() or 1
+    default_threads = min(nproc, 4)
+    out = {"kind": "port", "nproc": nproc}
+
+    def run(km, ins, outs, threads):
+        text = km.to_json()
+        return lambda: oracle.execute(text, ins, outs, (), 0, threads)
+
+    if name == "c1":
+        n = 1 << 22
+        x = inputs.uniform(inputs.SEEDS["c1_x"], n, -4.0, 4.0, "f32").astype(np.float64)
+        km = fx.config1_module(n=n)
+        y = np.zeros(n)
+        med, reps = _time_cpu(run(km, [x], [y], default_threads))
+        km.schedule["threads"] = nproc
+        med_all, _ = _time_cpu(run(km, [x], [y], nproc))
+        work, unit, scale = 8 * n, "GB/s", 1e9
+        sample = f"1-D path (poly7) over 2^22 of the 2^24 elements"
+    elif name == "c3":
+        rows, cols = 256, 4096
+        d = inputs.config_inputs("c3", {"rows": rows, "cols": cols})
+        km = fx.config3_module(rows, cols, tier=2)
+        y = np.zeros(rows * cols)
+        med, reps = _time_cpu(run(km, [d["x"].astype(np.float64), d["b"].astype(np.float64)], [y], default_threads))
+        med_all = None
+        default_threads = 1
+        work, unit, scale = 8 * rows * cols + 4 * cols, "GB/s", 1e9
+        sample = f"Tier-2 walker (serial: the synthesized nest carries no parallel marks), {rows} of 4096 rows"
+    elif name in ("c4a", "c4b"):
+        m, k, n = (1024, 1024, 1024) if name == "c4a" else (256, 4096, 4096)
+        dt = "f32" if name == "c4a" else "f16"
+        rng = np.random.default_rng(5)
+        a = rng.uniform(-1, 1, m * k).astype(np.float16 if dt == "f16" else np.float32).astype(np.float64)
+        b = rng.uniform(-1, 1, k * n).astype(np.float16 if dt == "f16" else np.float32).astype(np.float64)
+        km = fx.config4_module(m, k, n, dt, tier=1)
+        c = np.zeros(m * n)
+        med, reps = _time_cpu(run(km, [a, b], [c], default_threads), budget_s=4.0, max_reps=5)
+        km.schedule["threads"] = nproc
+        med_all, _ = _time_cpu(run(km, [a, b], [c], nproc), budget_s=4.0, max_reps=5)
+        work, unit, scale = 2 * m * n * k, "TFLOP/s", 1e12
+        sample = (f"Call(MatMul) blocked 64/64/32 (f64), {m}x{k}x{n}"
+                  + ("" if name == "c4a" else " (256 of the 4096 rows)"))
+    elif name == "c5":
+        b_, s_, d_ = 1, 512, 128
+        d = inputs.config_inputs("c5", {"batch": b_, "seq": s_, "dim": d_})
+        km = fx.score_softmax_module(b_, s_, d_)
+        y = np.zeros(b_ * s_ * s_)
+        med, reps = _time_cpu(run(km, [d["Q"].astype(np.float64), d["K"].astype(np.float64),
+                                       d["bias"].astype(np.float64)], [y], default_threads))
+        med_all = None
+        default_threads = 1
+        work, unit, scale = 2 * b_ * s_ * d_ * 2 + 4 * s_ + 4 * b_ * s_ * s_, "GB/s", 1e9
+        sample = "walker over the composed module (serial), 1 batch x 512 x 512 x 128"
+    else:
+        return {}
+    out.update({"value": round(work / med / scale, 4), "unit": unit, "cores": default_threads,
+                "sample": f"{sample}; median of {reps} ({med * 1e3:.1f} ms)"})
+    if med_all is not None:
+        out["value_threads_nproc"] = round(work / med_all / scale, 4)
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -200,6 +282,8 @@ def main() -> int:
     for name in names:
         try:
             configs[name] = bench_config(be, name, max(10, args.steps // 2), 5)
+            if not args.no_cpu:
+                configs[name]["cpu_baseline"] = cpu_baseline_config(name)
         except Exception as e:  # a config failing must not hide the headline line
             configs[name] = {"error": str(e)}
 
