@@ -75,7 +75,12 @@ int mlkd_launch_gemm(const mlkd_gemm* p, void* stream);
 /// Variant-space hook for the f16 GEMM (0: 8 waves x 128x64, 1: 4 waves x 128x128).
 void mlkd_gemm_set_variant(int variant);
 int mlkd_launch_score_softmax(const mlkd_score_softmax* p, void* stream);
-/// Variant-space hook for score-softmax (0: fused single pass, 1: two phase).
+/// Scratch bytes the two-pass score-softmax form needs for `p`'s shape (0 when
+/// that form does not apply).
+int64_t mlkd_score_scratch_bytes(const mlkd_score_softmax* p);
+/// Variant-space hook for score-softmax (0: best form for the shape, 1: scores
+/// then softmax, 2: fused single pass, 3: two-pass 256 x 256 blocks, 8:
+/// two-pass query-stationary).
 void mlkd_score_set_variant(int variant);
 
 #ifdef __cplusplus

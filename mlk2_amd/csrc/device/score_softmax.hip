@@ -3,13 +3,15 @@
 // broadcast elementwise chain Add(Div(S, c), bias[j]) (poly.synth.cpp:
 // 231-353) and the stable softmax (kernel_buffers.cpp:290-340).
 //
-// Scores: v_mfma_f32_32x32x16_f16. Both MFMA operands come straight from HBM
-// with 16-byte loads: Q rows are k-contiguous, and K rows are exactly the
-// columns of K^T, also k-contiguous, so no transpose is needed. A workgroup
-// of 4 waves computes a 64 (i) x 128 (j) block, each wave 32 x 64; the
-// epilogue divides by `div`, adds bias[j] and writes f32 scores into S. The
-// softmax then runs in place over the rows of S with the wave-per-row kernel.
-// Other shapes or dtypes run a scalar f64 path with the same two stages.
+// The output write (4 * batch * seq^2 bytes) bounds the class; the scores are
+// a GEMM with K = dim on v_mfma_f32_32x32x16_f16. Forms, best first:
+//   * two-pass, query-stationary (dim 128, seq % 256 == 0, seq <= 8192): a
+//     statistics pass and a recompute-and-write pass (scoreStatsQ /
+//     scoreStoreQ), rows' partial statistics in artifact scratch;
+//   * two-pass on 256 x 256 blocks (any seq % 256 == 0);
+//   * fused single pass holding a 32-row block in registers (seq <= 2048);
+//   * scores, then the softmax kernel in place over S (any shape, f16);
+//   * a scalar f64 path for other dtypes.
 #include <hip/hip_runtime.h>
 
 #include <stdint.h>
@@ -322,6 +324,548 @@ __global__ __launch_bounds__(WAVES * 64) void scoreSoftmaxFusedT(const _Float16*
     }
 }
 
+// ------------------------------------------------------------ two pass ----
+// Two-pass recompute form (dim 128, seq a multiple of 256): the score matrix
+// is a GEMM with K = 128, so recomputing it costs less than holding a row
+// block in registers while it is written. Both passes tile D in ROWS x COLS
+// blocks; a workgroup has (ROWS/64) x (COLS/128) waves, each computing a
+// 64 x 128 sub-block as 2 x 4 v_mfma_f32_32x32x16_f16 tiles from operand
+// panels staged in LDS (16-byte row padding: conflict-free 16-byte reads).
+// KST is the head-dim width staged per step: 128 stages each panel once,
+// 64 stages two halves through one buffer with the second half's global
+// loads in flight during the first half's MFMAs.
+//   Pass 1 (scoreStats2) computes D = K Q^T (keys x queries), so a query's
+//   scores lie in one lane's accumulators: it reduces max and
+//   sum(exp(v - max)) over 64 keys in registers (one exchange with the lane
+//   32 away), combines the key waves through LDS and writes the pair for its
+//   ROWS-key block to scratch[row][key block].
+//   Pass 2 (scoreStore2) combines a row's partials, computes D = Q K^T
+//   (queries x keys) and writes exp(v - max) / sum to S, each 32-lane
+//   half-wave one 128-byte line per store (plain stores, or nontemporal).
+// Both evaluate v = acc * (1/div) + bias[j] with the same operations on the
+// same MFMA results. Workgroups of one batch run on one XCD, whose L2 then
+// holds that batch's Q and K.
+constexpr int kD2 = 128;                 // head dim
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+
+/// Threads of a workgroup of (rows/64) x (cols/128) waves.
+constexpr int threads2(int rows, int cols) { return (rows / 64) * (cols / 128) * 64; }
+
+template <int ROWS, int COLS, int KST>
+struct Shape2 {
+    static constexpr int kWaves = (ROWS / 64) * (COLS / 128);
+    static constexpr int kThreads = kWaves * 64;
+    static constexpr int kRow = KST + 8;                       // halves per LDS row
+    static constexpr int kChunksRow = KST / 8;                 // 16-byte chunks per staged row
+    static constexpr int kChunks = (ROWS + COLS) * kChunksRow;
+    static constexpr int kPer = kChunks / kThreads;            // chunks per thread per stage
+    static constexpr size_t kLds = static_cast<size_t>(ROWS + COLS) * kRow * sizeof(_Float16);
+    static_assert(kChunks % kThreads == 0, "stage must split evenly over the threads");
+};
+
+/// Global -> registers for one head-dim stage of the two panels: ROWS rows of
+/// `m`, then COLS rows of `n`.
+template <class SH, int ROWS>
+__device__ __forceinline__ void loadStage2(const _Float16* __restrict__ m, const _Float16* __restrict__ n,
+                                           int stage, int tid, u32x4v (&v)[SH::kPer]) {
+#pragma unroll
+    for (int j = 0; j < SH::kPer; ++j) {
+        const int c = j * SH::kThreads + tid;
+        const int r = c / SH::kChunksRow;
+        const int ch = c % SH::kChunksRow;
+        const _Float16* src = r < ROWS ? m + r * kD2 : n + (r - ROWS) * kD2;
+        v[j] = *reinterpret_cast<const u32x4v*>(src + stage * SH::kChunksRow * 8 + ch * 8);
+    }
+}
+
+template <class SH>
+__device__ __forceinline__ void storeStage2(_Float16* lds, int tid, const u32x4v (&v)[SH::kPer]) {
+#pragma unroll
+    for (int j = 0; j < SH::kPer; ++j) {
+        const int c = j * SH::kThreads + tid;
+        *reinterpret_cast<u32x4v*>(lds + (c / SH::kChunksRow) * SH::kRow + (c % SH::kChunksRow) * 8) = v[j];
+    }
+}
+
+/// acc[2][4] += the wave's 64 x 128 sub-block over one staged head-dim range.
+template <class SH, int ROWS, int KST>
+__device__ __forceinline__ void mfmaStage2(const _Float16* lds, int wm, int wn, int l32, int hl,
+                                           f32x16 (&acc)[2][4]) {
+    const _Float16* pm = lds;
+    const _Float16* pn = lds + ROWS * SH::kRow;
+#pragma unroll
+    for (int ks = 0; ks < KST / 16; ++ks) {
+        f16x8 a[2], x[4];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            a[i] = *reinterpret_cast<const f16x8*>(pm + (wm * 64 + i * 32 + l32) * SH::kRow + ks * 16 + hl * 8);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            x[j] = *reinterpret_cast<const f16x8*>(pn + (wn * 128 + j * 32 + l32) * SH::kRow + ks * 16 + hl * 8);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], x[j], acc[i][j], 0, 0, 0);
+            }
+        }
+    }
+}
+
+/// The block's ROWS x COLS products over K = 128 (m: ROWS rows, n: COLS rows).
+template <int ROWS, int COLS, int KST>
+__device__ __forceinline__ void blockProduct2(const _Float16* __restrict__ m, const _Float16* __restrict__ n,
+                                              _Float16* lds, int tid, f32x16 (&acc)[2][4]) {
+    using SH = Shape2<ROWS, COLS, KST>;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / (COLS / 128), wn = wave % (COLS / 128), l32 = lane & 31, hl = lane >> 5;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+        }
+    }
+    u32x4v v[SH::kPer];
+    loadStage2<SH, ROWS>(m, n, 0, tid, v);
+    storeStage2<SH>(lds, tid, v);
+    __syncthreads();
+    if constexpr (KST == kD2) {
+        mfmaStage2<SH, ROWS, KST>(lds, wm, wn, l32, hl, acc);
+    } else {
+#pragma unroll
+        for (int st = 1; st < kD2 / KST; ++st) {
+            loadStage2<SH, ROWS>(m, n, st, tid, v);   // in flight during the previous stage's MFMAs
+            mfmaStage2<SH, ROWS, KST>(lds, wm, wn, l32, hl, acc);
+            __syncthreads();
+            storeStage2<SH>(lds, tid, v);
+            __syncthreads();
+        }
+        mfmaStage2<SH, ROWS, KST>(lds, wm, wn, l32, hl, acc);
+    }
+}
+
+/// Block coordinates: batch, block row and block column. A batch's blocks
+/// are contiguous within one XCD's share of the grid.
+__device__ __forceinline__ void blockOf2(int rowsB, int colsB, int64_t& b, int& tr, int& tc) {
+    const int total = static_cast<int>(gridDim.x);
+    int id = static_cast<int>(blockIdx.x);
+    if (total % 8 == 0) id = (id % 8) * (total / 8) + id / 8;
+    b = id / (rowsB * colsB);
+    const int rem = id % (rowsB * colsB);
+    tr = rem / colsB;
+    tc = rem % colsB;
+}
+
+template <int ROWS, int COLS, int KST>
+__global__ __launch_bounds__(threads2(ROWS, COLS), 512 / threads2(ROWS, COLS))
+void scoreStats2(const _Float16* __restrict__ Q, const _Float16* __restrict__ K, const float* __restrict__ bias,
+                 float2* __restrict__ part, int seq, float rdiv) {
+    constexpr int WN = COLS / 128;
+    constexpr int WM = ROWS / 64;
+    extern __shared__ __align__(16) _Float16 lds2[];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN, l32 = lane & 31, hl = lane >> 5;
+    const int nKB = seq / ROWS;          // key blocks (rows of D here)
+    int64_t b;
+    int tk, tq;
+    blockOf2(nKB, seq / COLS, b, tk, tq);
+    float bk[2][16];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) bk[i][r] = bias[tk * ROWS + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * hl + (r & 3)];
+    }
+    f32x16 acc[2][4];
+    blockProduct2<ROWS, COLS, KST>(K + (b * seq + static_cast<int64_t>(tk) * ROWS) * kD2,
+                                   Q + (b * seq + static_cast<int64_t>(tq) * COLS) * kD2, lds2, tid, acc);
+    float pm[4], pl[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float v = acc[i][j][r] * rdiv + bk[i][r];
+                acc[i][j][r] = v;
+                mx = fmaxf(mx, v);
+            }
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        float l = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) l += __expf(acc[i][j][r] - mx);
+        }
+        pm[j] = mx;
+        pl[j] = l + __shfl_xor(l, 32, 64);
+    }
+    // Combine the key waves of each query through LDS: [WM][COLS] max, then sum.
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(lds2);
+    if (hl == 0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            red[wm * COLS + wn * 128 + j * 32 + l32] = pm[j];
+            red[(WM + wm) * COLS + wn * 128 + j * 32 + l32] = pl[j];
+        }
+    }
+    __syncthreads();
+    for (int q = tid; q < COLS; q += Shape2<ROWS, COLS, KST>::kThreads) {
+        float mx = red[q];
+#pragma unroll
+        for (int w = 1; w < WM; ++w) mx = fmaxf(mx, red[w * COLS + q]);
+        float l = 0.0f;
+#pragma unroll
+        for (int w = 0; w < WM; ++w) l += red[(WM + w) * COLS + q] * __expf(red[w * COLS + q] - mx);
+        part[(b * seq + static_cast<int64_t>(tq) * COLS + q) * nKB + tk] = make_float2(mx, l);
+    }
+}
+
+template <int ROWS, int COLS, int KST, bool NT>
+__global__ __launch_bounds__(threads2(ROWS, COLS), 512 / threads2(ROWS, COLS))
+void scoreStore2(const _Float16* __restrict__ Q, const _Float16* __restrict__ K, const float* __restrict__ bias,
+                 const float2* __restrict__ part, float* __restrict__ S, int seq, int nKB, float rdiv) {
+    constexpr int WN = COLS / 128;
+    extern __shared__ __align__(16) _Float16 lds2[];
+    __shared__ float rowMax[ROWS];
+    __shared__ float rowInv[ROWS];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN, l32 = lane & 31, hl = lane >> 5;
+    int64_t b;
+    int tq, tk;
+    blockOf2(seq / ROWS, seq / COLS, b, tq, tk);
+    const int64_t row0 = b * seq + static_cast<int64_t>(tq) * ROWS;
+    for (int rr = tid; rr < ROWS; rr += Shape2<ROWS, COLS, KST>::kThreads) {
+        const float2* pr = part + (row0 + rr) * nKB;
+        float mx = -INFINITY;
+        for (int p = 0; p < nKB; ++p) mx = fmaxf(mx, pr[p].x);
+        float l = 0.0f;
+        for (int p = 0; p < nKB; ++p) l += pr[p].y * __expf(pr[p].x - mx);
+        rowMax[rr] = mx;
+        rowInv[rr] = l != 0.0f ? 1.0f / l : 0.0f;
+    }
+    float bj[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bj[j] = bias[tk * COLS + wn * 128 + j * 32 + l32];
+    f32x16 acc[2][4];
+    blockProduct2<ROWS, COLS, KST>(Q + row0 * kD2, K + (b * seq + static_cast<int64_t>(tk) * COLS) * kD2, lds2, tid,
+                                   acc);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int rl = wm * 64 + i * 32 + 8 * (r >> 2) + 4 * hl + (r & 3);
+            const float mx = rowMax[rl];
+            const float inv = rowInv[rl];
+            float* dst = S + (row0 + rl) * static_cast<int64_t>(seq) + tk * COLS + wn * 128 + l32;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float o = __expf(acc[i][j][r] * rdiv + bj[j] - mx) * inv;
+                if constexpr (NT) {
+                    __builtin_nontemporal_store(o, dst + j * 32);
+                } else {
+                    dst[j * 32] = o;
+                }
+            }
+        }
+    }
+}
+
+// Query-stationary form of the two passes (dim 128, seq a multiple of 256).
+// A wave owns 32 query rows and holds their Q fragments in registers for the
+// whole kernel; a workgroup of 4 waves (128 rows) streams one half of the
+// batch's keys through LDS in 128-key panels, double buffered, the next
+// panel's global loads in flight during the current panel's MFMAs. 73 KiB
+// of LDS and <= 256 registers per lane let two workgroups share a CU.
+//   Pass 1 (scoreStatsQ) computes D = K Q^T per panel, so each lane holds 64
+//   of its query's scores per panel and keeps a running max and
+//   sum(exp(v - max)) in two registers; the lane 32 away holds the other
+//   keys of the same query, and the pair is combined once at the end into
+//   scratch[row][key half].
+//   Pass 2 (scoreStoreQ) computes D = Q K^T per panel and writes
+//   exp(v - max) / sum for the panel at once: each 32-lane half-wave stores
+//   one 128-byte line, while the other workgroup on the CU computes.
+// Both passes work in base 2 with log2(e) folded into 1/div and the bias, so
+// a score costs one fused multiply-add and one v_exp_f32: the passes are
+// bound by VALU work (67M exponentials each), not by the MFMAs.
+constexpr int kPanelQ = 128;                   // keys per streamed panel
+constexpr float kLog2e = 1.44269504088896340736f;
+constexpr int kRowQ = kD2 + 8;                 // halves per LDS panel row
+constexpr int kPanelHalvesQ = kPanelQ * kRowQ;
+constexpr size_t kLdsStoreQ = 2 * kPanelHalvesQ * sizeof(_Float16);  // pass 1 adds seq/2 floats of bias
+constexpr int64_t kMaxSeqQ = 8192;             // pass 1's LDS stays <= 86 KiB
+
+/// 256 threads: global -> registers for one 128-key panel (8 chunks each).
+__device__ __forceinline__ void loadPanelQ(const _Float16* __restrict__ k, int tid, u32x4v (&v)[8]) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int c = j * 256 + tid;
+        v[j] = *reinterpret_cast<const u32x4v*>(k + (c >> 4) * kD2 + (c & 15) * 8);
+    }
+}
+
+__device__ __forceinline__ void storePanelQ(_Float16* dst, int tid, const u32x4v (&v)[8]) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int c = j * 256 + tid;
+        *reinterpret_cast<u32x4v*>(dst + (c >> 4) * kRowQ + (c & 15) * 8) = v[j];
+    }
+}
+
+/// Workgroup coordinates: batch, 128-row block, key half. A batch's
+/// workgroups are contiguous within one XCD's share of the grid.
+__device__ __forceinline__ void blockOfQ(int rowBlocks, int64_t& b, int& rb, int& kh) {
+    const int total = static_cast<int>(gridDim.x);
+    int id = static_cast<int>(blockIdx.x);
+    if (total % 8 == 0) id = (id % 8) * (total / 8) + id / 8;
+    b = id / (rowBlocks * 2);
+    const int rem = id % (rowBlocks * 2);
+    rb = rem / 2;
+    kh = rem % 2;
+}
+
+__global__ __launch_bounds__(256, 2) void scoreStatsQ(const _Float16* __restrict__ Q,
+                                                      const _Float16* __restrict__ K,
+                                                      const float* __restrict__ bias,
+                                                      float2* __restrict__ part, int seq, float c2) {
+    extern __shared__ __align__(16) _Float16 ldsQ[];
+    float* lbias = reinterpret_cast<float*>(ldsQ + 2 * kPanelHalvesQ);  // the key half's bias
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6, l32 = lane & 31, hl = lane >> 5;
+    int64_t b;
+    int rb, kh;
+    blockOfQ(seq / 128, b, rb, kh);
+    const int keys = seq / 2;
+    const int k0 = kh * keys;
+    const int np = keys / kPanelQ;
+    const int64_t qrow = b * seq + static_cast<int64_t>(rb) * 128 + wave * 32 + l32;
+    f16x8 xq[8];                                  // B operand: this lane's query, 8 x 16 head dims
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) xq[ks] = *reinterpret_cast<const f16x8*>(Q + qrow * kD2 + ks * 16 + hl * 8);
+    for (int i = tid; i < keys; i += 256) lbias[i] = bias[k0 + i] * kLog2e;
+    const _Float16* kb = K + (b * seq + k0) * kD2;
+    u32x4v v[8];
+    loadPanelQ(kb, tid, v);
+    storePanelQ(ldsQ, tid, v);
+    __syncthreads();
+    float m = -INFINITY, l = 0.0f;
+    for (int p = 0; p < np; ++p) {
+        if (p + 1 < np) loadPanelQ(kb + static_cast<int64_t>(p + 1) * kPanelQ * kD2, tid, v);
+        const _Float16* pk = ldsQ + (p & 1) * kPanelHalvesQ;
+        f32x16 acc[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][r] = 0.0f;
+        }
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const f16x8 a = *reinterpret_cast<const f16x8*>(pk + (i * 32 + l32) * kRowQ + ks * 16 + hl * 8);
+                acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, xq[ks], acc[i], 0, 0, 0);
+            }
+        }
+        // acc[i][r]: key p*128 + i*32 + 8*(r/4) + 4*hl + r%4 of this lane's query.
+        float mb = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const f32x4 bb = *reinterpret_cast<const f32x4*>(lbias + p * kPanelQ + i * 32 + 8 * g + 4 * hl);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float x = __builtin_fmaf(acc[i][4 * g + q], c2, bb[q]);
+                    acc[i][4 * g + q] = x;
+                    mb = fmaxf(mb, x);
+                }
+            }
+        }
+        const float mn = fmaxf(m, mb);
+        float sb = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sb += __builtin_amdgcn_exp2f(acc[i][r] - mn);
+        }
+        l = l * __builtin_amdgcn_exp2f(m - mn) + sb;
+        m = mn;
+        if (p + 1 < np) storePanelQ(ldsQ + ((p + 1) & 1) * kPanelHalvesQ, tid, v);
+        __syncthreads();
+    }
+    const float mo = __shfl_xor(m, 32, 64);
+    const float lo = __shfl_xor(l, 32, 64);
+    const float mx = fmaxf(m, mo);
+    const float lt = l * __builtin_amdgcn_exp2f(m - mx) + lo * __builtin_amdgcn_exp2f(mo - mx);
+    if (hl == 0) part[qrow * 2 + kh] = make_float2(mx, lt);
+}
+
+__global__ __launch_bounds__(256, 2) void scoreStoreQ(const _Float16* __restrict__ Q,
+                                                      const _Float16* __restrict__ K,
+                                                      const float* __restrict__ bias,
+                                                      const float2* __restrict__ part, float* __restrict__ S,
+                                                      int seq, float c2) {
+    extern __shared__ __align__(16) _Float16 ldsQ[];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6, l32 = lane & 31, hl = lane >> 5;
+    int64_t b;
+    int rb, kh;
+    blockOfQ(seq / 128, b, rb, kh);
+    const int keys = seq / 2;
+    const int k0 = kh * keys;
+    const int np = keys / kPanelQ;
+    const int64_t r0 = b * seq + static_cast<int64_t>(rb) * 128 + wave * 32;
+    f16x8 aq[8];                                  // A operand: row r0 + l32
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+        aq[ks] = *reinterpret_cast<const f16x8*>(Q + (r0 + l32) * kD2 + ks * 16 + hl * 8);
+    }
+    // Row statistics of the 16 rows this lane's accumulators hold.
+    float rmx[16], rinv[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const float2* pr = part + (r0 + 8 * (r >> 2) + 4 * hl + (r & 3)) * 2;
+        const float2 p0 = pr[0], p1 = pr[1];
+        const float mx = fmaxf(p0.x, p1.x);
+        const float lt = p0.y * __builtin_amdgcn_exp2f(p0.x - mx) + p1.y * __builtin_amdgcn_exp2f(p1.x - mx);
+        rmx[r] = mx;
+        rinv[r] = lt != 0.0f ? 1.0f / lt : 0.0f;
+    }
+    const _Float16* kb = K + (b * seq + k0) * kD2;
+    u32x4v v[8];
+    loadPanelQ(kb, tid, v);
+    storePanelQ(ldsQ, tid, v);
+    __syncthreads();
+    for (int p = 0; p < np; ++p) {
+        if (p + 1 < np) loadPanelQ(kb + static_cast<int64_t>(p + 1) * kPanelQ * kD2, tid, v);
+        const _Float16* pk = ldsQ + (p & 1) * kPanelHalvesQ;
+        f32x16 acc[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
+        }
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const f16x8 x = *reinterpret_cast<const f16x8*>(pk + (j * 32 + l32) * kRowQ + ks * 16 + hl * 8);
+                acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(aq[ks], x, acc[j], 0, 0, 0);
+            }
+        }
+        const int kc = k0 + p * kPanelQ;
+        float bj[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bj[j] = bias[kc + j * 32 + l32] * kLog2e;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            float* dst = S + (r0 + 8 * (r >> 2) + 4 * hl + (r & 3)) * static_cast<int64_t>(seq) + kc + l32;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                dst[j * 32] = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[j][r], c2, bj[j]) - rmx[r]) * rinv[r];
+            }
+        }
+        if (p + 1 < np) storePanelQ(ldsQ + ((p + 1) & 1) * kPanelHalvesQ, tid, v);
+        __syncthreads();
+    }
+}
+
+int launchQ(const mlkd_score_softmax* p, hipStream_t st) {
+    const size_t ldsStats = kLdsStoreQ + static_cast<size_t>(p->seq / 2) * sizeof(float);
+    static bool attrs = false;
+    if (!attrs) {
+        const size_t maxStats = kLdsStoreQ + static_cast<size_t>(kMaxSeqQ / 2) * sizeof(float);
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(scoreStatsQ), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                static_cast<int>(maxStats)) != hipSuccess ||
+            hipFuncSetAttribute(reinterpret_cast<const void*>(scoreStoreQ), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                static_cast<int>(kLdsStoreQ)) != hipSuccess) {
+            return MLKD_RT_LAUNCH;
+        }
+        attrs = true;
+    }
+    const unsigned blocks = static_cast<unsigned>(p->batch * (p->seq / 128) * 2);
+    // Both passes work in base 2: v2 = acc * (log2(e) / div) + bias * log2(e),
+    // exp(v - max) = exp2(v2 - max2).
+    const float c2 = static_cast<float>(1.4426950408889634 / p->div);
+    hipLaunchKernelGGL(scoreStatsQ, dim3(blocks), dim3(256), ldsStats, st, static_cast<const _Float16*>(p->q),
+                       static_cast<const _Float16*>(p->k), static_cast<const float*>(p->bias),
+                       static_cast<float2*>(p->scratch), static_cast<int>(p->seq), c2);
+    hipLaunchKernelGGL(scoreStoreQ, dim3(blocks), dim3(256), kLdsStoreQ, st, static_cast<const _Float16*>(p->q),
+                       static_cast<const _Float16*>(p->k), static_cast<const float*>(p->bias),
+                       static_cast<const float2*>(p->scratch), static_cast<float*>(p->s), static_cast<int>(p->seq),
+                       c2);
+    return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
+}
+
+bool twoPassApplies(const mlkd_score_softmax* p) {
+    return p->qk_dtype == MLKD_F16 && p->bias_dtype == MLKD_F32 && p->s_dtype == MLKD_F32 &&
+           p->dim == kD2 && p->seq % 256 == 0 && p->seq > 0 && p->seq <= (1 << 16) &&
+           (reinterpret_cast<uintptr_t>(p->q) & 15u) == 0 && (reinterpret_cast<uintptr_t>(p->k) & 15u) == 0 &&
+           p->batch * (p->seq / 128) * (p->seq / 256) <= 0x7FFFFFFF;
+}
+
+/// Partials are kept per 128-key block (the smallest key block any stats
+/// shape uses), so every stats shape fits the same scratch.
+int64_t scratch2(const mlkd_score_softmax* p) {
+    return p->batch * p->seq * (p->seq / 128) * static_cast<int64_t>(sizeof(float2));
+}
+
+template <int ROWS, int COLS, int KST>
+int launchStats2(const mlkd_score_softmax* p, hipStream_t st, float rdiv) {
+    using SH = Shape2<ROWS, COLS, KST>;
+    static bool attr = false;
+    if (!attr && SH::kLds > 65536) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(scoreStats2<ROWS, COLS, KST>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(SH::kLds)) != hipSuccess) {
+            return -1;
+        }
+    }
+    attr = true;
+    const unsigned blocks = static_cast<unsigned>(p->batch * (p->seq / ROWS) * (p->seq / COLS));
+    hipLaunchKernelGGL((scoreStats2<ROWS, COLS, KST>), dim3(blocks), dim3(SH::kThreads), SH::kLds, st,
+                       static_cast<const _Float16*>(p->q), static_cast<const _Float16*>(p->k),
+                       static_cast<const float*>(p->bias), static_cast<float2*>(p->scratch),
+                       static_cast<int>(p->seq), rdiv);
+    return static_cast<int>(p->seq / ROWS);
+}
+
+template <int ROWS, int COLS, int KST, bool NT>
+int launchStore2(const mlkd_score_softmax* p, hipStream_t st, float rdiv, int nKB) {
+    using SH = Shape2<ROWS, COLS, KST>;
+    static bool attr = false;
+    if (!attr && SH::kLds > 65536 - 2 * ROWS * 4) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(scoreStore2<ROWS, COLS, KST, NT>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(SH::kLds)) != hipSuccess) {
+            return -1;
+        }
+    }
+    attr = true;
+    const unsigned blocks = static_cast<unsigned>(p->batch * (p->seq / ROWS) * (p->seq / COLS));
+    hipLaunchKernelGGL((scoreStore2<ROWS, COLS, KST, NT>), dim3(blocks), dim3(SH::kThreads), SH::kLds, st,
+                       static_cast<const _Float16*>(p->q), static_cast<const _Float16*>(p->k),
+                       static_cast<const float*>(p->bias), static_cast<const float2*>(p->scratch),
+                       static_cast<float*>(p->s), static_cast<int>(p->seq), nKB, rdiv);
+    return 0;
+}
+
+// Two-pass forms: v8 (default) query-stationary, seq <= 8192; v3 the
+// 256 x 256 block form for any seq multiple of 256.
+int launchTwoPass(const mlkd_score_softmax* p, hipStream_t st, int variant) {
+    if (variant != 3 && p->seq <= kMaxSeqQ) return launchQ(p, st);
+    const float rdiv = static_cast<float>(1.0 / p->div);
+    const int nKB = launchStats2<256, 256, 128>(p, st, rdiv);
+    if (nKB < 0 || launchStore2<256, 256, 128, false>(p, st, rdiv, nKB) != 0) return MLKD_RT_LAUNCH;
+    return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
+}
+
 template <typename T>
 __device__ __forceinline__ double ldAny(const void* p, int dt, int64_t i) {
     if (dt == MLKD_F32) return static_cast<const float*>(p)[i];
@@ -352,22 +896,32 @@ __global__ __launch_bounds__(256) void scoresGeneral(mlkd_score_softmax p) {
     }
 }
 
-// 0: fused single pass where the shape allows it; 1: scores then softmax.
+// 0: the best form for the shape; 1: scores then softmax; 2: fused single
+// pass; 3: two-pass 256 x 256 blocks; 8: two-pass query-stationary.
 int gScoreVariant = 0;
 
 }  // namespace
 
 extern "C" void mlkd_score_set_variant(int variant) { gScoreVariant = variant; }
 
+extern "C" int64_t mlkd_score_scratch_bytes(const mlkd_score_softmax* p) {
+    return p != nullptr && twoPassApplies(p) ? scratch2(p) : 0;
+}
+
 extern "C" int mlkd_launch_score_softmax(const mlkd_score_softmax* p, void* stream) {
     if (p == nullptr || p->batch < 0 || p->seq < 0 || p->dim < 0) return MLKD_RT_LAUNCH;
     if (p->batch == 0 || p->seq == 0) return 0;
     hipStream_t st = static_cast<hipStream_t>(stream);
+    if ((gScoreVariant == 0 || gScoreVariant == 3 || gScoreVariant == 8) && twoPassApplies(p) &&
+        p->scratch != nullptr && (reinterpret_cast<uintptr_t>(p->scratch) & 7u) == 0 &&
+        p->scratch_bytes >= scratch2(p)) {
+        return launchTwoPass(p, st, gScoreVariant);
+    }
     const bool fast = p->qk_dtype == MLKD_F16 && p->bias_dtype == MLKD_F32 && p->s_dtype == MLKD_F32 &&
                       p->seq % 128 == 0 && p->dim % 16 == 0 && p->dim > 0 && p->seq < (1 << 20) &&
                       (reinterpret_cast<uintptr_t>(p->q) & 15u) == 0 &&
                       (reinterpret_cast<uintptr_t>(p->k) & 15u) == 0 && p->dim % 8 == 0;
-    const bool fused = fast && p->seq <= 2048 && p->dim <= 256 && gScoreVariant == 0;
+    const bool fused = fast && p->seq <= 2048 && p->dim <= 256 && gScoreVariant != 1;
     // Second fused form for dim 64/128 and seq a multiple of 256 (8 waves of
     // seq/256 tiles, at most 8 tiles per wave).
     if (fused && (p->dim == 128 || p->dim == 64) && p->seq % 256 == 0) {

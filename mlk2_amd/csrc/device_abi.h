@@ -51,6 +51,10 @@ typedef struct mlkd_score_softmax {
     int32_t qk_dtype, bias_dtype, s_dtype, pad;
     int64_t batch, seq, dim;
     double div;
+    /* Device scratch for the two-pass form's per-tile row statistics
+       (mlkd_score_scratch_bytes); may be NULL, which selects another form. */
+    void* scratch;
+    int64_t scratch_bytes;
 } mlkd_score_softmax;
 
 #ifdef __cplusplus

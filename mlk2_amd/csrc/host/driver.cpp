@@ -112,6 +112,8 @@ Result<std::unique_ptr<HipLoadedKernel>> buildHipKernelArtifact(const KernelModu
     }
     k->scratch_.assign(km.buffers.size(), nullptr);
     k->scratchElems_.assign(km.buffers.size(), 0);
+    k->stepScratch_.assign(k->plan_.steps.size(), nullptr);
+    k->stepScratchBytes_.assign(k->plan_.steps.size(), 0);
     return k;
 }
 
@@ -120,6 +122,9 @@ HipLoadedKernel::~HipLoadedKernel() {
         if (p != nullptr) mlkd_rt_free(p);
     }
     if (status_ != nullptr) mlkd_rt_free(status_);
+    for (void* p : stepScratch_) {
+        if (p != nullptr) mlkd_rt_free(p);
+    }
 }
 
 int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* scalars,
@@ -171,7 +176,8 @@ int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* 
     }
     mlkd_scalars sc;
     for (int i = 0; i < MLKD_MAX_SCALARS; ++i) sc.v[i] = (scalars != nullptr && i < nScalars) ? scalars[i] : 0.0;
-    for (const Step& st : plan_.steps) {
+    for (size_t si = 0; si < plan_.steps.size(); ++si) {
+        const Step& st = plan_.steps[si];
         int rc = 0;
         switch (st.kind) {
             case StepKind::Fail:
@@ -307,6 +313,23 @@ int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* 
                 p.seq = st.seq;
                 p.dim = st.dim;
                 p.div = st.div;
+                p.scratch = nullptr;
+                p.scratch_bytes = 0;
+                if (const int64_t need = mlkd_score_scratch_bytes(&p); need > 0) {
+                    std::lock_guard<std::mutex> g(scratchLock_);
+                    if (stepScratch_[si] == nullptr || stepScratchBytes_[si] < need) {
+                        if (stepScratch_[si] != nullptr) mlkd_rt_free(stepScratch_[si]);
+                        stepScratch_[si] = nullptr;
+                        if (mlkd_rt_malloc(&stepScratch_[si], static_cast<size_t>(need)) != 0) {
+                            stepScratch_[si] = nullptr;
+                            why = "score-softmax scratch allocation failed";
+                            return MLKHIP_RUNTIME;
+                        }
+                        stepScratchBytes_[si] = need;
+                    }
+                    p.scratch = stepScratch_[si];
+                    p.scratch_bytes = stepScratchBytes_[si];
+                }
                 rc = mlkd_launch_score_softmax(&p, stream);
                 break;
             }

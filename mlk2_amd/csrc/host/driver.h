@@ -65,6 +65,10 @@ private:
     mutable std::vector<int64_t> scratchElems_;
     // Status word of loop-nest steps with run-time bounds checks.
     mutable void* status_{nullptr};
+    // Per-step device scratch a launcher asks for (score-softmax row
+    // statistics), allocated on first use and kept.
+    mutable std::vector<void*> stepScratch_;
+    mutable std::vector<int64_t> stepScratchBytes_;
 };
 
 /// Plans, instantiates and loads (buildGpuKernelArtifact analogue).

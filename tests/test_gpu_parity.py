@@ -282,7 +282,7 @@ def _score_ref(Q, K, bias, rows=None):
     return np.concatenate(out)
 
 
-@pytest.mark.parametrize("b,s,dm", [(1, 2048, 128), (2, 512, 64), (1, 384, 16)])
+@pytest.mark.parametrize("b,s,dm", [(1, 2048, 128), (2, 512, 64), (1, 384, 16), (2, 512, 128), (3, 256, 128)])
 def test_c5_fused_shapes(hip, b, s, dm):
     say(f"c5 fused b={b} s={s} d={dm}")
     d = inputs.config_inputs("c5", {"batch": b, "seq": s, "dim": dm})
