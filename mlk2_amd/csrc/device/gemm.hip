@@ -196,6 +196,284 @@ __global__ __launch_bounds__(512) void gemmF16Mfma(const _Float16* __restrict__ 
     }
 }
 
+/// Three-stage variant of gemmF16Mfma: global loads run two K steps ahead
+/// into alternating register sets, so a tile's load latency is covered by
+/// two steps of MFMAs instead of one; the LDS tiles stay double buffered.
+/// The K loop is unrolled by two so both register sets are static.
+template <bool ACC>
+__global__ __launch_bounds__(512) void gemmF16Mfma3s(const _Float16* __restrict__ A,
+                                                     const _Float16* __restrict__ B,
+                                                     float* __restrict__ C, int M, int N, int K,
+                                                     int64_t lda, int64_t ldb, int64_t ldc,
+                                                     int /*accumulate: template ACC*/) {
+    extern __shared__ __align__(16) _Float16 lds[];
+    _Float16* As = lds;
+    _Float16* Bs = lds + 2 * kTileHalves;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave >> 2;
+    const int wn = wave & 3;
+    int tm, tn;
+    xcdTile(M / kBM, N / kBN, tm, tn);
+    const int64_t row0 = static_cast<int64_t>(tm) * kBM;
+    const int64_t col0 = static_cast<int64_t>(tn) * kBN;
+    const bool loadsA = tid < 256;
+    const int t = tid & 255;
+    const int bk = t & 7;
+    const int bn = t >> 3;
+    u32x4 r0[8], r1[8];
+
+    auto globalLoad = [&](int k0, u32x4(&reg)[8]) {
+        if (loadsA) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int c = j * 256 + t;
+                reg[j] = *reinterpret_cast<const u32x4*>(A + (row0 + (c >> 3)) * lda + k0 + (c & 7) * 8);
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                reg[r] = *reinterpret_cast<const u32x4*>(B + static_cast<int64_t>(k0 + bk * 8 + r) * ldb + col0 +
+                                                         bn * 8);
+            }
+        }
+    };
+    auto ldsStore = [&](int buf, const u32x4(&reg)[8]) {
+        if (loadsA) {
+            _Float16* dst = As + buf * kTileHalves;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int c = j * 256 + t;
+                *reinterpret_cast<u32x4*>(dst + (c >> 3) * kPadK + (c & 7) * 8) = reg[j];
+            }
+        } else {
+            _Float16* dst = Bs + buf * kTileHalves;
+#pragma unroll
+            for (int n = 0; n < 8; ++n) {
+                const int pp = n >> 1;
+                const uint32_t sel = (n & 1) ? 0x07060302u : 0x05040100u;
+                u32x4 o;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) o[j] = __builtin_amdgcn_perm(reg[2 * j + 1][pp], reg[2 * j][pp], sel);
+                *reinterpret_cast<u32x4*>(dst + (bn * 8 + n) * kPadK + bk * 8) = o;
+            }
+        }
+    };
+
+    f32x16 acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+        }
+    }
+    const int lrow = lane & 31;
+    const int lk = (lane >> 5) * 8;
+    auto mfmaStep = [&](int buf) {
+        const _Float16* as = As + buf * kTileHalves + (wm * 128 + lrow) * kPadK + lk;
+        const _Float16* bs = Bs + buf * kTileHalves + (wn * 64 + lrow) * kPadK + lk;
+#pragma unroll
+        for (int kk = 0; kk < kBK; kk += 16) {
+            f16x8 a[4], b[2];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const f16x8*>(as + i * 32 * kPadK + kk);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) b[j] = *reinterpret_cast<const f16x8*>(bs + j * 32 * kPadK + kk);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+                }
+            }
+        }
+    };
+
+    // Step s computes from LDS buffer s&1. At its start the registers hold
+    // tile s+1 (set (s+1)&1); tile s+2 is loaded into set s&1.
+    const int steps = K / kBK;
+    globalLoad(0, r0);
+    ldsStore(0, r0);
+    if (steps > 1) globalLoad(kBK, r1);
+    __syncthreads();
+    for (int s = 0; s < steps; s += 2) {
+        // even step s: buffer 0, registers r1 hold tile s+1
+        if (s + 2 < steps) globalLoad((s + 2) * kBK, r0);
+        mfmaStep(0);
+        if (s + 1 < steps) ldsStore(1, r1);
+        __syncthreads();
+        if (s + 1 >= steps) break;
+        // odd step s+1: buffer 1, registers r0 hold tile s+2
+        if (s + 3 < steps) globalLoad((s + 3) * kBK, r1);
+        mfmaStep(1);
+        if (s + 2 < steps) ldsStore(0, r0);
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int64_t cBase = col0 + wn * 64 + j * 32 + (lane & 31);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int64_t row = row0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                float* dst = C + row * ldc + cBase;
+                const float v = acc[i][j][r];
+                *dst = ACC ? *dst + v : v;
+            }
+        }
+    }
+}
+
+/// Two-per-CU variant: a 128 x 256 workgroup tile of 4 waves (each 64 x 128 =
+/// 2 x 4 MFMA tiles), K step 32, LDS tiles double buffered in 60 KiB, so
+/// two workgroups share a CU and one's load waits overlap the other's MFMAs.
+/// Global loads run two steps ahead in two register sets (the K loop is
+/// unrolled by two so the sets are static; AHEAD2 = false loads one step
+/// ahead in one set). A is staged as loaded ([m][k]);
+/// B arrives as 4 (k) x 8 (n) blocks and is transposed in registers to
+/// [n][k]; LDS rows are 40 halves (80 bytes), which keeps the 16-byte
+/// operand reads conflict-free.
+constexpr int kBM2 = 128, kBN2 = 256, kBK2 = 32, kPad2 = kBK2 + 8;
+constexpr int kTileA2 = kBM2 * kPad2, kTileB2 = kBN2 * kPad2;
+constexpr size_t kLdsGemm2 = 2 * (kTileA2 + kTileB2) * sizeof(_Float16);
+
+__device__ __forceinline__ void xcdTile2(int tilesM, int tilesN, int& tm, int& tn) {
+    // Consecutive ids go to different XCDs: give each XCD a contiguous block
+    // of tile ids, row-major over (tm, tn) within the block.
+    const int total = tilesM * tilesN;
+    int id = blockIdx.x;
+    if (total % 8 == 0) id = (id % 8) * (total / 8) + id / 8;
+    tm = id / tilesN;
+    tn = id % tilesN;
+}
+
+template <bool ACC, bool AHEAD2>
+__global__ __launch_bounds__(256, 2) void gemmF16Mfma2cu(const _Float16* __restrict__ A,
+                                                         const _Float16* __restrict__ B,
+                                                         float* __restrict__ C, int M, int N, int K,
+                                                         int64_t lda, int64_t ldb, int64_t ldc) {
+    extern __shared__ __align__(16) _Float16 lds[];
+    _Float16* As = lds;                     // [2][128][40]
+    _Float16* Bs = lds + 2 * kTileA2;       // [2][256][40]
+    const int t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6, l32 = lane & 31, hl = lane >> 5;
+    const int wm = wave >> 1, wn = wave & 1;
+    int tm, tn;
+    xcdTile2(M / kBM2, N / kBN2, tm, tn);
+    const int64_t row0 = static_cast<int64_t>(tm) * kBM2;
+    const int64_t col0 = static_cast<int64_t>(tn) * kBN2;
+    const int bk = t & 7;    // B block: k rows bk*4 .. +3
+    const int bn = t >> 3;   // B block: n cols bn*8 .. +7
+    u32x4 ra0[2], rb0[4], ra1[2], rb1[4];
+    auto load = [&](int k0, u32x4(&ra)[2], u32x4(&rb)[4]) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int c = j * 256 + t;   // 512 chunks: 128 rows x 4
+            ra[j] = *reinterpret_cast<const u32x4*>(A + (row0 + (c >> 2)) * lda + k0 + (c & 3) * 8);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            rb[r] = *reinterpret_cast<const u32x4*>(B + static_cast<int64_t>(k0 + bk * 4 + r) * ldb + col0 + bn * 8);
+        }
+    };
+    auto store = [&](int buf, const u32x4(&ra)[2], const u32x4(&rb)[4]) {
+        _Float16* da = As + buf * kTileA2;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int c = j * 256 + t;
+            *reinterpret_cast<u32x4*>(da + (c >> 2) * kPad2 + (c & 3) * 8) = ra[j];
+        }
+        _Float16* db = Bs + buf * kTileB2;
+#pragma unroll
+        for (int n = 0; n < 8; ++n) {
+            const int pp = n >> 1;
+            const uint32_t sel = (n & 1) ? 0x07060302u : 0x05040100u;
+            uint32_t o0 = __builtin_amdgcn_perm(rb[1][pp], rb[0][pp], sel);
+            uint32_t o1 = __builtin_amdgcn_perm(rb[3][pp], rb[2][pp], sel);
+            typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+            u32x2 o;
+            o[0] = o0;
+            o[1] = o1;
+            *reinterpret_cast<u32x2*>(db + (bn * 8 + n) * kPad2 + bk * 4) = o;
+        }
+    };
+    f32x16 acc[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+        }
+    }
+    auto mfmaStep = [&](int buf) {
+        const _Float16* as = As + buf * kTileA2 + (wm * 64 + l32) * kPad2 + hl * 8;
+        const _Float16* bs = Bs + buf * kTileB2 + (wn * 128 + l32) * kPad2 + hl * 8;
+#pragma unroll
+        for (int kk = 0; kk < kBK2; kk += 16) {
+            f16x8 a[2], b[4];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) a[i] = *reinterpret_cast<const f16x8*>(as + i * 32 * kPad2 + kk);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const f16x8*>(bs + j * 32 * kPad2 + kk);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+                }
+            }
+        }
+    };
+    // K / kBK2 is even (the launcher requires K % 64 == 0).
+    const int steps = K / kBK2;
+    load(0, ra0, rb0);
+    store(0, ra0, rb0);
+    if (AHEAD2) {
+        load(kBK2, ra1, rb1);
+        __syncthreads();
+        for (int s = 0; s < steps; s += 2) {
+            if (s + 2 < steps) load((s + 2) * kBK2, ra0, rb0);
+            mfmaStep(0);
+            store(1, ra1, rb1);
+            __syncthreads();
+            __builtin_amdgcn_sched_barrier(0);
+            if (s + 3 < steps) load((s + 3) * kBK2, ra1, rb1);
+            mfmaStep(1);
+            if (s + 2 < steps) store(0, ra0, rb0);
+            __syncthreads();
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    } else {
+        __syncthreads();
+        for (int s = 0; s < steps; ++s) {
+            if (s + 1 < steps) load((s + 1) * kBK2, ra0, rb0);
+            mfmaStep(s & 1);
+            if (s + 1 < steps) store((s + 1) & 1, ra0, rb0);
+            __syncthreads();
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t cBase = col0 + wn * 128 + j * 32 + l32;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int64_t row = row0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * hl + (r & 3);
+                float* dst = C + row * ldc + cBase;
+                const float v = acc[i][j][r];
+                *dst = ACC ? *dst + v : v;
+            }
+        }
+    }
+}
+
 /// 4-wave variant: the same 256x256x64 workgroup tile with each wave owning a
 /// 128x128 quadrant (4x4 MFMA tiles, 256 accumulators in AGPRs), so every
 /// kk step issues 8 LDS operand reads for 16 MFMAs. Thread t loads 8 A chunks
@@ -771,6 +1049,36 @@ extern "C" int mlkd_launch_gemm(const mlkd_gemm* p, void* stream) {
                 return MLKD_RT_LAUNCH;
             }
             ldsRaised = true;
+        }
+        if (gGemmF16Variant == 5 || gGemmF16Variant == 6) {
+            const int tiles2 = static_cast<int>((p->m / kBM2) * (p->n / kBN2));
+            auto kern = gGemmF16Variant == 5
+                            ? (p->accumulate ? gemmF16Mfma2cu<true, true> : gemmF16Mfma2cu<false, true>)
+                            : (p->accumulate ? gemmF16Mfma2cu<true, false> : gemmF16Mfma2cu<false, false>);
+            hipLaunchKernelGGL(kern, dim3(tiles2), dim3(256), kLdsGemm2, st, static_cast<const _Float16*>(p->a),
+                               static_cast<const _Float16*>(p->b), static_cast<float*>(p->c),
+                               static_cast<int>(p->m), static_cast<int>(p->n), static_cast<int>(p->k), p->lda,
+                               p->ldb, p->ldc);
+            return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
+        }
+        if (gGemmF16Variant == 4) {
+            static bool raised4 = false;
+            if (!raised4) {
+                if (hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF16Mfma3s<true>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        static_cast<int>(ldsBytes)) != hipSuccess ||
+                    hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF16Mfma3s<false>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        static_cast<int>(ldsBytes)) != hipSuccess) {
+                    return MLKD_RT_LAUNCH;
+                }
+                raised4 = true;
+            }
+            hipLaunchKernelGGL((p->accumulate ? gemmF16Mfma3s<true> : gemmF16Mfma3s<false>), dim3(tiles), dim3(512),
+                               ldsBytes, st, static_cast<const _Float16*>(p->a), static_cast<const _Float16*>(p->b),
+                               static_cast<float*>(p->c), static_cast<int>(p->m), static_cast<int>(p->n),
+                               static_cast<int>(p->k), p->lda, p->ldb, p->ldc, 0);
+            return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
         }
         if (gGemmF16Variant == 3) {
             const size_t ldsDirect = (2 * kTileA + 2 * kTileHalves) * sizeof(_Float16);

