@@ -136,6 +136,64 @@ int mlkhip_time_device_span(const mlkhip_artifact* a, const mlkhip_binding* bind
                             const double* scalars, int64_t n_scalars, int64_t elements, void* stream,
                             int warmup, int reps, float* avg_ms);
 
+/* ---- launch-form search (fastkernel on the gfx950 kernels) ------------ */
+/* The reference's fastkernel search (fastkernel/include/mlk/fastkernel/
+ * fast_kernel.h:165-355, src/fast_kernel.cpp:797-887) certifies tile and
+ * exec-path variants of a kernel and keeps the fastest. Here the declared
+ * space is the launch forms of each step's hand-written kernel: softmax
+ * rows (exp form, store cache policy, pipelining), f16 GEMM tiles and
+ * schedules, score-softmax pass structure. */
+
+/* Number of steps (kernel launches) of the artifact's plan. */
+int mlkhip_num_steps(const mlkhip_artifact* a);
+
+/* Declared variant space of step `step` (VariantConfig, fast_kernel.h:
+ * 170-174): writes up to `cap` form ids into `out` (may be NULL) and
+ * returns how many there are (0 = only the default form) or -1. The first
+ * id is the kernel's default form. */
+int mlkhip_step_variants(const mlkhip_artifact* a, int step, int* out, int cap);
+
+/* The same without a device: plans the module and lists step `step`'s
+ * variant space. */
+int mlkhip_plan_variants(const char* module_json, size_t len, int step, int* out, int cap);
+
+/* Form step `step` launches with (-1 = the kernel's default); -2 when the
+ * step does not exist. */
+int mlkhip_step_variant(const mlkhip_artifact* a, int step);
+
+/* Pins step `step` to form `variant` (-1 = default). Returns 0, or
+ * MLKHIP_BAD_BINDING for a step or form outside the declared space. */
+int mlkhip_set_step_variant(mlkhip_artifact* a, int step, int variant);
+
+/* Completeness fingerprint of the artifact's cache entry (fast_kernel.cpp:
+ * 727-763): module hash, declared target, hipRTC version, policy, device.
+ * 16 hex digits. */
+const char* mlkhip_fingerprint(const mlkhip_artifact* a);
+
+/* 1 when mlkhip_build applied a cached choice (<cache_dir>/fk-<fingerprint>
+ * .json) to the steps; the reference's cacheHits (fast_kernel.h:345-346). */
+int mlkhip_variants_from_cache(const mlkhip_artifact* a);
+
+/* Replaces runFastKernelSearch (fast_kernel.h:355-357) for the artifact's
+ * own launch forms. On the caller's device buffers (bindings as for
+ * mlkhip_run_device): runs every step in its default form as the
+ * reference; for each step with more than one form, runs each form with the
+ * other steps at default, certifies it when its outputs are within half of
+ * the artifact's tolerance policy of the reference's (bit-identical under a
+ * bit-exact policy; the identity gate of fast_kernel.cpp:1251-1261), times
+ * `reps` single launches after 2 warmups and takes the median (fast_kernel
+ * .cpp:697-719); keeps the fastest certified form per step and certifies the
+ * chosen combination as a whole (falling back to all defaults if it fails).
+ * The buffers the artifact writes are snapshotted before and restored after
+ * the search. When `cache_dir` is not NULL or empty the choice is written to
+ * <cache_dir>/fk-<fingerprint>.json, which mlkhip_build with the same
+ * cache_dir applies. `report` (may be NULL) receives a JSON document of every
+ * candidate with its certificate or rejection (FastKernelReport::toJson,
+ * fast_kernel.cpp:940-1040). Synchronous; returns a status code. */
+int mlkhip_autotune(mlkhip_artifact* a, const mlkhip_binding* binds, int n_binds, const double* scalars,
+                    int64_t n_scalars, int64_t elements, int reps, const char* cache_dir, char* report,
+                    size_t report_cap);
+
 /* ---- device memory plumbing for hosts without another HIP runtime ----- */
 int mlkhip_malloc(void** p, size_t bytes);
 int mlkhip_free(void* p);

@@ -9,6 +9,7 @@ or CPU fallback: a missing library or device raises.
 from __future__ import annotations
 
 import ctypes
+import json
 import os
 from dataclasses import dataclass
 from typing import Dict, List, Optional, Sequence
@@ -83,6 +84,16 @@ def lib():
     L.mlkhip_time_device_span.argtypes = [c.c_void_p, c.POINTER(Binding), c.c_int, _PD, c.c_int64,
                                           c.c_int64, c.c_void_p, c.c_int, c.c_int,
                                           c.POINTER(c.c_float)]
+    L.mlkhip_num_steps.argtypes = [c.c_void_p]
+    L.mlkhip_step_variants.argtypes = [c.c_void_p, c.c_int, c.POINTER(c.c_int), c.c_int]
+    L.mlkhip_plan_variants.argtypes = [c.c_char_p, c.c_size_t, c.c_int, c.POINTER(c.c_int), c.c_int]
+    L.mlkhip_step_variant.argtypes = [c.c_void_p, c.c_int]
+    L.mlkhip_set_step_variant.argtypes = [c.c_void_p, c.c_int, c.c_int]
+    L.mlkhip_fingerprint.argtypes = [c.c_void_p]
+    L.mlkhip_fingerprint.restype = c.c_char_p
+    L.mlkhip_variants_from_cache.argtypes = [c.c_void_p]
+    L.mlkhip_autotune.argtypes = [c.c_void_p, c.POINTER(Binding), c.c_int, _PD, c.c_int64, c.c_int64,
+                                  c.c_int, c.c_char_p, c.c_char_p, c.c_size_t]
     L.mlkhip_malloc.argtypes = [c.POINTER(c.c_void_p), c.c_size_t]
     L.mlkhip_free.argtypes = [c.c_void_p]
     L.mlkhip_memcpy_h2d.argtypes = [c.c_void_p, c.c_void_p, c.c_size_t]
@@ -130,6 +141,17 @@ def compile_check(km: KernelModule, step: int = 0, arch: str = "gfx950"):
     if n < 0:
         raise MlkHipError(REFUSED, last_error())
     return n, src.value.decode()
+
+
+def plan_variants(km: KernelModule, step: int = 0) -> List[int]:
+    """Declared launch forms of step `step` (first = default; empty when the
+    step has only its default form), without a device."""
+    data = km.to_json().encode()
+    out = (ctypes.c_int * 32)()
+    n = lib().mlkhip_plan_variants(data, len(data), step, out, 32)
+    if n < 0:
+        raise MlkHipError(REFUSED, last_error())
+    return list(out[:n])
 
 
 class DeviceBuffer:
@@ -286,6 +308,45 @@ class LoadedKernel:
         _check(lib().mlkhip_time_device_span(self._h, arr, n, sc.ctypes.data_as(_PD), nsc,
                                              int(elements), stream, warmup, reps, ctypes.byref(ms)))
         return float(ms.value)
+
+
+    # ---- launch-form search (fastkernel analogue) ----
+    def num_steps(self) -> int:
+        return int(lib().mlkhip_num_steps(self._h))
+
+    def step_variants(self, step: int) -> List[int]:
+        out = (ctypes.c_int * 32)()
+        n = lib().mlkhip_step_variants(self._h, step, out, 32)
+        if n < 0:
+            raise MlkHipError(BAD_BINDING, last_error())
+        return list(out[:n])
+
+    def step_variant(self, step: int) -> int:
+        return int(lib().mlkhip_step_variant(self._h, step))
+
+    def set_step_variant(self, step: int, variant: int) -> None:
+        _check(lib().mlkhip_set_step_variant(self._h, step, variant))
+
+    @property
+    def fingerprint(self) -> str:
+        return lib().mlkhip_fingerprint(self._h).decode()
+
+    @property
+    def variants_from_cache(self) -> bool:
+        return bool(lib().mlkhip_variants_from_cache(self._h))
+
+    def autotune(self, bufs: Dict[int, DeviceBuffer], scalars: Sequence[float] = (), elements: int = 0,
+                 reps: int = 10, cache_dir: Optional[str] = None) -> dict:
+        """Certifies and times every launch form of every step on `bufs`
+        (restored afterwards), keeps the fastest certified form per step and
+        returns the search report."""
+        arr, n = self._bindings(bufs)
+        sc, nsc = self._scalars(scalars)
+        cap = 1 << 16
+        rep = ctypes.create_string_buffer(cap)
+        _check(lib().mlkhip_autotune(self._h, arr, n, sc.ctypes.data_as(_PD), nsc, int(elements), int(reps),
+                                     (cache_dir or "").encode(), rep, cap))
+        return json.loads(rep.value.decode())
 
 
 def _numel(b, elements: int) -> int:

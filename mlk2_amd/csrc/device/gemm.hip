@@ -1014,8 +1014,11 @@ __global__ __launch_bounds__(256) void gemmGeneral(mlkd_gemm p) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// f16 GEMM launch variant (0: 8 waves of 128x64; 1: 4 waves of 128x128),
-// set by the variant search through mlkd_gemm_set_variant.
+// Process default of the f16 GEMM launch form (a launch's own `variant`
+// field overrides it): 0: 8 waves of 128x64; 1: 4 waves of 128x128; 2: 4
+// waves with A direct to LDS; 3: 4 waves, explicitly pipelined; 4: 8 waves,
+// loads two steps ahead (register-limited: spills, kept for measurement);
+// 5/6: 128x256 tiles, two workgroups per CU, loads two / one step ahead.
 int gGemmF16Variant = 0;
 
 }  // namespace
@@ -1026,6 +1029,7 @@ extern "C" int mlkd_launch_gemm(const mlkd_gemm* p, void* stream) {
     if (p == nullptr || p->m < 0 || p->n < 0 || p->k < 0) return MLKD_RT_LAUNCH;
     if (p->m == 0 || p->n == 0) return 0;
     hipStream_t st = static_cast<hipStream_t>(stream);
+    const int variant = p->variant >= 0 ? p->variant : gGemmF16Variant;
     const bool fits32 = p->m < (1LL << 31) && p->n < (1LL << 31) && p->k < (1LL << 31);
     if (p->k > 0 && fits32 && p->a_dtype == MLKD_F16 && p->b_dtype == MLKD_F16 &&
         p->c_dtype == MLKD_F32 && p->m % kBM == 0 && p->n % kBN == 0 && p->k % kBK == 0 &&
@@ -1050,9 +1054,9 @@ extern "C" int mlkd_launch_gemm(const mlkd_gemm* p, void* stream) {
             }
             ldsRaised = true;
         }
-        if (gGemmF16Variant == 5 || gGemmF16Variant == 6) {
+        if (variant == 5 || variant == 6) {
             const int tiles2 = static_cast<int>((p->m / kBM2) * (p->n / kBN2));
-            auto kern = gGemmF16Variant == 5
+            auto kern = variant == 5
                             ? (p->accumulate ? gemmF16Mfma2cu<true, true> : gemmF16Mfma2cu<false, true>)
                             : (p->accumulate ? gemmF16Mfma2cu<true, false> : gemmF16Mfma2cu<false, false>);
             hipLaunchKernelGGL(kern, dim3(tiles2), dim3(256), kLdsGemm2, st, static_cast<const _Float16*>(p->a),
@@ -1061,7 +1065,7 @@ extern "C" int mlkd_launch_gemm(const mlkd_gemm* p, void* stream) {
                                p->ldb, p->ldc);
             return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
         }
-        if (gGemmF16Variant == 4) {
+        if (variant == 4) {
             static bool raised4 = false;
             if (!raised4) {
                 if (hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF16Mfma3s<true>),
@@ -1080,7 +1084,7 @@ extern "C" int mlkd_launch_gemm(const mlkd_gemm* p, void* stream) {
                                static_cast<int>(p->k), p->lda, p->ldb, p->ldc, 0);
             return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
         }
-        if (gGemmF16Variant == 3) {
+        if (variant == 3) {
             const size_t ldsDirect = (2 * kTileA + 2 * kTileHalves) * sizeof(_Float16);
             static bool raised3 = false;
             if (!raised3) {
@@ -1101,7 +1105,7 @@ extern "C" int mlkd_launch_gemm(const mlkd_gemm* p, void* stream) {
                                p->ldb, p->ldc);
             return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
         }
-        if (gGemmF16Variant == 2) {
+        if (variant == 2) {
             const size_t ldsDirect = (2 * kTileA + 2 * kTileHalves) * sizeof(_Float16);
             static bool raised2 = false;
             if (!raised2) {
@@ -1121,7 +1125,7 @@ extern "C" int mlkd_launch_gemm(const mlkd_gemm* p, void* stream) {
                                static_cast<int>(p->k), p->lda, p->ldb, p->ldc, p->accumulate);
             return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
         }
-        if (gGemmF16Variant == 1) {
+        if (variant == 1) {
             hipLaunchKernelGGL((p->accumulate ? gemmF16Mfma4w<true> : gemmF16Mfma4w<false>), dim3(tiles), dim3(256), ldsBytes, st,
                                static_cast<const _Float16*>(p->a), static_cast<const _Float16*>(p->b),
                                static_cast<float*>(p->c), static_cast<int>(p->m), static_cast<int>(p->n),

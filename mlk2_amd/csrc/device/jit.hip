@@ -85,6 +85,11 @@ void writeFileAtomic(const std::string& path, const std::vector<char>& data) {
 
 extern "C" {
 
+/// hipRTC's version (part of the variant-cache fingerprint).
+int mlkd_jit_version(int* major, int* minor) {
+    return hiprtcVersion(major, minor) == HIPRTC_SUCCESS ? 0 : MLKD_RT_LAUNCH;
+}
+
 /// Compiles (or fetches) `name` from `src` for `arch`. Returns 0 and the
 /// function handle, or MLKD_RT_LAUNCH with the compiler log.
 int mlkd_jit_build(const char* src, size_t len, const char* name, const char* arch,

@@ -42,6 +42,7 @@ int mlkd_rt_event_elapsed_ms(void* start, void* stop, float* ms);
 const char* mlkd_rt_last_error(void);
 
 /// hipRTC instances of kernel templates (jit.hip).
+int mlkd_jit_version(int* major, int* minor);
 int mlkd_jit_build(const char* src, size_t len, const char* name, const char* arch,
                    const char* cache_dir, void** fn_out, uint64_t* fingerprint_out, char* log,
                    size_t cap);

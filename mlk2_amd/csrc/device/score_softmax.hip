@@ -912,16 +912,17 @@ extern "C" int mlkd_launch_score_softmax(const mlkd_score_softmax* p, void* stre
     if (p == nullptr || p->batch < 0 || p->seq < 0 || p->dim < 0) return MLKD_RT_LAUNCH;
     if (p->batch == 0 || p->seq == 0) return 0;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if ((gScoreVariant == 0 || gScoreVariant == 3 || gScoreVariant == 8) && twoPassApplies(p) &&
+    const int variant = p->variant >= 0 ? p->variant : gScoreVariant;
+    if ((variant == 0 || variant == 3 || variant == 8) && twoPassApplies(p) &&
         p->scratch != nullptr && (reinterpret_cast<uintptr_t>(p->scratch) & 7u) == 0 &&
         p->scratch_bytes >= scratch2(p)) {
-        return launchTwoPass(p, st, gScoreVariant);
+        return launchTwoPass(p, st, variant);
     }
     const bool fast = p->qk_dtype == MLKD_F16 && p->bias_dtype == MLKD_F32 && p->s_dtype == MLKD_F32 &&
                       p->seq % 128 == 0 && p->dim % 16 == 0 && p->dim > 0 && p->seq < (1 << 20) &&
                       (reinterpret_cast<uintptr_t>(p->q) & 15u) == 0 &&
                       (reinterpret_cast<uintptr_t>(p->k) & 15u) == 0 && p->dim % 8 == 0;
-    const bool fused = fast && p->seq <= 2048 && p->dim <= 256 && gScoreVariant != 1;
+    const bool fused = fast && p->seq <= 2048 && p->dim <= 256 && variant != 1;
     // Second fused form for dim 64/128 and seq a multiple of 256 (8 waves of
     // seq/256 tiles, at most 8 tiles per wave).
     if (fused && (p->dim == 128 || p->dim == 64) && p->seq % 256 == 0) {
@@ -1001,6 +1002,8 @@ extern "C" int mlkd_launch_score_softmax(const mlkd_score_softmax* p, void* stre
     }
     if (hipGetLastError() != hipSuccess) return MLKD_RT_LAUNCH;
     mlkd_softmax sm;
+    sm.variant = -1;
+    sm.pad = 0;
     sm.x = p->s;
     sm.y = p->s;
     sm.x_dtype = p->s_dtype;

@@ -236,7 +236,8 @@ int64_t gSoftmaxWaves = 0;
 
 template <int CH>
 int launchWave(const mlkd_softmax& p, hipStream_t st) {
-    if (gSoftmaxVariant == 1) {
+    const int variant = p.variant >= 0 ? p.variant : gSoftmaxVariant;
+    if (variant == 1) {
         int64_t waves = gSoftmaxWaves > 0 ? gSoftmaxWaves : 2048;
         if (waves > p.rows) waves = p.rows;
         const int64_t blocks = (waves + 3) / 4;
@@ -249,9 +250,9 @@ int launchWave(const mlkd_softmax& p, hipStream_t st) {
     if (gSoftmaxWaves > 0 && blocks > (gSoftmaxWaves + 3) / 4) blocks = (gSoftmaxWaves + 3) / 4;
     if (blocks > 8192) blocks = 8192;
     auto kern = softmaxWaveRow<CH, true, true>;
-    if (gSoftmaxVariant == 2) kern = softmaxWaveRow<CH, false, true>;
-    if (gSoftmaxVariant == 3) kern = softmaxWaveRow<CH, true, false>;
-    if (gSoftmaxVariant == 4) kern = softmaxWaveRow<CH, false, false>;
+    if (variant == 2) kern = softmaxWaveRow<CH, false, true>;
+    if (variant == 3) kern = softmaxWaveRow<CH, true, false>;
+    if (variant == 4) kern = softmaxWaveRow<CH, false, false>;
     hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, static_cast<const float*>(p.x),
                        static_cast<float*>(p.y), p.rows, p.cols, p.x_row_stride, p.y_row_stride);
     return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;

@@ -29,6 +29,8 @@ typedef struct mlkd_softmax {
     int32_t x_dtype, y_dtype;
     int64_t rows, cols;
     int64_t x_row_stride, y_row_stride;
+    int32_t variant;     /* launch form; -1: the process default */
+    int32_t pad;
 } mlkd_softmax;
 
 /// C[M,N] (+)= A[M,K] * B[K,N], row-major, leading dims in elements.
@@ -40,6 +42,8 @@ typedef struct mlkd_gemm {
     int32_t accumulate;   /* 1: C += A*B (Call form); 0: C = A*B */
     int64_t m, n, k;
     int64_t lda, ldb, ldc;
+    int32_t variant;      /* launch form; -1: the process default */
+    int32_t pad;
 } mlkd_gemm;
 
 /// S[b*seq + i, j] = softmax_j((Q[b,i,:] . K[b,j,:]) / div + bias[j]).
@@ -48,7 +52,8 @@ typedef struct mlkd_score_softmax {
     const void* k;
     const void* bias;
     void* s;
-    int32_t qk_dtype, bias_dtype, s_dtype, pad;
+    int32_t qk_dtype, bias_dtype, s_dtype;
+    int32_t variant;      /* launch form; -1: the process default */
     int64_t batch, seq, dim;
     double div;
     /* Device scratch for the two-pass form's per-tile row statistics

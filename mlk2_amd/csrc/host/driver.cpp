@@ -110,6 +110,8 @@ Result<std::unique_ptr<HipLoadedKernel>> buildHipKernelArtifact(const KernelModu
         }
         st.fn = fn;
     }
+    k->fingerprint_ = artifactFingerprint(k->km_, k->plan_, config.arch);
+    k->fromCache_ = applyCachedVariants(config.cacheDir, k->fingerprint_, k->km_, k->plan_);
     k->scratch_.assign(km.buffers.size(), nullptr);
     k->scratchElems_.assign(km.buffers.size(), 0);
     k->stepScratch_.assign(k->plan_.steps.size(), nullptr);
@@ -226,6 +228,8 @@ int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* 
             case StepKind::Softmax:
             case StepKind::RowSum: {
                 mlkd_softmax p;
+                p.variant = st.variant;
+                p.pad = 0;
                 p.x = ptr[st.x];
                 p.y = ptr[st.y];
                 p.x_dtype = dtypeCode(km_.buffers[st.x].dtype);
@@ -239,6 +243,8 @@ int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* 
             }
             case StepKind::Gemm: {
                 mlkd_gemm p;
+                p.variant = st.variant;
+                p.pad = 0;
                 p.a = ptr[st.a];
                 p.b = ptr[st.b];
                 p.c = ptr[st.c];
@@ -297,6 +303,7 @@ int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* 
             }
             case StepKind::ScoreSoftmax: {
                 mlkd_score_softmax p;
+                p.variant = st.variant;
                 p.q = ptr[st.q];
                 p.k = ptr[st.kk];
                 p.bias = ptr[st.bias];
@@ -308,7 +315,6 @@ int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* 
                 }
                 p.bias_dtype = dtypeCode(km_.buffers[st.bias].dtype);
                 p.s_dtype = dtypeCode(km_.buffers[st.s].dtype);
-                p.pad = 0;
                 p.batch = st.batch;
                 p.seq = st.seq;
                 p.dim = st.dim;
@@ -641,6 +647,72 @@ int mlkhip_time_device_span(const mlkhip_artifact* a, const mlkhip_binding* bind
     mlkd_rt_event_destroy(e0);
     mlkd_rt_event_destroy(e1);
     return rc;
+}
+
+int mlkhip_num_steps(const mlkhip_artifact* a) {
+    return a != nullptr ? static_cast<int>(a->k->plan().steps.size()) : 0;
+}
+
+namespace {
+int listVariants(const mlk::hip::KernelModule& km, const mlk::hip::Plan& plan, int step, int* out, int cap) {
+    if (step < 0 || static_cast<size_t>(step) >= plan.steps.size()) return setError(-1, "step out of range");
+    const std::vector<int> v = mlk::hip::variantSpace(km, plan.steps[static_cast<size_t>(step)]);
+    for (size_t i = 0; i < v.size() && static_cast<int>(i) < cap; ++i) {
+        if (out != nullptr) out[i] = v[i];
+    }
+    return static_cast<int>(v.size());
+}
+}  // namespace
+
+int mlkhip_step_variants(const mlkhip_artifact* a, int step, int* out, int cap) {
+    if (a == nullptr) return setError(-1, "null artifact");
+    return listVariants(a->k->module(), a->k->plan(), step, out, cap);
+}
+
+int mlkhip_plan_variants(const char* module_json, size_t len, int step, int* out, int cap) {
+    auto km = mlk::hip::parseKernelModule(module_json, len);
+    if (!km.has_value()) return setError(-1, km.error().message);
+    const mlk::hip::KernelModule dm = mlk::hip::deviceModule(*km);
+    auto plan = mlk::hip::planModule(dm);
+    if (!plan.has_value()) return setError(-1, plan.error().message);
+    return listVariants(dm, *plan, step, out, cap);
+}
+
+int mlkhip_step_variant(const mlkhip_artifact* a, int step) {
+    if (a == nullptr || step < 0 || static_cast<size_t>(step) >= a->k->plan().steps.size()) return -2;
+    return a->k->plan().steps[static_cast<size_t>(step)].variant;
+}
+
+int mlkhip_set_step_variant(mlkhip_artifact* a, int step, int variant) {
+    if (a == nullptr) return setError(MLKHIP_BAD_BINDING, "null artifact");
+    std::string why;
+    const int rc = a->k->setStepVariant(step, variant, why);
+    return rc == MLKHIP_OK ? rc : setError(rc, why);
+}
+
+const char* mlkhip_fingerprint(const mlkhip_artifact* a) {
+    return a != nullptr ? a->k->fingerprint().c_str() : "";
+}
+
+int mlkhip_variants_from_cache(const mlkhip_artifact* a) {
+    return a != nullptr && a->k->variantsFromCache() ? 1 : 0;
+}
+
+int mlkhip_autotune(mlkhip_artifact* a, const mlkhip_binding* binds, int n_binds, const double* scalars,
+                    int64_t n_scalars, int64_t elements, int reps, const char* cache_dir, char* report,
+                    size_t report_cap) {
+    if (a == nullptr) return setError(MLKHIP_BAD_BINDING, "null artifact");
+    std::vector<mlk::hip::DeviceBinding> b(static_cast<size_t>(n_binds > 0 ? n_binds : 0));
+    for (int i = 0; i < n_binds; ++i) {
+        b[static_cast<size_t>(i)].ptr = binds[i].ptr;
+        b[static_cast<size_t>(i)].elements = binds[i].elements;
+        b[static_cast<size_t>(i)].dtype = binds[i].dtype;
+    }
+    std::string why, rep;
+    const int rc = a->k->autotune(b.data(), n_binds, scalars, n_scalars, elements, reps,
+                                  cache_dir != nullptr ? cache_dir : "", rep, why);
+    copyOut(report, report_cap, rep);
+    return rc == MLKHIP_OK ? rc : setError(rc, why);
 }
 
 int mlkhip_malloc(void** p, size_t bytes) { return mlkd_rt_malloc(p, bytes); }

@@ -50,12 +50,33 @@ public:
     int runHost(double* const* ptrs, int n, const double* scalars, int64_t nScalars,
                 int64_t elements, std::string& why) const;
 
+    /// Fingerprint of the variant cache entry (module hash, target, hipRTC
+    /// version, policy, device) and whether the build applied a cached entry.
+    const std::string& fingerprint() const { return fingerprint_; }
+    bool variantsFromCache() const { return fromCache_; }
+
+    /// Pins step `step` to launch form `variant` (-1: the kernel's default);
+    /// refuses a form outside the step's variant space.
+    int setStepVariant(int step, int variant, std::string& why);
+
+    /// Times every launch form of every step that has more than one on the
+    /// caller's device buffers, certifies each against the default form's
+    /// outputs, keeps the fastest certified form per step and, when
+    /// `cacheDir` is not empty, stores the choice under the fingerprint. The
+    /// written buffers are snapshotted first and restored before returning.
+    /// `report` receives a JSON document of every candidate.
+    int autotune(const DeviceBinding* binds, int n, const double* scalars, int64_t nScalars,
+                 int64_t elements, int reps, const std::string& cacheDir, std::string& report,
+                 std::string& why);
+
 private:
     friend Result<std::unique_ptr<HipLoadedKernel>> buildHipKernelArtifact(
         const KernelModule& km, const HipBackendDriverConfig& config);
     KernelModule km_;
     Plan plan_;
     std::string arch_;
+    std::string fingerprint_;
+    bool fromCache_{false};
     std::vector<uint32_t> bindables_;   // buffer ids in table order
     std::vector<int> bindIndex_;        // buffer id -> bindable index or -1
     // Artifact-owned temp scratch (allocated on first use, kept; zeroed on
@@ -70,6 +91,19 @@ private:
     mutable std::vector<void*> stepScratch_;
     mutable std::vector<int64_t> stepScratchBytes_;
 };
+
+/// Launch forms a step's hand-written kernel offers for its shape (empty
+/// when there is only the default); the first entry is the default form.
+std::vector<int> variantSpace(const KernelModule& km, const Step& st);
+
+/// Variant-cache fingerprint of a planned module on device 0.
+std::string artifactFingerprint(const KernelModule& km, const Plan& plan, const std::string& arch);
+
+/// Applies <dir>/fk-<fingerprint>.json to the plan's steps when the file
+/// exists, names the same fingerprint and lists a form of each step's
+/// variant space; returns whether it applied.
+bool applyCachedVariants(const std::string& dir, const std::string& fingerprint, const KernelModule& km,
+                         Plan& plan);
 
 /// Plans, instantiates and loads (buildGpuKernelArtifact analogue).
 Result<std::unique_ptr<HipLoadedKernel>> buildHipKernelArtifact(const KernelModule& km,

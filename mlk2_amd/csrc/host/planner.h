@@ -68,6 +68,10 @@ struct Step {
     bool narrowRoundTrip{false};
     bool touchesF16{false};
 
+    // Launch form of a hand-written kernel (-1: the kernel's default); set
+    // by mlkhip_set_step_variant, the variant search or its cache.
+    int variant{-1};
+
     // Fail: the step reports this ABI code at run time (1 = negative store
     // address, as the reference walker's InvalidGraph at execution).
     int failCode{0};

@@ -117,3 +117,21 @@ def test_chain_codegen_exact_constants():
     _, src = be.compile_check(km, 0, "gfx950")
     assert "0x1.999999999999ap-4" in src
     assert "(-__builtin_inf())" in src
+
+
+@pytest.mark.parametrize("km,space", [
+    (fx.config2_module(8192, 4096, 2), [0, 2, 3, 4, 1]),
+    (fx.config4_module(4096, 4096, 4096, "f16", 2), [0, 1, 2, 3, 5, 6]),
+    (fx.score_softmax_module(16, 2048, 128), [0, 3, 2, 1]),
+    (fx.score_softmax_module(2, 4096, 128), [0, 3, 1]),
+    (fx.config4_module(1024, 1024, 1024, "f32", 2), []),
+    (fx.config1_module(1 << 12), []),
+    (fx.config4_module(64, 64, 64, "f16", 1), []),     # below the 256-multiple tiles
+])
+def test_declared_variant_space(km, space):
+    assert be.plan_variants(km, 0) == space
+
+
+def test_variant_space_step_out_of_range():
+    with pytest.raises(be.MlkHipError):
+        be.plan_variants(fx.config2_module(64, 128, 2), 3)

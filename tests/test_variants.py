@@ -1,0 +1,169 @@
+"""Launch-form search (the fastkernel analogue) on the device, through the C
+ABI: every declared form of every searched kernel meets the path's
+tolerance against the oracle; the search certifies, times and picks among
+them without disturbing the caller's buffers; its choice is cached under the
+artifact's fingerprint and applied by a later build.
+
+Tolerances as in test_gpu_parity: softmax <= 1e-6 relative; f16 GEMM and
+score+softmax <= 1e-2 relative (|got-ref|/max(|ref|,1)).
+"""
+import math
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from mlk2_amd import fixtures as fx
+from mlk2_amd import inputs
+from mlk2_amd.backend import DeviceBuffer, MlkHipError
+from mlk2_amd.parity import max_rel
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(f"[gpu] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def _gemm_ref(A, B):
+    m, k = A.shape
+    call = fx.matmul_call_module(m, k, B.shape[1], "f64", "f64")
+    return oracle.run(call, {0: A, 1: B}, hw_threads=8)[2].reshape(m, B.shape[1])
+
+
+def _score_ref(Q, K, bias):
+    B, S, D = Q.shape
+    out = []
+    for b in range(B):
+        sc = _gemm_ref(Q[b].astype(np.float64), np.ascontiguousarray(K[b].astype(np.float64).T))
+        sc = sc / math.sqrt(D) + bias.astype(np.float64)
+        out.append(oracle.run(fx.softmax_call_module(S, S, "f64"), {0: sc})[1].reshape(S, S))
+    return np.concatenate(out)
+
+
+def _softmax_case(m=512, k=4096):
+    x = inputs.normal(inputs.SEEDS["c2_x"], m * k, 0.0, 2.0).reshape(m, k)
+    km = fx.config2_module(m, k, 2)
+    ref = oracle.run(fx.config2_module(m, k, 1), {0: x})[1]
+    bufs = {0: DeviceBuffer.from_array(x, "f32"), 1: DeviceBuffer(m * k, "f32")}
+    return km, bufs, 1, ref, 1e-6
+
+
+def _gemm_case(m=512, k=1024, n=512):
+    d = inputs.config_inputs("c4b", {"m": m, "k": k, "n": n})
+    km = fx.config4_module(m, k, n, "f16", 2)
+    ref = _gemm_ref(d["A"].astype(np.float64), d["B"].astype(np.float64)).reshape(-1)
+    bufs = {0: DeviceBuffer.from_array(d["A"], "f16"), 1: DeviceBuffer.from_array(d["B"], "f16"),
+            2: DeviceBuffer(m * n, "f32")}
+    return km, bufs, 2, ref, 1e-2
+
+
+def _score_case(b=2, s=512, dm=128):
+    d = inputs.config_inputs("c5", {"batch": b, "seq": s, "dim": dm})
+    km = fx.score_softmax_module(b, s, dm)
+    ref = _score_ref(d["Q"], d["K"], d["bias"]).reshape(-1)
+    bufs = {0: DeviceBuffer.from_array(d["Q"], "f16"), 1: DeviceBuffer.from_array(d["K"], "f16"),
+            2: DeviceBuffer.from_array(d["bias"], "f32"), 3: DeviceBuffer(b * s * s, "f32")}
+    return km, bufs, 3, ref, 1e-2
+
+
+CASES = {
+    "softmax-512x4096": _softmax_case,
+    "gemm-f16-512x1024x512": _gemm_case,
+    "score-2x512x128": _score_case,
+    "score-1x2048x128": lambda: _score_case(1, 2048, 128),
+}
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_every_declared_form_meets_tolerance(hip, name):
+    km, bufs, out, ref, tol = CASES[name]()
+    art = hip.build(km)
+    space = art.step_variants(0)
+    assert len(space) >= 2, name
+    for v in space:
+        say(f"variants {name} form {v}")
+        art.set_step_variant(0, v)
+        assert art.step_variant(0) == v
+        bufs[out].fill_zero()
+        art.run_device(bufs)
+        e = max_rel(bufs[out].to_numpy(), ref)
+        say(f"variants {name} form {v} max_rel={e:.3e}")
+        assert e <= tol, (name, v)
+
+
+def test_set_variant_outside_space_refused(hip):
+    km, _, _, _, _ = _softmax_case(64, 256)
+    art = hip.build(km)
+    with pytest.raises(MlkHipError):
+        art.set_step_variant(0, 99)
+    with pytest.raises(MlkHipError):
+        art.set_step_variant(5, 0)
+    art.set_step_variant(0, -1)
+    assert art.step_variant(0) == -1
+    assert art.step_variant(7) == -2
+
+
+@pytest.mark.parametrize("name", ["softmax-512x4096", "gemm-f16-512x1024x512", "score-2x512x128"])
+def test_autotune_certifies_restores_and_caches(hip, name, tmp_path):
+    km, bufs, out, ref, tol = CASES[name]()
+    # A sentinel in the output: the search must hand the buffer back as it was.
+    n_out = bufs[out].elements
+    sentinel = np.full(n_out, 0.75, dtype=np.float32)
+    bufs[out].free()
+    bufs[out] = DeviceBuffer.from_array(sentinel, "f32")
+    art = hip.build(km, cache_dir=str(tmp_path))
+    assert not art.variants_from_cache
+    fp = art.fingerprint
+    assert len(fp) == 16
+    say(f"autotune {name} start")
+    rep = art.autotune(bufs, reps=5, cache_dir=str(tmp_path))
+    say(f"autotune {name} chose {rep['variants']}")
+    assert rep["fingerprint"] == fp
+    assert rep["combined_certified"] is True
+    assert np.array_equal(bufs[out].to_numpy(), sentinel)
+    (step,) = rep["steps"]
+    space = art.step_variants(0)
+    assert [c["variant"] for c in step["candidates"]] == space
+    assert step["chosen"] in space
+    chosen = [c for c in step["candidates"] if c["variant"] == step["chosen"]][0]
+    assert chosen["admissible"] and chosen["certificate"]["identity"]["certified"]
+    rt = chosen["certificate"]["runtime"]
+    assert 0 < rt["min_sec"] <= rt["upper_bound_sec"] <= rt["max_sec"]
+    for c in step["candidates"]:
+        if c["admissible"]:
+            assert c["certificate"]["runtime"]["upper_bound_sec"] >= rt["upper_bound_sec"]
+        else:
+            assert c["rejected"]["reason"] in ("identity-mismatch", "build-failed")
+    assert art.step_variant(0) == step["chosen"]
+    # The chosen form meets the path's tolerance against the oracle.
+    bufs[out].fill_zero()
+    art.run_device(bufs)
+    assert max_rel(bufs[out].to_numpy(), ref) <= tol
+    # A second build with the same cache directory applies the choice.
+    assert rep["cache"]["file"].endswith(f"fk-{fp}.json")
+    art2 = hip.build(km, cache_dir=str(tmp_path))
+    assert art2.fingerprint == fp
+    assert art2.variants_from_cache
+    assert art2.step_variant(0) == step["chosen"]
+    # Another shape has another fingerprint and ignores the entry.
+    km3, _, _, _, _ = (_softmax_case(256, 4096) if name.startswith("softmax") else
+                       _gemm_case(256, 1024, 512) if name.startswith("gemm") else _score_case(1, 512, 128))
+    art3 = hip.build(km3, cache_dir=str(tmp_path))
+    assert art3.fingerprint != fp
+    assert not art3.variants_from_cache
+
+
+def test_autotune_without_variants_is_a_no_op(hip):
+    # An f32 GEMM has one form: the search times nothing and keeps defaults.
+    m = k = n = 256
+    d = inputs.config_inputs("c4a", {"m": m, "k": k, "n": n})
+    km = fx.config4_module(m, k, n, "f32", 2)
+    art = hip.build(km)
+    bufs = {0: DeviceBuffer.from_array(d["A"], "f32"), 1: DeviceBuffer.from_array(d["B"], "f32"),
+            2: DeviceBuffer(m * n, "f32")}
+    rep = art.autotune(bufs, reps=3)
+    assert rep["steps"] == [] and rep["variants"] == [-1]
+    assert rep["cache"]["file"] == ""
