@@ -867,6 +867,187 @@ __global__ __launch_bounds__(256) void gemmF16Mfma4wPipe(const _Float16* __restr
     }
 }
 
+/// Variant 7: both operands moved global -> LDS by the gfx950 direct path
+/// (global_load_lds_dwordx4, no VGPR staging) into a 4-deep ring of K steps
+/// of 32; B is kept as loaded ([k][n]) and read with ds_read_b64_tr_b16,
+/// which hands each lane 4 consecutive k of one column, i.e. the MFMA B
+/// operand without a register transpose. 4 waves (2 x 2), each owning a
+/// 128 x 128 quadrant (4 x 4 MFMA tiles, 256 accumulators). The fragments of
+/// the next 16-deep sub-step are read while the current one's 16 MFMAs run
+/// (one LDS read per MFMA). One barrier per K step certifies the next stage;
+/// every step issues exactly one stage (past the end a harmless reload into
+/// a slot nothing reads), so the wait before the barrier is a constant
+/// vmcnt. The direct loads are inline asm: the kernel accounts for them
+/// itself, so the compiler adds no conservative waits on them.
+/// LDS swizzles: A rows are 64 bytes (4 chunks), chunk c of row r sits at
+/// c ^ ((r >> 2) & 3); B rows are 512 bytes, chunk c of k-row r sits at
+/// c ^ ((r & 3) * 4). Both measured conflict-free (SQ_LDS_BANK_CONFLICT 0).
+constexpr int kDmaBK = 32, kDmaStages = 4;
+constexpr int kDmaA = 256 * kDmaBK;                   // halves per A stage
+constexpr int kDmaStage = 2 * kDmaA;                  // A then B
+constexpr size_t kLdsDma = static_cast<size_t>(kDmaStages) * kDmaStage * sizeof(_Float16);   // 128 KiB
+constexpr int kDmaPerWave = 8;                        // direct loads per wave per stage
+
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef __fp16 fp16x4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
+
+__device__ __forceinline__ uint32_t ldsOffset(const void* p) {
+    // Generic pointers into LDS carry the LDS offset in their low 32 bits.
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
+}
+
+/// 16 bytes per lane from `src` to LDS `dst` + 16 * lane; `dst` is the same
+/// for the whole wave and goes through M0.
+__device__ __forceinline__ void dmaLoad16(const _Float16* src, const _Float16* dst) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(ldsOffset(dst));
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+}
+
+struct DmaFrag {
+    f16x8 a[4];
+    f16x4 b[4][2];
+};
+
+template <bool ACC>
+__global__ __launch_bounds__(256, 1) void gemmF16Dma(const _Float16* __restrict__ A,
+                                                     const _Float16* __restrict__ B,
+                                                     float* __restrict__ C, int M, int N, int K,
+                                                     int64_t lda, int64_t ldb, int64_t ldc) {
+    extern __shared__ __align__(16) _Float16 lds[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    int tm, tn;
+    xcdTile(M / kBM, N / kBN, tm, tn);
+    const int64_t row0 = static_cast<int64_t>(tm) * kBM;
+    const int64_t col0 = static_cast<int64_t>(tn) * kBN;
+    const int steps = K / kDmaBK;
+
+    // Stage `slot` receives K step min(slot, steps - 1) in ring slot
+    // slot % kDmaStages. Wave w issues A instructions 4w..4w+3 (16 rows
+    // each) and B instructions 4w..4w+3 (2 k-rows each).
+    auto issue = [&](int slot) {
+        const int k0 = min(slot, steps - 1) * kDmaBK;
+        const _Float16* st = lds + (slot % kDmaStages) * kDmaStage;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int ins = wave * 4 + j;
+            const int q = ins * 64 + lane;
+            const int row = q >> 2;
+            const int c = (q & 3) ^ ((row >> 2) & 3);
+            dmaLoad16(A + (row0 + row) * lda + k0 + c * 8, st + ins * 512);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int ins = wave * 4 + j;
+            const int q = ins * 64 + lane;
+            const int krow = q >> 5;
+            const int c = (q & 31) ^ ((krow & 3) * 4);
+            dmaLoad16(B + static_cast<int64_t>(k0 + krow) * ldb + col0 + c * 8, st + kDmaA + ins * 512);
+        }
+    };
+
+    f32x16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < kDmaStages - 1; ++s) issue(s);
+
+    const int l32 = lane & 31, hl = lane >> 5;
+    const int g = lane >> 4, sl = lane & 15;
+    // Lane byte offsets inside a stage. A: per sub-step kk (tile i adds 32
+    // rows = 2048 bytes). B: per (kk, j, h) for the two 4-deep halves of the
+    // transposed read (lanes of group g read k-rows 8 * (g >> 1) + sl / 4).
+    uint32_t offA[2], offB[2][4][2];
+    {
+        const int row = wm * 128 + l32;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) offA[kk] = 2u * (row * kDmaBK + (((kk * 2 + hl) ^ ((row >> 2) & 3)) * 8));
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int krow = kk * 16 + 8 * (g >> 1) + (sl >> 2) + 4 * h;
+                    const int col = wn * 128 + j * 32 + 16 * (g & 1) + 4 * (sl & 3);
+                    offB[kk][j][h] = 2u * (kDmaA + krow * 256 + (((col >> 3) ^ ((krow & 3) * 4)) * 8) + (col & 7));
+                }
+            }
+        }
+    }
+    const uint32_t ldsBase = ldsOffset(lds);
+    // Read r of a sub-step: r 0..3 the A tiles, r 4..11 the B halves (j, h).
+    auto readOne = [&](DmaFrag& f, uint32_t base, int kk, int r) {
+        if (r < 4) {
+            f.a[r] = *reinterpret_cast<const __attribute__((address_space(3))) f16x8*>(base + offA[kk] + 2048u * r);
+        } else {
+            const int j = (r - 4) >> 1, h = (r - 4) & 1;
+            const fp16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                reinterpret_cast<__attribute__((address_space(3))) fp16x4*>(base + offB[kk][j][h]));
+            f.b[j][h] = __builtin_bit_cast(f16x4, v);
+        }
+    };
+    auto mfma = [&](const DmaFrag& f, int idx) {
+        const int i = idx >> 2, j = idx & 3;
+        const f16x8 bb = __builtin_shufflevector(f.b[j][0], f.b[j][1], 0, 1, 2, 3, 4, 5, 6, 7);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[i], bb, acc[i][j], 0, 0, 0);
+    };
+    // 16 MFMAs of `cur` with the 12 reads of the next sub-step between them.
+    auto subStep = [&](DmaFrag& cur, DmaFrag& nxt, uint32_t nbase, int nkk) {
+#pragma unroll
+        for (int idx = 0; idx < 16; ++idx) {
+            mfma(cur, idx);
+            if (idx < 12) readOne(nxt, nbase, nkk, idx);
+        }
+#pragma unroll
+        for (int idx = 0; idx < 12; ++idx) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    };
+
+    DmaFrag x, y;
+    // Stage 0 landed (stages 1 and 2 may be in flight).
+    asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    asm volatile("s_barrier" ::: "memory");
+#pragma unroll
+    for (int r = 0; r < 12; ++r) readOne(x, ldsBase, 0, r);
+    for (int s = 0; s < steps; ++s) {
+        const uint32_t cb = ldsBase + 2u * static_cast<uint32_t>((s % kDmaStages) * kDmaStage);
+        subStep(x, y, cb, 1);   // sub-step (s, 0); reads (s, 1)
+        // Stage s + 1 landed (one later stage may be in flight); after the
+        // barrier every wave is past step s - 1, so its slot can be refilled.
+        asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        asm volatile("s_barrier" ::: "memory");
+        issue(s + kDmaStages - 1);
+        const uint32_t nb = ldsBase + 2u * static_cast<uint32_t>(((s + 1) % kDmaStages) * kDmaStage);
+        subStep(y, x, nb, 0);   // sub-step (s, 1); reads (s + 1, 0)
+    }
+    // No direct load may still be writing LDS when the workgroup ends.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t cBase = col0 + wn * 128 + j * 32 + l32;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int64_t row = row0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * hl + (r & 3);
+                float* dst = C + row * ldc + cBase;
+                const float v = acc[i][j][r];
+                *dst = ACC ? *dst + v : v;
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------- f32 ----
 constexpr int kFM = 64, kFN = 64, kFK = 32;
 
@@ -1018,8 +1199,10 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 // field overrides it): 0: 8 waves of 128x64; 1: 4 waves of 128x128; 2: 4
 // waves with A direct to LDS; 3: 4 waves, explicitly pipelined; 4: 8 waves,
 // loads two steps ahead (register-limited: spills, kept for measurement);
-// 5/6: 128x256 tiles, two workgroups per CU, loads two / one step ahead.
-int gGemmF16Variant = 0;
+// 5/6: 128x256 tiles, two workgroups per CU, loads two / one step ahead;
+// 7: 4 waves, both operands direct to a 4-deep LDS ring, B read transposed
+// (measured fastest on gfx950).
+int gGemmF16Variant = 7;
 
 }  // namespace
 
@@ -1053,6 +1236,25 @@ extern "C" int mlkd_launch_gemm(const mlkd_gemm* p, void* stream) {
                 return MLKD_RT_LAUNCH;
             }
             ldsRaised = true;
+        }
+        if (variant == 7) {
+            static bool raised7 = false;
+            if (!raised7) {
+                if (hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF16Dma<true>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        static_cast<int>(kLdsDma)) != hipSuccess ||
+                    hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF16Dma<false>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        static_cast<int>(kLdsDma)) != hipSuccess) {
+                    return MLKD_RT_LAUNCH;
+                }
+                raised7 = true;
+            }
+            hipLaunchKernelGGL((p->accumulate ? gemmF16Dma<true> : gemmF16Dma<false>), dim3(tiles), dim3(256),
+                               kLdsDma, st, static_cast<const _Float16*>(p->a), static_cast<const _Float16*>(p->b),
+                               static_cast<float*>(p->c), static_cast<int>(p->m), static_cast<int>(p->n),
+                               static_cast<int>(p->k), p->lda, p->ldb, p->ldc);
+            return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
         }
         if (variant == 5 || variant == 6) {
             const int tiles2 = static_cast<int>((p->m / kBM2) * (p->n / kBN2));

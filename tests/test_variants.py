@@ -16,7 +16,7 @@ import pytest
 import oracle
 from mlk2_amd import fixtures as fx
 from mlk2_amd import inputs
-from mlk2_amd.backend import DeviceBuffer, MlkHipError
+from mlk2_amd.backend import DeviceBuffer, MlkHipError, lib
 from mlk2_amd.parity import max_rel
 
 pytestmark = pytest.mark.gpu
@@ -69,7 +69,28 @@ def _score_case(b=2, s=512, dm=128):
     return km, bufs, 3, ref, 1e-2
 
 
+def _gemm_call_acc_case(m=256, k=128, n=512):
+    # Call(MatMul) adds into C (kernel_buffers.cpp:406-432): the accumulate
+    # form of every kernel.
+    d = inputs.config_inputs("c4b", {"m": m, "k": k, "n": n})
+    c0 = inputs.uniform(9, m * n, -1, 1)
+    km = fx.matmul_call_module(m, k, n, "f16", "f32")
+    ref = oracle.run(km, {0: d["A"], 1: d["B"]}, init={2: c0})[2]
+
+    class InitialC(DeviceBuffer):
+        """The output buffer; "zeroing" it restores the initial C."""
+
+        def fill_zero(self):
+            host = np.ascontiguousarray(c0.astype(np.float32))
+            assert lib().mlkhip_memcpy_h2d(self.ptr, host.ctypes.data, self.nbytes) == 0
+
+    out = InitialC(m * n, "f32")
+    bufs = {0: DeviceBuffer.from_array(d["A"], "f16"), 1: DeviceBuffer.from_array(d["B"], "f16"), 2: out}
+    return km, bufs, 2, ref, 1e-2
+
+
 CASES = {
+    "gemm-f16-call-accumulate": _gemm_call_acc_case,
     "softmax-512x4096": _softmax_case,
     "gemm-f16-512x1024x512": _gemm_case,
     "score-2x512x128": _score_case,
