@@ -194,6 +194,37 @@ int mlkhip_autotune(mlkhip_artifact* a, const mlkhip_binding* binds, int n_binds
                     int64_t n_scalars, int64_t elements, int reps, const char* cache_dir, char* report,
                     size_t report_cap);
 
+/* ---- run route (the ExecutionEngine hook of `mlkc run`) ---------------- */
+/* `mlkc run` reaches only the CPU executor (tools/mlkc/mlkc.cpp:206-263,
+ * runtime/src/execution/execution.cpp:195-256). These two entries are what
+ * an ExecutionEngine hook behind a `--backend=hip` flag calls in place of
+ * the CPU executor, falling back to Tier 0 on any nonzero code. Each builds
+ * the module for `arch` on first use and keeps the artifact in a
+ * process-wide cache keyed by target and module text. */
+
+/* Replaces executeKernelOnBuffers (runtime/include/mlk/runtime/execution.h:
+ * 113-140, kernel_buffers.cpp:839-1106) with KernelBufferBindings spelled
+ * out: dense f64 host buffers, an input buffer id indexing `inputs` and an
+ * output buffer id indexing `outputs` after the input count, as the
+ * reference resolves them (kernel_buffers.cpp:200-230); temps are the
+ * artifact's. Outputs are read and written (+= and max stores). An unbound
+ * buffer is MLKHIP_BAD_BINDING (the reference would skip its stores).
+ * Synchronous; returns a status code. */
+int mlkhip_execute_kernel_on_buffers(const char* module_json, size_t len, const char* arch, double* const* inputs,
+                                     int n_inputs, double* const* outputs, int n_outputs, const double* scalars,
+                                     int64_t n_scalars, int64_t elements);
+
+/* Replaces executeKernel (execution.cpp:195-256), the scalar ABI: inputs
+ * are the ScalarParams in value-id order, each output buffer gets its own
+ * f64 slots, element 0 of output buffer i goes to output_scalars[i], one
+ * instance. A module with input buffers is MLKHIP_REFUSED, as there. */
+int mlkhip_execute_kernel(const char* module_json, size_t len, const char* arch, const double* input_scalars,
+                          int n_inputs, double* output_scalars, int n_outputs);
+
+/* Number of artifacts the execute entries hold, and releasing them. */
+int mlkhip_execute_cache_size(void);
+void mlkhip_execute_cache_clear(void);
+
 /* ---- device memory plumbing for hosts without another HIP runtime ----- */
 int mlkhip_malloc(void** p, size_t bytes);
 int mlkhip_free(void* p);

@@ -94,6 +94,12 @@ def lib():
     L.mlkhip_variants_from_cache.argtypes = [c.c_void_p]
     L.mlkhip_autotune.argtypes = [c.c_void_p, c.POINTER(Binding), c.c_int, _PD, c.c_int64, c.c_int64,
                                   c.c_int, c.c_char_p, c.c_char_p, c.c_size_t]
+    L.mlkhip_execute_kernel_on_buffers.argtypes = [c.c_char_p, c.c_size_t, c.c_char_p, c.POINTER(_PD), c.c_int,
+                                                   c.POINTER(_PD), c.c_int, _PD, c.c_int64, c.c_int64]
+    L.mlkhip_execute_kernel.argtypes = [c.c_char_p, c.c_size_t, c.c_char_p, _PD, c.c_int, _PD, c.c_int]
+    L.mlkhip_execute_cache_size.argtypes = []
+    L.mlkhip_execute_cache_clear.argtypes = []
+    L.mlkhip_execute_cache_clear.restype = None
     L.mlkhip_malloc.argtypes = [c.POINTER(c.c_void_p), c.c_size_t]
     L.mlkhip_free.argtypes = [c.c_void_p]
     L.mlkhip_memcpy_h2d.argtypes = [c.c_void_p, c.c_void_p, c.c_size_t]
@@ -152,6 +158,40 @@ def plan_variants(km: KernelModule, step: int = 0) -> List[int]:
     if n < 0:
         raise MlkHipError(REFUSED, last_error())
     return list(out[:n])
+
+
+def _f64(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.float64).reshape(-1))
+
+
+def execute_kernel_on_buffers(km: KernelModule, inputs: Sequence[np.ndarray], outputs: Sequence[np.ndarray],
+                              scalars: Sequence[float] = (), elements: int = 0, arch: str = "gfx950") -> None:
+    """executeKernelOnBuffers analogue (the run route): dense f64 host arrays,
+    inputs in input-buffer order, outputs in output-buffer order; each output
+    must be a C-contiguous float64 array and is updated in place."""
+    for o in outputs:
+        if not (isinstance(o, np.ndarray) and o.dtype == np.float64 and o.flags.c_contiguous):
+            raise MlkHipError(BAD_BINDING, "outputs must be C-contiguous float64 arrays")
+    ins = [_f64(a) for a in inputs]
+    data = km.to_json().encode()
+    pin = (_PD * max(1, len(ins)))(*[a.ctypes.data_as(_PD) for a in ins])
+    pout = (_PD * max(1, len(outputs)))(*[o.ctypes.data_as(_PD) for o in outputs])
+    sc = np.asarray(list(scalars) or [0.0], dtype=np.float64)
+    _check(lib().mlkhip_execute_kernel_on_buffers(data, len(data), arch.encode(), pin, len(ins), pout,
+                                                  len(outputs), sc.ctypes.data_as(_PD), len(scalars),
+                                                  int(elements)))
+
+
+def execute_kernel(km: KernelModule, input_scalars: Sequence[float], arch: str = "gfx950") -> List[float]:
+    """executeKernel analogue (scalar ABI): ScalarParams in, element 0 of
+    each output buffer out."""
+    data = km.to_json().encode()
+    n_out = sum(1 for b in km.buffers if b.is_output)
+    out = np.zeros(max(1, n_out), dtype=np.float64)
+    sc = np.asarray(list(input_scalars) or [0.0], dtype=np.float64)
+    _check(lib().mlkhip_execute_kernel(data, len(data), arch.encode(), sc.ctypes.data_as(_PD), len(input_scalars),
+                                       out.ctypes.data_as(_PD), n_out))
+    return [float(v) for v in out[:n_out]]
 
 
 class DeviceBuffer:

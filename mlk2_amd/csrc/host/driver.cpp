@@ -4,6 +4,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <unordered_map>
 
 #include "../device/runtime_abi.h"
 #include "../../../include/mlk_hip.h"
@@ -713,6 +714,122 @@ int mlkhip_autotune(mlkhip_artifact* a, const mlkhip_binding* binds, int n_binds
                                   cache_dir != nullptr ? cache_dir : "", rep, why);
     copyOut(report, report_cap, rep);
     return rc == MLKHIP_OK ? rc : setError(rc, why);
+}
+
+}  // extern "C"
+
+namespace {
+/// Artifacts built by the execute entries, keyed by target and module text:
+/// an ExecutionEngine hook calls per graph run and must not rebuild.
+struct ExecCache {
+    std::mutex lock;
+    std::unordered_map<std::string, std::unique_ptr<mlk::hip::HipLoadedKernel>> map;
+};
+
+ExecCache& execCache() {
+    static ExecCache c;
+    return c;
+}
+
+int cachedArtifact(const char* module_json, size_t len, const char* arch, mlk::hip::HipLoadedKernel** out) {
+    if (module_json == nullptr || arch == nullptr) return setError(MLKHIP_REFUSED, "null argument");
+    std::string key = std::string(arch) + '\n';
+    key.append(module_json, len);
+    ExecCache& c = execCache();
+    std::lock_guard<std::mutex> g(c.lock);
+    auto it = c.map.find(key);
+    if (it == c.map.end()) {
+        auto km = mlk::hip::parseKernelModule(module_json, len);
+        if (!km.has_value()) return setError(MLKHIP_REFUSED, km.error().message);
+        mlk::hip::HipBackendDriverConfig cfg;
+        cfg.arch = arch;
+        auto k = mlk::hip::buildHipKernelArtifact(*km, cfg);
+        if (!k.has_value()) {
+            const bool noDevice = k.error().message.find("no HIP device") != std::string::npos;
+            return setError(noDevice ? MLKHIP_NO_DEVICE : mapBuildError(k.error().code), k.error().message);
+        }
+        it = c.map.emplace(std::move(key), std::move(*k)).first;
+    }
+    *out = it->second.get();
+    return MLKHIP_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int mlkhip_execute_kernel_on_buffers(const char* module_json, size_t len, const char* arch, double* const* inputs,
+                                     int n_inputs, double* const* outputs, int n_outputs, const double* scalars,
+                                     int64_t n_scalars, int64_t elements) {
+    mlk::hip::HipLoadedKernel* k = nullptr;
+    if (const int rc = cachedArtifact(module_json, len, arch, &k); rc != MLKHIP_OK) return rc;
+    // The reference resolves a buffer id through the table layout (inputs
+    // first, then outputs): an input id indexes `inputs`, an output id
+    // indexes `outputs` after the input count (kernel_buffers.cpp:200-230).
+    // Temps are the artifact's own scratch.
+    const mlk::hip::KernelModule& km = k->module();
+    std::vector<double*> ptrs;
+    for (const uint32_t b : k->bindables()) {
+        const mlk::hip::KernelBuffer& kb = km.buffers[b];
+        double* p = nullptr;
+        if (kb.isTemp) {
+            p = nullptr;
+        } else if (kb.isInput) {
+            if (static_cast<int>(b) >= n_inputs || inputs == nullptr) {
+                return setError(MLKHIP_BAD_BINDING, "input buffer " + std::to_string(b) + " is not bound");
+            }
+            p = inputs[b];
+        } else {
+            const int o = static_cast<int>(b) - n_inputs;
+            if (o < 0 || o >= n_outputs || outputs == nullptr) {
+                return setError(MLKHIP_BAD_BINDING, "output buffer " + std::to_string(b) + " is not bound");
+            }
+            p = outputs[o];
+        }
+        if (!kb.isTemp && p == nullptr) {
+            return setError(MLKHIP_BAD_BINDING, "buffer " + std::to_string(b) + " is bound to NULL");
+        }
+        ptrs.push_back(p);
+    }
+    std::string why;
+    const int rc = k->runHost(ptrs.data(), static_cast<int>(ptrs.size()), scalars, n_scalars, elements, why);
+    return rc == MLKHIP_OK ? rc : setError(rc, why);
+}
+
+int mlkhip_execute_kernel(const char* module_json, size_t len, const char* arch, const double* input_scalars,
+                          int n_inputs, double* output_scalars, int n_outputs) {
+    mlk::hip::HipLoadedKernel* k = nullptr;
+    if (const int rc = cachedArtifact(module_json, len, arch, &k); rc != MLKHIP_OK) return rc;
+    const mlk::hip::KernelModule& km = k->module();
+    std::vector<std::vector<double>> slots;
+    for (const mlk::hip::KernelBuffer& kb : km.buffers) {
+        if (kb.isInput) {
+            return setError(MLKHIP_REFUSED, "tensor kernel requires buffer bindings, not scalar inputs");
+        }
+        if (kb.isOutput) slots.emplace_back(static_cast<size_t>(kb.elements > 0 ? kb.elements : 1), 0.0);
+    }
+    if (slots.empty()) return setError(MLKHIP_REFUSED, "kernel module has no output buffer");
+    if (n_outputs != static_cast<int>(slots.size()) || output_scalars == nullptr) {
+        return setError(MLKHIP_BAD_BINDING, "expected " + std::to_string(slots.size()) + " output slots");
+    }
+    std::vector<double*> outs;
+    for (auto& sl : slots) outs.push_back(sl.data());
+    const int rc = mlkhip_execute_kernel_on_buffers(module_json, len, arch, nullptr, 0, outs.data(),
+                                                    static_cast<int>(outs.size()), input_scalars, n_inputs, 1);
+    if (rc != MLKHIP_OK) return rc;
+    for (size_t i = 0; i < slots.size(); ++i) output_scalars[i] = slots[i][0];
+    return MLKHIP_OK;
+}
+
+int mlkhip_execute_cache_size(void) {
+    ExecCache& c = execCache();
+    std::lock_guard<std::mutex> g(c.lock);
+    return static_cast<int>(c.map.size());
+}
+
+void mlkhip_execute_cache_clear(void) {
+    ExecCache& c = execCache();
+    std::lock_guard<std::mutex> g(c.lock);
+    c.map.clear();
 }
 
 int mlkhip_malloc(void** p, size_t bytes) { return mlkd_rt_malloc(p, bytes); }

@@ -20,7 +20,7 @@ from typing import List, Optional, Sequence
 
 from .kernel_ir import (DYNAMIC, KernelBuffer, KernelExpr, KernelModule,
                         KernelNode, KernelOperand, const, elem_a, elem_b,
-                        elem_idx, temp)
+                        elem_idx, scalar, temp)
 
 
 def _numel(dims: Sequence[int]) -> int:
@@ -87,6 +87,27 @@ def exp_affine_chain(a_operand: Optional[KernelOperand] = None) -> List[KernelEx
             KernelExpr("add", temp(0), elem_b()),
             KernelExpr("exp", temp(1), const(0.0)),
             KernelExpr("mul", temp(2), elem_a())]
+
+
+def scalar_kernel_module(chain: List[KernelExpr], family: Optional[str] = None) -> KernelModule:
+    """A scalar graph as lower.to_kernel_ir emits it (:355-425): ScalarParam
+    operands, one f64 output slot, a loop of exactly one instance."""
+    km = KernelModule()
+    out_id = km.add_buffer(KernelBuffer(name="out", dtype="f64", is_output=True, elements=1))
+    cid = km.add_node(KernelNode(op="compute", math=chain[-1].op, family=family, exprs=list(chain)))
+    sid = km.add_node(KernelNode(op="store", out=out_id))
+    km.add_node(KernelNode(op="loop", var="i", begin=0, end=1, children=[cid, sid]))
+    km.schedule["vector_width"] = 8
+    return km
+
+
+def sin_graph_scalar_module() -> KernelModule:
+    """examples/scalar/sin_graph.mlk:12-17 lowered as a scalar kernel: x is
+    ScalarParam 0, y = sin(x*x + 3*x) with the poly7 family."""
+    x = scalar(0)
+    return scalar_kernel_module([KernelExpr("mul", x, x), KernelExpr("mul", const(3.0), x),
+                                 KernelExpr("add", temp(0), temp(1)), KernelExpr("sin", temp(2), const(0.0))],
+                                family="poly7")
 
 
 def config1_module(n: int = 1 << 24, family: str = "poly7", dtype: str = "f32") -> KernelModule:
