@@ -632,21 +632,19 @@ __device__ __forceinline__ void blockOfQ(int rowBlocks, int64_t& b, int& rb, int
     kh = rem % 2;
 }
 
-__global__ __launch_bounds__(256, 2) void scoreStatsQ(const _Float16* __restrict__ Q,
-                                                      const _Float16* __restrict__ K,
-                                                      const float* __restrict__ bias,
-                                                      float2* __restrict__ part, int seq, float c2) {
-    extern __shared__ __align__(16) _Float16 ldsQ[];
-    float* lbias = reinterpret_cast<float*>(ldsQ + 2 * kPanelHalvesQ);  // the key half's bias
+/// Pass-1 statistics of this wave's 32 queries of row block (b, rb) over
+/// keys [k0, k0 + keys): D = K Q^T per 128-key panel, so each lane keeps a
+/// running max and sum(exp2(v - max)) of its query; the lane 32 away holds
+/// the other keys of the same query and the pair is combined at the end.
+/// Returns (max, sum) of query row `qrow` in base 2 (both half-waves agree).
+__device__ __forceinline__ float2 statsRangeQ(const _Float16* __restrict__ Q, const _Float16* __restrict__ K,
+                                              const float* __restrict__ bias, int seq, float c2, int64_t b,
+                                              int rb, int k0, int keys, _Float16* ldsQ, int64_t& qrow) {
+    float* lbias = reinterpret_cast<float*>(ldsQ + 2 * kPanelHalvesQ);  // this key range's bias
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6, l32 = lane & 31, hl = lane >> 5;
-    int64_t b;
-    int rb, kh;
-    blockOfQ(seq / 128, b, rb, kh);
-    const int keys = seq / 2;
-    const int k0 = kh * keys;
     const int np = keys / kPanelQ;
-    const int64_t qrow = b * seq + static_cast<int64_t>(rb) * 128 + wave * 32 + l32;
+    qrow = b * seq + static_cast<int64_t>(rb) * 128 + wave * 32 + l32;
     f16x8 xq[8];                                  // B operand: this lane's query, 8 x 16 head dims
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) xq[ks] = *reinterpret_cast<const f16x8*>(Q + qrow * kD2 + ks * 16 + hl * 8);
@@ -705,39 +703,46 @@ __global__ __launch_bounds__(256, 2) void scoreStatsQ(const _Float16* __restrict
     const float lo = __shfl_xor(l, 32, 64);
     const float mx = fmaxf(m, mo);
     const float lt = l * __builtin_amdgcn_exp2f(m - mx) + lo * __builtin_amdgcn_exp2f(mo - mx);
-    if (hl == 0) part[qrow * 2 + kh] = make_float2(mx, lt);
+    return make_float2(mx, lt);
 }
 
-__global__ __launch_bounds__(256, 2) void scoreStoreQ(const _Float16* __restrict__ Q,
-                                                      const _Float16* __restrict__ K,
-                                                      const float* __restrict__ bias,
-                                                      const float2* __restrict__ part, float* __restrict__ S,
-                                                      int seq, float c2) {
-    extern __shared__ __align__(16) _Float16 ldsQ[];
+/// Row statistics of the 16 rows this lane's pass-2 accumulators hold,
+/// merged from NP key-range partials part[row * NP + i] (base 2).
+template <int NP>
+__device__ __forceinline__ void mergeStatsQ(const float2* __restrict__ part, int64_t r0, float (&rmx)[16],
+                                            float (&rinv)[16]) {
+    const int hl = (threadIdx.x & 63) >> 5;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const float2* pr = part + (r0 + 8 * (r >> 2) + 4 * hl + (r & 3)) * NP;
+        float2 pp[NP];
+#pragma unroll
+        for (int i = 0; i < NP; ++i) pp[i] = pr[i];
+        float mx = pp[0].x;
+#pragma unroll
+        for (int i = 1; i < NP; ++i) mx = fmaxf(mx, pp[i].x);
+        float lt = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NP; ++i) lt += pp[i].y * __builtin_amdgcn_exp2f(pp[i].x - mx);
+        rmx[r] = mx;
+        rinv[r] = lt != 0.0f ? 1.0f / lt : 0.0f;
+    }
+}
+
+/// Pass 2 over keys [k0, k0 + keys) of this wave's 32 rows r0..r0+31 of
+/// batch b: D = Q K^T per panel, written as exp2(v - max) / sum at once;
+/// each 32-lane half-wave stores one 128-byte line.
+__device__ __forceinline__ void storeRangeQ(const _Float16* __restrict__ Q, const _Float16* __restrict__ K,
+                                            const float* __restrict__ bias, float* __restrict__ S, int seq,
+                                            float c2, int64_t b, int64_t r0, int k0, int keys,
+                                            const float (&rmx)[16], const float (&rinv)[16], _Float16* ldsQ) {
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6, l32 = lane & 31, hl = lane >> 5;
-    int64_t b;
-    int rb, kh;
-    blockOfQ(seq / 128, b, rb, kh);
-    const int keys = seq / 2;
-    const int k0 = kh * keys;
+    const int lane = tid & 63, l32 = lane & 31, hl = lane >> 5;
     const int np = keys / kPanelQ;
-    const int64_t r0 = b * seq + static_cast<int64_t>(rb) * 128 + wave * 32;
     f16x8 aq[8];                                  // A operand: row r0 + l32
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
         aq[ks] = *reinterpret_cast<const f16x8*>(Q + (r0 + l32) * kD2 + ks * 16 + hl * 8);
-    }
-    // Row statistics of the 16 rows this lane's accumulators hold.
-    float rmx[16], rinv[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const float2* pr = part + (r0 + 8 * (r >> 2) + 4 * hl + (r & 3)) * 2;
-        const float2 p0 = pr[0], p1 = pr[1];
-        const float mx = fmaxf(p0.x, p1.x);
-        const float lt = p0.y * __builtin_amdgcn_exp2f(p0.x - mx) + p1.y * __builtin_amdgcn_exp2f(p1.x - mx);
-        rmx[r] = mx;
-        rinv[r] = lt != 0.0f ? 1.0f / lt : 0.0f;
     }
     const _Float16* kb = K + (b * seq + k0) * kD2;
     u32x4v v[8];
@@ -776,6 +781,34 @@ __global__ __launch_bounds__(256, 2) void scoreStoreQ(const _Float16* __restrict
         if (p + 1 < np) storePanelQ(ldsQ + ((p + 1) & 1) * kPanelHalvesQ, tid, v);
         __syncthreads();
     }
+}
+
+__global__ __launch_bounds__(256, 2) void scoreStatsQ(const _Float16* __restrict__ Q,
+                                                      const _Float16* __restrict__ K,
+                                                      const float* __restrict__ bias,
+                                                      float2* __restrict__ part, int seq, float c2) {
+    extern __shared__ __align__(16) _Float16 ldsQ[];
+    int64_t b;
+    int rb, kh;
+    blockOfQ(seq / 128, b, rb, kh);
+    int64_t qrow;
+    const float2 st = statsRangeQ(Q, K, bias, seq, c2, b, rb, kh * (seq / 2), seq / 2, ldsQ, qrow);
+    if (((threadIdx.x & 63) >> 5) == 0) part[qrow * 2 + kh] = st;
+}
+
+__global__ __launch_bounds__(256, 2) void scoreStoreQ(const _Float16* __restrict__ Q,
+                                                      const _Float16* __restrict__ K,
+                                                      const float* __restrict__ bias,
+                                                      const float2* __restrict__ part, float* __restrict__ S,
+                                                      int seq, float c2) {
+    extern __shared__ __align__(16) _Float16 ldsQ[];
+    int64_t b;
+    int rb, kh;
+    blockOfQ(seq / 128, b, rb, kh);
+    const int64_t r0 = b * seq + static_cast<int64_t>(rb) * 128 + (threadIdx.x >> 6) * 32;
+    float rmx[16], rinv[16];
+    mergeStatsQ<2>(part, r0, rmx, rinv);
+    storeRangeQ(Q, K, bias, S, seq, c2, b, r0, kh * (seq / 2), seq / 2, rmx, rinv, ldsQ);
 }
 
 int launchQ(const mlkd_score_softmax* p, hipStream_t st) {
