@@ -196,139 +196,6 @@ __global__ __launch_bounds__(512) void gemmF16Mfma(const _Float16* __restrict__ 
     }
 }
 
-/// Three-stage variant of gemmF16Mfma: global loads run two K steps ahead
-/// into alternating register sets, so a tile's load latency is covered by
-/// two steps of MFMAs instead of one; the LDS tiles stay double buffered.
-/// The K loop is unrolled by two so both register sets are static.
-template <bool ACC>
-__global__ __launch_bounds__(512) void gemmF16Mfma3s(const _Float16* __restrict__ A,
-                                                     const _Float16* __restrict__ B,
-                                                     float* __restrict__ C, int M, int N, int K,
-                                                     int64_t lda, int64_t ldb, int64_t ldc,
-                                                     int /*accumulate: template ACC*/) {
-    extern __shared__ __align__(16) _Float16 lds[];
-    _Float16* As = lds;
-    _Float16* Bs = lds + 2 * kTileHalves;
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wm = wave >> 2;
-    const int wn = wave & 3;
-    int tm, tn;
-    xcdTile(M / kBM, N / kBN, tm, tn);
-    const int64_t row0 = static_cast<int64_t>(tm) * kBM;
-    const int64_t col0 = static_cast<int64_t>(tn) * kBN;
-    const bool loadsA = tid < 256;
-    const int t = tid & 255;
-    const int bk = t & 7;
-    const int bn = t >> 3;
-    u32x4 r0[8], r1[8];
-
-    auto globalLoad = [&](int k0, u32x4(&reg)[8]) {
-        if (loadsA) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int c = j * 256 + t;
-                reg[j] = *reinterpret_cast<const u32x4*>(A + (row0 + (c >> 3)) * lda + k0 + (c & 7) * 8);
-            }
-        } else {
-#pragma unroll
-            for (int r = 0; r < 8; ++r) {
-                reg[r] = *reinterpret_cast<const u32x4*>(B + static_cast<int64_t>(k0 + bk * 8 + r) * ldb + col0 +
-                                                         bn * 8);
-            }
-        }
-    };
-    auto ldsStore = [&](int buf, const u32x4(&reg)[8]) {
-        if (loadsA) {
-            _Float16* dst = As + buf * kTileHalves;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int c = j * 256 + t;
-                *reinterpret_cast<u32x4*>(dst + (c >> 3) * kPadK + (c & 7) * 8) = reg[j];
-            }
-        } else {
-            _Float16* dst = Bs + buf * kTileHalves;
-#pragma unroll
-            for (int n = 0; n < 8; ++n) {
-                const int pp = n >> 1;
-                const uint32_t sel = (n & 1) ? 0x07060302u : 0x05040100u;
-                u32x4 o;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) o[j] = __builtin_amdgcn_perm(reg[2 * j + 1][pp], reg[2 * j][pp], sel);
-                *reinterpret_cast<u32x4*>(dst + (bn * 8 + n) * kPadK + bk * 8) = o;
-            }
-        }
-    };
-
-    f32x16 acc[4][2];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-        }
-    }
-    const int lrow = lane & 31;
-    const int lk = (lane >> 5) * 8;
-    auto mfmaStep = [&](int buf) {
-        const _Float16* as = As + buf * kTileHalves + (wm * 128 + lrow) * kPadK + lk;
-        const _Float16* bs = Bs + buf * kTileHalves + (wn * 64 + lrow) * kPadK + lk;
-#pragma unroll
-        for (int kk = 0; kk < kBK; kk += 16) {
-            f16x8 a[4], b[2];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const f16x8*>(as + i * 32 * kPadK + kk);
-#pragma unroll
-            for (int j = 0; j < 2; ++j) b[j] = *reinterpret_cast<const f16x8*>(bs + j * 32 * kPadK + kk);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
-                }
-            }
-        }
-    };
-
-    // Step s computes from LDS buffer s&1. At its start the registers hold
-    // tile s+1 (set (s+1)&1); tile s+2 is loaded into set s&1.
-    const int steps = K / kBK;
-    globalLoad(0, r0);
-    ldsStore(0, r0);
-    if (steps > 1) globalLoad(kBK, r1);
-    __syncthreads();
-    for (int s = 0; s < steps; s += 2) {
-        // even step s: buffer 0, registers r1 hold tile s+1
-        if (s + 2 < steps) globalLoad((s + 2) * kBK, r0);
-        mfmaStep(0);
-        if (s + 1 < steps) ldsStore(1, r1);
-        __syncthreads();
-        if (s + 1 >= steps) break;
-        // odd step s+1: buffer 1, registers r0 hold tile s+2
-        if (s + 3 < steps) globalLoad((s + 3) * kBK, r1);
-        mfmaStep(1);
-        if (s + 2 < steps) ldsStore(0, r0);
-        __syncthreads();
-    }
-
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int64_t cBase = col0 + wn * 64 + j * 32 + (lane & 31);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int64_t row = row0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                float* dst = C + row * ldc + cBase;
-                const float v = acc[i][j][r];
-                *dst = ACC ? *dst + v : v;
-            }
-        }
-    }
-}
-
 /// Two-per-CU variant: a 128 x 256 workgroup tile of 4 waves (each 64 x 128 =
 /// 2 x 4 MFMA tiles), K step 32, LDS tiles double buffered in 60 KiB, so
 /// two workgroups share a CU and one's load waits overlap the other's MFMAs.
@@ -1197,9 +1064,8 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 // Process default of the f16 GEMM launch form (a launch's own `variant`
 // field overrides it): 0: 8 waves of 128x64; 1: 4 waves of 128x128; 2: 4
-// waves with A direct to LDS; 3: 4 waves, explicitly pipelined; 4: 8 waves,
-// loads two steps ahead (register-limited: spills, kept for measurement);
-// 5/6: 128x256 tiles, two workgroups per CU, loads two / one step ahead;
+// waves with A direct to LDS; 3: 4 waves, explicitly pipelined; 5/6:
+// 128x256 tiles, two workgroups per CU, loads two / one step ahead;
 // 7: 4 waves, both operands direct to a 4-deep LDS ring, B read transposed
 // (measured fastest on gfx950).
 int gGemmF16Variant = 7;
@@ -1265,25 +1131,6 @@ extern "C" int mlkd_launch_gemm(const mlkd_gemm* p, void* stream) {
                                static_cast<const _Float16*>(p->b), static_cast<float*>(p->c),
                                static_cast<int>(p->m), static_cast<int>(p->n), static_cast<int>(p->k), p->lda,
                                p->ldb, p->ldc);
-            return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
-        }
-        if (variant == 4) {
-            static bool raised4 = false;
-            if (!raised4) {
-                if (hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF16Mfma3s<true>),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        static_cast<int>(ldsBytes)) != hipSuccess ||
-                    hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF16Mfma3s<false>),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        static_cast<int>(ldsBytes)) != hipSuccess) {
-                    return MLKD_RT_LAUNCH;
-                }
-                raised4 = true;
-            }
-            hipLaunchKernelGGL((p->accumulate ? gemmF16Mfma3s<true> : gemmF16Mfma3s<false>), dim3(tiles), dim3(512),
-                               ldsBytes, st, static_cast<const _Float16*>(p->a), static_cast<const _Float16*>(p->b),
-                               static_cast<float*>(p->c), static_cast<int>(p->m), static_cast<int>(p->n),
-                               static_cast<int>(p->k), p->lda, p->ldb, p->ldc, 0);
             return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
         }
         if (variant == 3) {

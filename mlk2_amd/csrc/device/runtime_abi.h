@@ -74,7 +74,9 @@ int mlkd_launch_softmax(const mlkd_softmax* p, void* stream);
 /// with plain stores; waves <= 0 keeps the default grid).
 void mlkd_softmax_set_variant(int variant, int64_t waves);
 int mlkd_launch_gemm(const mlkd_gemm* p, void* stream);
-/// Variant-space hook for the f16 GEMM (0: 8 waves x 128x64, 1: 4 waves x 128x128).
+/// Process default of the f16 GEMM launch form (7: direct-to-LDS ring, the
+/// default; 0: 8 waves x 128x64; 1: 4 waves x 128x128; 2: A direct to LDS;
+/// 3: pipelined step; 5/6: 128x256 tiles, two workgroups per CU).
 void mlkd_gemm_set_variant(int variant);
 int mlkd_launch_score_softmax(const mlkd_score_softmax* p, void* stream);
 /// Scratch bytes the two-pass score-softmax form needs for `p`'s shape (0 when
