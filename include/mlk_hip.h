@@ -194,6 +194,25 @@ int mlkhip_autotune(mlkhip_artifact* a, const mlkhip_binding* binds, int n_binds
                     int64_t n_scalars, int64_t elements, int reps, const char* cache_dir, char* report,
                     size_t report_cap);
 
+/* Replaces essentialWorkModel + rooflineLowerBound (fastkernel/src/
+ * fast_kernel.cpp:319-384, fast_kernel.h:100-117) with element sizes from
+ * the buffers' dtypes: min_bytes counts every non-temp input and output
+ * once at 8/4/2 bytes per f64/f32/f16 element (the reference counts 8 for
+ * all); min_ops follows the reference's walk (MatMul 2MKN, Softmax 5 per
+ * element, ReduceSum 1 per element, 1 per Compute expression and per
+ * accumulate store, counted once per path from the node list). The lower
+ * bound is max(min_bytes / bytes_per_sec, min_ops / ops_per_sec), 0 when a
+ * count is unknown (a dynamic extent without dims). bytes_per_sec <= 0
+ * takes MI355X HBM (8e12 B/s); ops_per_sec <= 0 takes the datasheet rate
+ * of the plan (2.5e15 with an f16 GEMM or score step, 78.6e12 for f64-only
+ * modules, else 157.3e12). No device needed. mlkhip_autotune reports the
+ * same quantities with its winner's gap over the bound, and a launch
+ * coverage certificate per step (certifyLaunchCoverage, fast_kernel.cpp:
+ * 386-497, restated for the GPU decomposition). */
+int mlkhip_essential_work(const char* module_json, size_t len, double bytes_per_sec, double ops_per_sec,
+                          int64_t* min_bytes, int64_t* min_ops, int* bytes_known, int* ops_known,
+                          double* roofline_lower_sec);
+
 /* ---- run route (the ExecutionEngine hook of `mlkc run`) ---------------- */
 /* `mlkc run` reaches only the CPU executor (tools/mlkc/mlkc.cpp:206-263,
  * runtime/src/execution/execution.cpp:195-256). These two entries are what

@@ -94,6 +94,9 @@ def lib():
     L.mlkhip_variants_from_cache.argtypes = [c.c_void_p]
     L.mlkhip_autotune.argtypes = [c.c_void_p, c.POINTER(Binding), c.c_int, _PD, c.c_int64, c.c_int64,
                                   c.c_int, c.c_char_p, c.c_char_p, c.c_size_t]
+    L.mlkhip_essential_work.argtypes = [c.c_char_p, c.c_size_t, c.c_double, c.c_double, c.POINTER(c.c_int64),
+                                        c.POINTER(c.c_int64), c.POINTER(c.c_int), c.POINTER(c.c_int),
+                                        c.POINTER(c.c_double)]
     L.mlkhip_execute_kernel_on_buffers.argtypes = [c.c_char_p, c.c_size_t, c.c_char_p, c.POINTER(_PD), c.c_int,
                                                    c.POINTER(_PD), c.c_int, _PD, c.c_int64, c.c_int64]
     L.mlkhip_execute_kernel.argtypes = [c.c_char_p, c.c_size_t, c.c_char_p, _PD, c.c_int, _PD, c.c_int]
@@ -158,6 +161,19 @@ def plan_variants(km: KernelModule, step: int = 0) -> List[int]:
     if n < 0:
         raise MlkHipError(REFUSED, last_error())
     return list(out[:n])
+
+
+def essential_work(km: KernelModule, bytes_per_sec: float = 0.0, ops_per_sec: float = 0.0) -> dict:
+    """EssentialWork + roofline lower bound (mlkhip_essential_work); rates
+    <= 0 take the MI355X datasheet values. No device needed."""
+    data = km.to_json().encode()
+    b, o = ctypes.c_int64(), ctypes.c_int64()
+    bk, ok = ctypes.c_int(), ctypes.c_int()
+    low = ctypes.c_double()
+    _check(lib().mlkhip_essential_work(data, len(data), float(bytes_per_sec), float(ops_per_sec), ctypes.byref(b),
+                                       ctypes.byref(o), ctypes.byref(bk), ctypes.byref(ok), ctypes.byref(low)))
+    return {"min_bytes": b.value, "min_ops": o.value, "bytes_known": bool(bk.value), "ops_known": bool(ok.value),
+            "roofline_lower_sec": low.value}
 
 
 def _f64(a) -> np.ndarray:

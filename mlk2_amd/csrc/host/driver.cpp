@@ -832,6 +832,28 @@ void mlkhip_execute_cache_clear(void) {
     c.map.clear();
 }
 
+int mlkhip_essential_work(const char* module_json, size_t len, double bytes_per_sec, double ops_per_sec,
+                          int64_t* min_bytes, int64_t* min_ops, int* bytes_known, int* ops_known,
+                          double* roofline_lower_sec) {
+    if (module_json == nullptr) return setError(MLKHIP_REFUSED, "null argument");
+    auto km = mlk::hip::parseKernelModule(module_json, len);
+    if (!km.has_value()) return setError(MLKHIP_REFUSED, km.error().message);
+    const mlk::hip::EssentialWork w = mlk::hip::essentialWork(*km);
+    double tput = ops_per_sec;
+    if (tput <= 0.0) {
+        auto plan = mlk::hip::planModule(mlk::hip::deviceModule(*km));
+        if (!plan.has_value()) return setError(MLKHIP_REFUSED, plan.error().message);
+        tput = mlk::hip::peakOpsPerSec(*km, *plan);
+    }
+    const double bw = bytes_per_sec > 0.0 ? bytes_per_sec : 8.0e12;
+    if (min_bytes != nullptr) *min_bytes = w.minBytes;
+    if (min_ops != nullptr) *min_ops = w.minOps;
+    if (bytes_known != nullptr) *bytes_known = w.bytesKnown ? 1 : 0;
+    if (ops_known != nullptr) *ops_known = w.opsKnown ? 1 : 0;
+    if (roofline_lower_sec != nullptr) *roofline_lower_sec = mlk::hip::rooflineLowerSec(w, bw, tput);
+    return MLKHIP_OK;
+}
+
 int mlkhip_malloc(void** p, size_t bytes) { return mlkd_rt_malloc(p, bytes); }
 int mlkhip_free(void* p) { return mlkd_rt_free(p); }
 int mlkhip_memcpy_h2d(void* dst, const void* src, size_t bytes) {

@@ -92,6 +92,29 @@ private:
     mutable std::vector<int64_t> stepScratchBytes_;
 };
 
+/// Essential work of a module (the reference's EssentialWork,
+/// fastkernel/include/mlk/fastkernel/fast_kernel.h:100-117): bytes of every
+/// non-temp input and output moved once, at the buffer's own element size;
+/// operations by the reference's walk (fast_kernel.cpp:228-317).
+struct EssentialWork {
+    int64_t minBytes{0};
+    int64_t minOps{0};
+    bool bytesKnown{true};
+    bool opsKnown{true};
+};
+EssentialWork essentialWork(const KernelModule& km);
+
+/// max(bytes / bandwidth, ops / throughput), or 0 when either count is
+/// unknown (fast_kernel.cpp:372-384).
+double rooflineLowerSec(const EssentialWork& w, double bytesPerSec, double opsPerSec);
+
+/// The MI355X datasheet rate a plan's operations are priced at.
+double peakOpsPerSec(const KernelModule& km, const Plan& plan);
+
+/// JSON launch-coverage certificate of one step (the GPU counterpart of
+/// certifyLaunchCoverage, fast_kernel.cpp:386-497).
+std::string launchCoverage(const KernelModule& km, const Step& st, int64_t elements);
+
 /// Launch forms a step's hand-written kernel offers for its shape (empty
 /// when there is only the default); the first entry is the default form.
 std::vector<int> variantSpace(const KernelModule& km, const Step& st);

@@ -148,7 +148,200 @@ bool compare(const std::vector<std::vector<double>>& ref, const std::vector<std:
     return ok;
 }
 
+/// Elements of a buffer from its dims, else its element count; unknown for
+/// a dynamic extent without dims (fast_kernel.cpp:211-226).
+int64_t bufferElements(const KernelBuffer& b, bool& known) {
+    if (!b.dims.empty()) {
+        int64_t prod = 1;
+        for (const int64_t d : b.dims) {
+            if (d < 0 || (d > 0 && prod > (int64_t{1} << 40) / d)) {
+                known = false;
+                return 0;
+            }
+            prod *= d;
+        }
+        return prod;
+    }
+    if (b.elements >= 0 && b.elements < kDynamicBound) return b.elements;
+    known = false;
+    return 0;
+}
+
+/// The reference's operation walk (fast_kernel.cpp:228-317): a Compute node
+/// adds one op per expression plus one per accumulate store, a Call node
+/// its class model (MatMul 2MKN, ReduceSum one per element of A, Softmax 5
+/// per element), anything else leaves the count unknown. Like the
+/// reference, the walk is started from every node and recurses into
+/// children, so a nested node is counted once per path to it.
+void walkOps(const KernelModule& km, const KernelNode& node, EssentialWork& w, int depth) {
+    if (depth > 64) {
+        w.opsKnown = false;
+        return;
+    }
+    constexpr int64_t kCap = int64_t{1} << 40;
+    if (node.op == KernelOp::Compute && w.opsKnown) {
+        const int64_t add = static_cast<int64_t>(node.exprs.size()) + (node.accum != AccumMode::None ? 1 : 0);
+        if (add > kCap - w.minOps) {
+            w.opsKnown = false;
+        } else {
+            w.minOps += add;
+        }
+    } else if (node.op == KernelOp::Call && w.opsKnown) {
+        bool known = true;
+        if (node.bufferA >= km.buffers.size()) {
+            w.opsKnown = false;
+        } else {
+            const int64_t aElems = bufferElements(km.buffers[node.bufferA], known);
+            if (!known) {
+                w.opsKnown = false;
+            } else if (node.math == MathOp::MatMul) {
+                const KernelBuffer* ba = &km.buffers[node.bufferA];
+                const KernelBuffer* bb = node.bufferB < km.buffers.size() ? &km.buffers[node.bufferB] : nullptr;
+                if (bb == nullptr || ba->dims.size() < 2 || bb->dims.size() < 2 || ba->dims[0] <= 0 ||
+                    ba->dims[1] <= 0 || bb->dims.back() <= 0) {
+                    w.opsKnown = false;
+                } else {
+                    const int64_t mk = ba->dims[0] * ba->dims[1];
+                    if (mk > kCap - w.minOps) {
+                        w.opsKnown = false;
+                    } else {
+                        w.minOps += 2 * mk * bb->dims.back();
+                    }
+                }
+            } else if (node.math == MathOp::ReduceSum) {
+                if (aElems > kCap - w.minOps) {
+                    w.opsKnown = false;
+                } else {
+                    w.minOps += aElems;
+                }
+            } else if (node.math == MathOp::Softmax) {
+                if (aElems > (kCap - w.minOps) / 5) {
+                    w.opsKnown = false;
+                } else {
+                    w.minOps += 5 * aElems;
+                }
+            } else {
+                w.opsKnown = false;
+            }
+        }
+    }
+    for (const uint32_t c : node.children) {
+        if (c >= km.nodes.size()) {
+            w.opsKnown = false;
+            return;
+        }
+        walkOps(km, km.nodes[c], w, depth + 1);
+    }
+}
+
 }  // namespace
+
+EssentialWork essentialWork(const KernelModule& km) {
+    EssentialWork w;
+    // Bytes: every non-temp input or output buffer moved once, at its own
+    // element size (the reference counts 8 bytes for every element).
+    for (const KernelBuffer& b : km.buffers) {
+        if (b.isTemp || (!b.isInput && !b.isOutput)) continue;
+        bool known = true;
+        const int64_t elems = bufferElements(b, known);
+        if (!known || elems > (int64_t{1} << 40)) {
+            w.bytesKnown = false;
+            break;
+        }
+        w.minBytes += elems * dtypeBytes(b.dtype);
+    }
+    for (const KernelNode& n : km.nodes) {
+        walkOps(km, n, w, 0);
+        if (!w.opsKnown) break;
+    }
+    return w;
+}
+
+double peakOpsPerSec(const KernelModule& km, const Plan& plan) {
+    // MI355X datasheet (dense): f16 MFMA 2.5 PFLOP/s, f32 157.3 TFLOP/s,
+    // f64 78.6 TFLOP/s. A plan with an f16 GEMM is priced at the f16 rate,
+    // one touching only f64 buffers at the f64 rate, anything else at f32.
+    bool allF64 = true;
+    for (const KernelBuffer& b : km.buffers) {
+        if (!b.isTemp && b.dtype != Dtype::F64) allF64 = false;
+    }
+    for (const Step& st : plan.steps) {
+        if ((st.kind == StepKind::Gemm && st.a != kInvalidId && km.buffers[st.a].dtype == Dtype::F16) ||
+            st.kind == StepKind::ScoreSoftmax) {
+            return 2.5e15;
+        }
+    }
+    return allF64 ? 78.6e12 : 157.3e12;
+}
+
+double rooflineLowerSec(const EssentialWork& w, double bytesPerSec, double opsPerSec) {
+    if (!w.bytesKnown || !w.opsKnown || bytesPerSec <= 0.0 || opsPerSec <= 0.0) return 0.0;
+    return std::max(static_cast<double>(w.minBytes) / bytesPerSec, static_cast<double>(w.minOps) / opsPerSec);
+}
+
+std::string launchCoverage(const KernelModule& km, const Step& st, int64_t elements) {
+    // Each launcher's decomposition restated: instances of the step, the
+    // workgroups that carry them, and whether their union is the domain
+    // exactly once. Grid-stride forms cover any instance count; tiled forms
+    // cover when the tile divides the extent (the launcher checks the same
+    // divisibility and falls back to the bounds-checked general kernel).
+    (void)km;
+    int64_t instances = 0, workgroups = 0, perGroup = 0;
+    bool covered = true;
+    const char* form = "";
+    switch (st.kind) {
+        case StepKind::Elementwise: {
+            const int64_t w = st.dynamicExtent ? elements - st.dynBegin : st.extent[st.rank - 1];
+            int64_t rows = 1;
+            for (int d = 0; d + 1 < st.rank; ++d) rows *= st.extent[d];
+            instances = rows * std::max<int64_t>(w, 0);
+            const int64_t segs = rows * ((std::max<int64_t>(w, 0) + 1023) / 1024);
+            workgroups = std::min<int64_t>(std::max<int64_t>((segs * 64 + 255) / 256, 1), 16384);
+            perGroup = 4 * 1024;
+            form = "grid-stride 1024-element segments, one per wave";
+            break;
+        }
+        case StepKind::Nest:
+            instances = st.threads;
+            workgroups = std::min<int64_t>(std::max<int64_t>((st.threads + 255) / 256, 1), 16384);
+            perGroup = 256;
+            form = "grid-stride over the collapsed parallel loops";
+            break;
+        case StepKind::Softmax:
+        case StepKind::RowSum:
+            instances = st.rows;
+            workgroups = std::min<int64_t>(std::max<int64_t>((st.rows + 3) / 4, 1), 65536);
+            perGroup = 4;
+            form = "rows over waves, grid-stride";
+            break;
+        case StepKind::Gemm: {
+            instances = st.m * st.n;
+            const bool tiled = st.m % 256 == 0 && st.n % 256 == 0;
+            workgroups = tiled ? (st.m / 256) * (st.n / 256) : ((st.m + 63) / 64) * ((st.n + 63) / 64);
+            perGroup = tiled ? 256 * 256 : 64 * 64;
+            covered = workgroups * perGroup >= instances;
+            form = tiled ? "256 x 256 output tiles" : "64 x 64 output tiles, bounds-checked";
+            break;
+        }
+        case StepKind::ScoreSoftmax: {
+            // Output scores; the two-pass form (dim 128, seq % 256 == 0)
+            // gives each workgroup of a pass 128 rows x half the keys.
+            instances = st.batch * st.seq * st.seq;
+            const bool twoPass = st.dim == 128 && st.seq % 256 == 0;
+            workgroups = twoPass ? st.batch * (st.seq / 128) * 2 : st.batch * ((st.seq + 31) / 32);
+            perGroup = twoPass ? 64 * st.seq : 32 * st.seq;
+            covered = workgroups * perGroup >= instances;
+            form = twoPass ? "128-row blocks x key halves, per pass" : "32-row blocks";
+            break;
+        }
+        case StepKind::Fail:
+            covered = false;
+            break;
+    }
+    return "{\"form\":\"" + std::string(form) + "\",\"instances\":" + std::to_string(instances) +
+           ",\"workgroups\":" + std::to_string(workgroups) + ",\"per_workgroup\":" + std::to_string(perGroup) +
+           ",\"covered\":" + (covered ? "true" : "false") + "}";
+}
 
 std::vector<int> variantSpace(const KernelModule& km, const Step& st) {
     auto dt = [&](uint32_t b) { return km.buffers[b].dtype; };
@@ -441,7 +634,7 @@ int HipLoadedKernel::autotune(const DeviceBinding* binds, int n, const double* s
         if (!steps.empty()) steps += ",";
         steps += "{\"step\":" + std::to_string(si) + ",\"class\":\"" + plan_.steps[si].what + "\",\"kernel\":\"" +
                  kindName(plan_.steps[si].kind) + "\",\"chosen\":" + std::to_string(chosen[si]) +
-                 ",\"candidates\":[" + cands + "]}";
+                 ",\"launch\":" + launchCoverage(km_, plan_.steps[si], elements) + ",\"candidates\":[" + cands + "]}";
     }
     for (size_t i = 0; i < plan_.steps.size(); ++i) plan_.steps[i].variant = chosen[i];
     bool combined = true;
@@ -454,6 +647,13 @@ int HipLoadedKernel::autotune(const DeviceBinding* binds, int n, const double* s
             for (Step& st : plan_.steps) st.variant = -1;
         }
     }
+    // The whole artifact with the chosen forms, against the roofline lower
+    // bound of its essential work (FastKernelReport's winner gap,
+    // fast_kernel.h:327-346).
+    Bench whole;
+    const bool timedWhole = restore() && timeRuns(whole) == MLKHIP_OK;
+    const EssentialWork work = essentialWork(km_);
+    const double lower = rooflineLowerSec(work, 8.0e12, peakOpsPerSec(km_, plan_));
     const bool restored = restore();
     release();
     std::string variants;
@@ -473,7 +673,12 @@ int HipLoadedKernel::autotune(const DeviceBinding* binds, int n, const double* s
              num(thr) + ",\"reps\":" + std::to_string(reps) + ",\"warmup\":" + std::to_string(kWarmup) +
              ",\"combined_certified\":" + (combined ? "true" : "false") + ",\"variants\":[" + variants +
              "],\"cache\":{\"file\":\"" + cacheFile + "\",\"hits\":" + (fromCache_ ? "1" : "0") +
-             ",\"misses\":" + (fromCache_ ? "0" : "1") + "},\"steps\":[" + steps + "]}";
+             ",\"misses\":" + (fromCache_ ? "0" : "1") + "},\"work\":{\"min_bytes\":" +
+             std::to_string(work.minBytes) + ",\"min_ops\":" + std::to_string(work.minOps) + ",\"bytes_known\":" +
+             (work.bytesKnown ? "true" : "false") + ",\"ops_known\":" + (work.opsKnown ? "true" : "false") +
+             "},\"roofline_lower_sec\":" + num(lower) + ",\"winner_sec\":" + num(timedWhole ? whole.median : 0.0) +
+             ",\"winner_gap_over_lower\":" + num(timedWhole && lower > 0.0 ? whole.median / lower - 1.0 : 0.0) +
+             ",\"steps\":[" + steps + "]}";
     if (!restored) {
         why = "could not restore the caller's buffers after the search";
         return MLKHIP_RUNTIME;

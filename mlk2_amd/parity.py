@@ -6,6 +6,13 @@
   against the f64 reference rounded to f32.
 * ``max_rel`` restates ``bench/math/math_bench.cpp:172-181``:
   ``|got - ref| / max(|ref|, 1)``.
+* ``bit_exact`` restates the Rule-43 element gate
+  (``tools/mlk-poly/poly_bench.cpp:211-224``): no element differs under
+  ``!=``, so a NaN never matches, not even a NaN.
+* ``policy_gate`` is the policy-driven gate of the GPU rows
+  (``poly_bench.cpp:499-575``) for this backend's policy ids: bit-exact
+  policies gate with ``bit_exact``, the others with their tolerance on the
+  measured ULP distance or relative error.
 """
 from __future__ import annotations
 
@@ -55,3 +62,37 @@ def max_rel(got: np.ndarray, ref: np.ndarray) -> float:
     e = np.where(both_nan, 0.0, e)
     e = np.where(np.isnan(e), np.inf, e)
     return float(e.max())
+
+
+def bit_exact(got: np.ndarray, ref: np.ndarray):
+    """(passed, first differing index or -1): every element equal under !=
+    semantics, so NaN anywhere fails."""
+    g = np.asarray(got, dtype=np.float64).reshape(-1)
+    r = np.asarray(ref, dtype=np.float64).reshape(-1)
+    if g.shape != r.shape:
+        return False, 0
+    diff = np.nonzero(~(g == r))[0]
+    return (diff.size == 0), (int(diff[0]) if diff.size else -1)
+
+
+def policy_gate(policy: str, got: np.ndarray, ref: np.ndarray, k: int = 1):
+    """(passed, measure, note) of an artifact's output under its tolerance
+    policy id (``mlkhip_policy``): the measure is the first differing index
+    for bit-exact policies, the max f32 ULP distance for the 4-ULP policy,
+    and the max relative error for the relative ones."""
+    if policy.startswith("bitexact"):
+        ok, idx = bit_exact(got, ref)
+        return ok, float(idx), "bit-exact-policy"
+    if policy.startswith("tol-4ulp"):
+        d = float(ulp_distance_f32(got, ref).max()) if np.size(ref) else 0.0
+        return d <= 4.0, d, f"ulp-bounded-policy max={d:g} ulp (measured)"
+    if policy.startswith("tol-rel1e-5sqrtk"):
+        tol = 1e-5 * float(np.sqrt(k))
+    elif policy.startswith("tol-rel1e-6"):
+        tol = 1e-6
+    elif policy.startswith("tol-rel1e-2"):
+        tol = 1e-2
+    else:
+        raise ValueError(f"unknown policy {policy!r}")
+    e = max_rel(got, ref)
+    return e <= tol, e, f"relative-policy max={e:.3g} (tolerance {tol:g})"

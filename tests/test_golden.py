@@ -47,3 +47,4 @@ def test_oracle_reproduces_golden(case):
     out = oracle.run(mk(), mkin(), hw_threads=1)[out_id]
     assert make_golden.summary(out) == {k: v for k, v in GOLDEN["cases"][case].items()
                                         if k != "output_buffer"}
+

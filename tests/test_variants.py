@@ -159,6 +159,12 @@ def test_autotune_certifies_restores_and_caches(hip, name, tmp_path):
         else:
             assert c["rejected"]["reason"] in ("identity-mismatch", "build-failed")
     assert art.step_variant(0) == step["chosen"]
+    # Work model, roofline bound and the winner's gap over it; the step's
+    # launch-coverage certificate.
+    assert rep["work"]["bytes_known"] and rep["work"]["min_bytes"] > 0
+    assert rep["roofline_lower_sec"] > 0 and rep["winner_sec"] > rep["roofline_lower_sec"]
+    assert abs(rep["winner_gap_over_lower"] - (rep["winner_sec"] / rep["roofline_lower_sec"] - 1)) < 1e-3
+    assert step["launch"]["covered"] and step["launch"]["workgroups"] > 0
     # The chosen form meets the path's tolerance against the oracle.
     bufs[out].fill_zero()
     art.run_device(bufs)
