@@ -213,6 +213,14 @@ int mlkhip_essential_work(const char* module_json, size_t len, double bytes_per_
                           int64_t* min_bytes, int64_t* min_ops, int* bytes_known, int* ops_known,
                           double* roofline_lower_sec);
 
+/* Replaces measureEnvironment (fast_kernel.cpp:319-335, which probes CPU
+ * bandwidth and throughput) for the device: HBM bytes/s of a streaming copy
+ * of 256 MiB and the f16 MFMA rate of register-only v_mfma_f32_32x32x16_f16
+ * loops, one wave per SIMD. Probed once per process (about 30 ms, 512 MiB
+ * of temporary device memory); later calls return the same numbers.
+ * mlkhip_autotune reports them with the bound they give. */
+int mlkhip_measure_environment(double* bytes_per_sec, double* f16_flops_per_sec);
+
 /* ---- run route (the ExecutionEngine hook of `mlkc run`) ---------------- */
 /* `mlkc run` reaches only the CPU executor (tools/mlkc/mlkc.cpp:206-263,
  * runtime/src/execution/execution.cpp:195-256). These two entries are what

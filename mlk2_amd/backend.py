@@ -97,6 +97,7 @@ def lib():
     L.mlkhip_essential_work.argtypes = [c.c_char_p, c.c_size_t, c.c_double, c.c_double, c.POINTER(c.c_int64),
                                         c.POINTER(c.c_int64), c.POINTER(c.c_int), c.POINTER(c.c_int),
                                         c.POINTER(c.c_double)]
+    L.mlkhip_measure_environment.argtypes = [c.POINTER(c.c_double), c.POINTER(c.c_double)]
     L.mlkhip_execute_kernel_on_buffers.argtypes = [c.c_char_p, c.c_size_t, c.c_char_p, c.POINTER(_PD), c.c_int,
                                                    c.POINTER(_PD), c.c_int, _PD, c.c_int64, c.c_int64]
     L.mlkhip_execute_kernel.argtypes = [c.c_char_p, c.c_size_t, c.c_char_p, _PD, c.c_int, _PD, c.c_int]
@@ -174,6 +175,13 @@ def essential_work(km: KernelModule, bytes_per_sec: float = 0.0, ops_per_sec: fl
                                        ctypes.byref(o), ctypes.byref(bk), ctypes.byref(ok), ctypes.byref(low)))
     return {"min_bytes": b.value, "min_ops": o.value, "bytes_known": bool(bk.value), "ops_known": bool(ok.value),
             "roofline_lower_sec": low.value}
+
+
+def measure_environment() -> dict:
+    """Measured HBM bytes/s and f16 MFMA flop/s of the device (probed once)."""
+    bw, f16 = ctypes.c_double(), ctypes.c_double()
+    _check(lib().mlkhip_measure_environment(ctypes.byref(bw), ctypes.byref(f16)))
+    return {"bytes_per_sec": bw.value, "f16_flops_per_sec": f16.value}
 
 
 def _f64(a) -> np.ndarray:

@@ -29,7 +29,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 CLANG = os.path.join(ROCM, "llvm", "bin", "clang++")
 
-DEVICE_SOURCES = ["runtime.hip", "jit.hip", "softmax.hip", "gemm.hip", "score_softmax.hip"]
+DEVICE_SOURCES = ["runtime.hip", "jit.hip", "softmax.hip", "gemm.hip", "score_softmax.hip", "probe.hip"]
 HOST_SOURCES = ["kernel_ir.cpp", "planner.cpp", "codegen.cpp", "nestgen.cpp", "canonical.cpp", "driver.cpp", "tune.cpp"]
 
 HIP_FLAGS = [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",

@@ -87,6 +87,11 @@ int64_t mlkd_score_scratch_bytes(const mlkd_score_softmax* p);
 /// two-pass query-stationary).
 void mlkd_score_set_variant(int variant);
 
+/// Measured HBM bandwidth (streaming copy of 256 MiB) and f16 MFMA
+/// throughput (register-only MFMAs, one wave per SIMD) of the current
+/// device, timed on `stream` (probe.hip).
+int mlkd_probe_environment(double* bytes_per_sec, double* f16_flops_per_sec, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

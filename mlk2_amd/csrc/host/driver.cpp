@@ -854,6 +854,16 @@ int mlkhip_essential_work(const char* module_json, size_t len, double bytes_per_
     return MLKHIP_OK;
 }
 
+int mlkhip_measure_environment(double* bytes_per_sec, double* f16_flops_per_sec) {
+    if (bytes_per_sec == nullptr || f16_flops_per_sec == nullptr) return setError(MLKHIP_BAD_BINDING, "null argument");
+    if (mlkd_rt_device_count() <= 0) return setError(MLKHIP_NO_DEVICE, "no HIP device visible");
+    const mlk::hip::MeasuredEnvironment& env = mlk::hip::measuredEnvironment();
+    if (!env.ok) return setError(MLKHIP_LAUNCH, "environment probe failed");
+    *bytes_per_sec = env.bytesPerSec;
+    *f16_flops_per_sec = env.f16FlopsPerSec;
+    return MLKHIP_OK;
+}
+
 int mlkhip_malloc(void** p, size_t bytes) { return mlkd_rt_malloc(p, bytes); }
 int mlkhip_free(void* p) { return mlkd_rt_free(p); }
 int mlkhip_memcpy_h2d(void* dst, const void* src, size_t bytes) {

@@ -115,6 +115,15 @@ double peakOpsPerSec(const KernelModule& km, const Plan& plan);
 /// certifyLaunchCoverage, fast_kernel.cpp:386-497).
 std::string launchCoverage(const KernelModule& km, const Step& st, int64_t elements);
 
+/// The device's measured HBM bandwidth and f16 MFMA rate (the environment
+/// model of fast_kernel.h:66-84), probed once per process on first use.
+struct MeasuredEnvironment {
+    bool ok{false};
+    double bytesPerSec{0.0};
+    double f16FlopsPerSec{0.0};
+};
+const MeasuredEnvironment& measuredEnvironment();
+
 /// Launch forms a step's hand-written kernel offers for its shape (empty
 /// when there is only the default); the first entry is the default form.
 std::vector<int> variantSpace(const KernelModule& km, const Step& st);

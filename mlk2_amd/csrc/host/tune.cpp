@@ -14,6 +14,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -272,6 +273,20 @@ double peakOpsPerSec(const KernelModule& km, const Plan& plan) {
         }
     }
     return allF64 ? 78.6e12 : 157.3e12;
+}
+
+const MeasuredEnvironment& measuredEnvironment() {
+    static std::once_flag once;
+    static MeasuredEnvironment env;
+    std::call_once(once, [] {
+        double bw = 0.0, f16 = 0.0;
+        if (mlkd_probe_environment(&bw, &f16, nullptr) == 0 && bw > 0.0 && f16 > 0.0) {
+            env.ok = true;
+            env.bytesPerSec = bw;
+            env.f16FlopsPerSec = f16;
+        }
+    });
+    return env;
 }
 
 double rooflineLowerSec(const EssentialWork& w, double bytesPerSec, double opsPerSec) {
@@ -653,7 +668,13 @@ int HipLoadedKernel::autotune(const DeviceBinding* binds, int n, const double* s
     Bench whole;
     const bool timedWhole = restore() && timeRuns(whole) == MLKHIP_OK;
     const EssentialWork work = essentialWork(km_);
-    const double lower = rooflineLowerSec(work, 8.0e12, peakOpsPerSec(km_, plan_));
+    const double peak = peakOpsPerSec(km_, plan_);
+    const double lower = rooflineLowerSec(work, 8.0e12, peak);
+    // The same bound at the probed rates (other dtypes scaled from the
+    // measured f16 rate by the datasheet ratio).
+    const MeasuredEnvironment& menv = measuredEnvironment();
+    const double lowerMeasured =
+        menv.ok ? rooflineLowerSec(work, menv.bytesPerSec, peak * menv.f16FlopsPerSec / 2.5e15) : 0.0;
     const bool restored = restore();
     release();
     std::string variants;
@@ -676,7 +697,11 @@ int HipLoadedKernel::autotune(const DeviceBinding* binds, int n, const double* s
              ",\"misses\":" + (fromCache_ ? "0" : "1") + "},\"work\":{\"min_bytes\":" +
              std::to_string(work.minBytes) + ",\"min_ops\":" + std::to_string(work.minOps) + ",\"bytes_known\":" +
              (work.bytesKnown ? "true" : "false") + ",\"ops_known\":" + (work.opsKnown ? "true" : "false") +
-             "},\"roofline_lower_sec\":" + num(lower) + ",\"winner_sec\":" + num(timedWhole ? whole.median : 0.0) +
+             "},\"environment\":{\"declared_bytes_per_sec\":8e+12,\"declared_ops_per_sec\":" + num(peak) +
+             ",\"measured_bytes_per_sec\":" + num(menv.ok ? menv.bytesPerSec : 0.0) +
+             ",\"measured_f16_flops_per_sec\":" + num(menv.ok ? menv.f16FlopsPerSec : 0.0) +
+             "},\"roofline_lower_sec\":" + num(lower) + ",\"roofline_lower_sec_measured\":" + num(lowerMeasured) +
+             ",\"winner_sec\":" + num(timedWhole ? whole.median : 0.0) +
              ",\"winner_gap_over_lower\":" + num(timedWhole && lower > 0.0 ? whole.median / lower - 1.0 : 0.0) +
              ",\"steps\":[" + steps + "]}";
     if (!restored) {

@@ -16,6 +16,7 @@ import pytest
 import oracle
 from mlk2_amd import fixtures as fx
 from mlk2_amd import inputs
+from mlk2_amd import backend as be
 from mlk2_amd.backend import DeviceBuffer, MlkHipError, lib
 from mlk2_amd.parity import max_rel
 
@@ -165,6 +166,9 @@ def test_autotune_certifies_restores_and_caches(hip, name, tmp_path):
     assert rep["roofline_lower_sec"] > 0 and rep["winner_sec"] > rep["roofline_lower_sec"]
     assert abs(rep["winner_gap_over_lower"] - (rep["winner_sec"] / rep["roofline_lower_sec"] - 1)) < 1e-3
     assert step["launch"]["covered"] and step["launch"]["workgroups"] > 0
+    env = rep["environment"]
+    assert 1e12 < env["measured_bytes_per_sec"] < 1e13 and 1e14 < env["measured_f16_flops_per_sec"] < 3e15
+    assert rep["roofline_lower_sec_measured"] >= rep["roofline_lower_sec"]
     # The chosen form meets the path's tolerance against the oracle.
     bufs[out].fill_zero()
     art.run_device(bufs)
@@ -194,3 +198,12 @@ def test_autotune_without_variants_is_a_no_op(hip):
     rep = art.autotune(bufs, reps=3)
     assert rep["steps"] == [] and rep["variants"] == [-1]
     assert rep["cache"]["file"] == ""
+
+
+def test_measured_environment(hip):
+    env = be.measure_environment()
+    say(f"environment: {env['bytes_per_sec'] / 1e12:.2f} TB/s HBM, "
+        f"{env['f16_flops_per_sec'] / 1e12:.0f} TFLOP/s f16 MFMA")
+    assert 1e12 < env["bytes_per_sec"] < 1e13
+    assert 1e14 < env["f16_flops_per_sec"] < 3e15
+    assert be.measure_environment() == env           # probed once per process
