@@ -18,7 +18,7 @@ from __future__ import annotations
 import math
 from typing import List, Optional, Sequence
 
-from .kernel_ir import (DYNAMIC, KernelBuffer, KernelExpr, KernelModule,
+from .kernel_ir import (KernelBuffer, KernelExpr, KernelModule,
                         KernelNode, KernelOperand, const, elem_a, elem_b,
                         elem_idx, scalar, temp)
 

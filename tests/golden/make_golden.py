@@ -12,7 +12,6 @@ requires bit-identical results.
 """
 import hashlib
 import json
-import math
 import os
 import sys
 
