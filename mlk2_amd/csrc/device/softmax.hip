@@ -37,9 +37,89 @@ __device__ __forceinline__ double waveSum(double v) {
     return v;
 }
 
-/// FAST: exp as v_exp_f32 of (x - max) * log2(e), and the row sum as f64 over
-/// f32 sums of each 4-element group (the error of either stays below 1e-7
-/// relative of the result, against the class's 1e-6). NT: nontemporal stores.
+/// Loads one row into the lane's CH float4 (columns past `cols` read as -inf,
+/// which leaves the max unchanged and adds exp(-inf) = 0 to nothing: the sum
+/// skips them). FULL: cols == 256 * CH, so every column is in range and the
+/// guards compile away.
+template <int CH, bool FULL>
+__device__ __forceinline__ void loadRow(const float* xr, int64_t cols, int lane, f32x4 (&v)[CH]) {
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int64_t col = (static_cast<int64_t>(c) * 64 + lane) * 4;
+        if (FULL || col < cols) {
+            v[c] = *reinterpret_cast<const f32x4*>(xr + col);
+        } else {
+            v[c] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        }
+    }
+}
+
+/// The row max, wave-reduced (every lane returns it).
+template <int CH>
+__device__ __forceinline__ float rowMax(const f32x4 (&v)[CH]) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) m = fmaxf(m, v[c][e]);
+    }
+    return waveMax(m);
+}
+
+/// exp(v - m), the row sum, and the stores of v / sum. FAST: exp as
+/// v_exp_f32 of (x - max) * log2(e), and the row sum as f64 over f32 sums of
+/// each 4-element group (the error of either stays below 1e-7 relative of the
+/// result, against the class's 1e-6). NT: nontemporal stores.
+template <int CH, bool FAST, bool NT, bool FULL>
+__device__ __forceinline__ void normalizeRow(f32x4 (&v)[CH], float m, float* yr, int64_t cols, int lane) {
+    double s = 0.0;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int64_t col = (static_cast<int64_t>(c) * 64 + lane) * 4;
+        if constexpr (FAST) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[c][e] = __builtin_amdgcn_exp2f((v[c][e] - m) * 1.44269504088896340736f);
+            if (FULL || col < cols) s += static_cast<double>((v[c][0] + v[c][1]) + (v[c][2] + v[c][3]));
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float ex = expf(v[c][e] - m);
+                v[c][e] = ex;
+                if (FULL || col < cols) s += static_cast<double>(ex);
+            }
+        }
+    }
+    s = waveSum(s);
+    // The reference's `s != 0 ? y / s : 0` never takes its zero arm here: an
+    // in-range element equal to the max m contributes exp(0) = 1, and a row
+    // with no such element (m = +-inf, or every element NaN) makes some term
+    // NaN (inf - inf, NaN - m). So s >= 1 or s is NaN, and y * (1 / s) is
+    // the reference's value without a per-element select.
+    const float inv = static_cast<float>(1.0 / s);
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int64_t col = (static_cast<int64_t>(c) * 64 + lane) * 4;
+        if (FULL || col < cols) {
+            f32x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = v[c][e] * inv;
+            if constexpr (NT) {
+                __builtin_nontemporal_store(o, reinterpret_cast<f32x4*>(yr + col));
+            } else {
+                *reinterpret_cast<f32x4*>(yr + col) = o;
+            }
+        }
+    }
+}
+
+template <int CH, bool FAST, bool NT, bool FULL>
+__device__ __forceinline__ void finishRow(f32x4 (&v)[CH], float* yr, int64_t cols, int lane) {
+    normalizeRow<CH, FAST, NT, FULL>(v, rowMax<CH>(v), yr, cols, lane);
+}
+
+/// One row per wave. Always the guarded row body: the guard-free one
+/// (FULL) holds 150 VGPRs here against 88, and at 3 waves per SIMD instead
+/// of 5 it measured 41.3 us against 40.2 us at 8192 x 4096.
 template <int CH, bool FAST = false, bool NT = true>
 __global__ __launch_bounds__(256) void softmaxWaveRow(const float* x,
                                                       float* y, int64_t rows,
@@ -48,64 +128,52 @@ __global__ __launch_bounds__(256) void softmaxWaveRow(const float* x,
     const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
     const int64_t waves = static_cast<int64_t>(gridDim.x) * 4;
     for (int64_t row = wave; row < rows; row += waves) {
-        const float* xr = x + row * xs;
-        float* yr = y + row * ys;
         f32x4 v[CH];
-#pragma unroll
-        for (int c = 0; c < CH; ++c) {
-            const int64_t col = (static_cast<int64_t>(c) * 64 + lane) * 4;
-            if (col < cols) {
-                v[c] = *reinterpret_cast<const f32x4*>(xr + col);
-            } else {
-                v[c] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-            }
-        }
-        float m = -INFINITY;
-#pragma unroll
-        for (int c = 0; c < CH; ++c) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) m = fmaxf(m, v[c][e]);
-        }
-        m = waveMax(m);
-        double s = 0.0;
-#pragma unroll
-        for (int c = 0; c < CH; ++c) {
-            const int64_t col = (static_cast<int64_t>(c) * 64 + lane) * 4;
-            if constexpr (FAST) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) v[c][e] = __builtin_amdgcn_exp2f((v[c][e] - m) * 1.44269504088896340736f);
-                if (col < cols) s += static_cast<double>((v[c][0] + v[c][1]) + (v[c][2] + v[c][3]));
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float ex = expf(v[c][e] - m);
-                    v[c][e] = ex;
-                    if (col < cols) s += static_cast<double>(ex);
-                }
-            }
-        }
-        s = waveSum(s);
-        const float inv = s != 0.0 ? static_cast<float>(1.0 / s) : 0.0f;
-#pragma unroll
-        for (int c = 0; c < CH; ++c) {
-            const int64_t col = (static_cast<int64_t>(c) * 64 + lane) * 4;
-            if (col < cols) {
-                f32x4 o;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) o[e] = s != 0.0 ? v[c][e] * inv : 0.0f;
-                if constexpr (NT) {
-                    __builtin_nontemporal_store(o, reinterpret_cast<f32x4*>(yr + col));
-                } else {
-                    *reinterpret_cast<f32x4*>(yr + col) = o;
-                }
-            }
-        }
+        loadRow<CH, false>(x + row * xs, cols, lane, v);
+        finishRow<CH, FAST, NT, false>(v, y + row * ys, cols, lane);
     }
 }
 
-/// Same arithmetic as softmaxWaveRow, with each wave walking several rows and
-/// the next row's loads issued before the current row's reductions, so HBM
-/// reads of row r+1 overlap the exp/sum/stores of row r.
+/// Two adjacent rows per wave: the second row's loads are issued once the
+/// first row's max is known, so they land while the first row is
+/// exponentiated, summed and stored. The per-row arithmetic is that of form 0
+/// (rowMax, then normalizeRow<CH, true, true>), so the two forms agree bit
+/// for bit.
+template <int CH, bool FULL>
+__global__ __launch_bounds__(256) void softmaxWaveRowPair(const float* x, float* y, int64_t rows, int64_t cols,
+                                                          int64_t xs, int64_t ys) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int64_t waves = static_cast<int64_t>(gridDim.x) * 4;
+    const int64_t pairs = (rows + 1) / 2;
+    for (int64_t pr = wave; pr < pairs; pr += waves) {
+        // An odd last row pairs with itself: the same wave computes it twice
+        // from the same data and stores the same bits twice. A branch around
+        // the second row instead makes the compiler's wait counts assume the
+        // second row's loads were issued and drain them all before the first
+        // row's reductions, which serialises the pair.
+        const int64_t r0 = 2 * pr;
+        const int64_t r1 = r0 + 1 < rows ? r0 + 1 : r0;
+        f32x4 a[CH], b[CH];
+        loadRow<CH, FULL>(x + r0 * xs, cols, lane, a);
+        const float ma = rowMax<CH>(a);
+        // The barriers fix the order (measured at 8192 x 4096: 39.3 us with
+        // it, 39.7 us with both rows' loads first, 40.1 us with the rows'
+        // bodies merged by the scheduler, which then waits for both rows
+        // before either reduction and holds both rows' temporaries).
+        __builtin_amdgcn_sched_barrier(0);
+        loadRow<CH, FULL>(x + r1 * xs, cols, lane, b);
+        __builtin_amdgcn_sched_barrier(0);
+        normalizeRow<CH, true, true, FULL>(a, ma, y + r0 * ys, cols, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        finishRow<CH, true, true, FULL>(b, y + r1 * ys, cols, lane);
+    }
+}
+
+/// The row body of form 2 (expf, per-element f64 sums), with each wave
+/// walking several rows and the next row's loads issued before the current
+/// row's reductions, so HBM reads of row r+1 overlap the exp/sum/stores of
+/// row r.
 template <int CH>
 __global__ __launch_bounds__(256) void softmaxWaveRowPipelined(const float* x, float* y, int64_t rows,
                                                                int64_t cols, int64_t xs, int64_t ys) {
@@ -113,50 +181,11 @@ __global__ __launch_bounds__(256) void softmaxWaveRowPipelined(const float* x, f
     const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
     const int64_t waves = static_cast<int64_t>(gridDim.x) * 4;
     f32x4 cur[CH], nxt[CH];
-    auto load = [&](int64_t row, f32x4 (&v)[CH]) {
-        const float* xr = x + row * xs;
-#pragma unroll
-        for (int c = 0; c < CH; ++c) {
-            const int64_t col = (static_cast<int64_t>(c) * 64 + lane) * 4;
-            v[c] = col < cols ? *reinterpret_cast<const f32x4*>(xr + col)
-                              : f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-        }
-    };
-    if (wave < rows) load(wave, cur);
+    if (wave < rows) loadRow<CH, false>(x + wave * xs, cols, lane, cur);
     for (int64_t row = wave; row < rows; row += waves) {
         const int64_t nrow = row + waves;
-        if (nrow < rows) load(nrow, nxt);
-        float m = -INFINITY;
-#pragma unroll
-        for (int c = 0; c < CH; ++c) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) m = fmaxf(m, cur[c][e]);
-        }
-        m = waveMax(m);
-        double s = 0.0;
-#pragma unroll
-        for (int c = 0; c < CH; ++c) {
-            const int64_t col = (static_cast<int64_t>(c) * 64 + lane) * 4;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float ex = expf(cur[c][e] - m);
-                cur[c][e] = ex;
-                if (col < cols) s += static_cast<double>(ex);
-            }
-        }
-        s = waveSum(s);
-        const float inv = s != 0.0 ? static_cast<float>(1.0 / s) : 0.0f;
-        float* yr = y + row * ys;
-#pragma unroll
-        for (int c = 0; c < CH; ++c) {
-            const int64_t col = (static_cast<int64_t>(c) * 64 + lane) * 4;
-            if (col < cols) {
-                f32x4 o;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) o[e] = s != 0.0 ? cur[c][e] * inv : 0.0f;
-                __builtin_nontemporal_store(o, reinterpret_cast<f32x4*>(yr + col));
-            }
-        }
+        if (nrow < rows) loadRow<CH, false>(x + nrow * xs, cols, lane, nxt);
+        finishRow<CH, false, true, false>(cur, y + row * ys, cols, lane);
 #pragma unroll
         for (int c = 0; c < CH; ++c) cur[c] = nxt[c];
     }
@@ -226,12 +255,13 @@ __global__ __launch_bounds__(256) void softmaxBlockRow(mlkd_softmax p) {
 }
 
 // Launch variant of the wave-per-row path. 0: one row per wave, v_exp_f32 and
-// grouped sums, nontemporal stores (measured best on gfx950: 40.2 us for
-// 8192 x 4096); 1: rows pipelined over a grid of `gSoftmaxWaves` waves; 2: as
-// 0 with the accurate expf and per-element f64 sums (42.4 us); 3: as 0 with
-// plain stores; 4: as 2 with plain stores. Set by the variant search
-// (mlkd_softmax_set_variant).
-int gSoftmaxVariant = 0;
+// grouped sums, nontemporal stores; 1: rows pipelined over a grid of
+// `gSoftmaxWaves` waves; 2: as 0 with the accurate expf and per-element f64
+// sums; 3: as 0 with plain stores; 4: as 2 with plain stores; 5: as 0 with two
+// adjacent rows per wave (the default: on gfx950 at 8192 x 4096, 38.9 us
+// against 39.8 us for form 0 and 37.4 us for a copy of the same bytes). Set
+// by the variant search (mlkd_softmax_set_variant).
+int gSoftmaxVariant = 5;
 int64_t gSoftmaxWaves = 0;
 
 template <int CH>
@@ -242,6 +272,16 @@ int launchWave(const mlkd_softmax& p, hipStream_t st) {
         if (waves > p.rows) waves = p.rows;
         const int64_t blocks = (waves + 3) / 4;
         hipLaunchKernelGGL(softmaxWaveRowPipelined<CH>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st,
+                           static_cast<const float*>(p.x), static_cast<float*>(p.y), p.rows, p.cols,
+                           p.x_row_stride, p.y_row_stride);
+        return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
+    }
+    const bool full = p.cols == 256 * CH;
+    if (variant == 5) {
+        int64_t blocks = ((p.rows + 1) / 2 + 3) / 4;
+        if (blocks > 8192) blocks = 8192;
+        auto pair = full ? softmaxWaveRowPair<CH, true> : softmaxWaveRowPair<CH, false>;
+        hipLaunchKernelGGL(pair, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st,
                            static_cast<const float*>(p.x), static_cast<float*>(p.y), p.rows, p.cols,
                            p.x_row_stride, p.y_row_stride);
         return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;

@@ -363,7 +363,7 @@ std::vector<int> variantSpace(const KernelModule& km, const Step& st) {
     switch (st.kind) {
         case StepKind::Softmax:
             if (dt(st.x) == Dtype::F32 && dt(st.y) == Dtype::F32 && st.cols % 4 == 0 && st.cols <= 8192) {
-                return {0, 2, 3, 4, 1};
+                return {5, 0, 2, 3, 4, 1};
             }
             return {};
         case StepKind::Gemm:

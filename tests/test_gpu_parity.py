@@ -147,6 +147,35 @@ def test_softmax_adversarial_rows(hip):
     assert np.array_equal(got, np.ones(5))
 
 
+@pytest.mark.parametrize("K", [256, 4096, 1000])
+def test_softmax_infinite_and_nan_rows(hip, K):
+    # Rows whose max is +inf, rows of -inf, all-NaN rows, and a lone finite
+    # element among -inf: the reference yields NaN rows for the first three
+    # (inf - inf, NaN) and a one-hot row for the last. Whole rows of
+    # 256 * CH columns take the guard-free kernels, K = 1000 the guarded ones.
+    say(f"softmax inf/nan rows K={K}")
+    rows = []
+    base = np.array([((i * 7) % 23) * 0.5 - 5.0 for i in range(K)])
+    r = base.copy(); r[K // 3] = np.inf; rows.append(r)
+    r = base.copy(); r[1] = np.inf; r[K - 1] = np.inf; rows.append(r)
+    rows.append(np.full(K, -np.inf))
+    rows.append(np.full(K, np.nan))
+    r = np.full(K, -np.inf); r[K // 2] = 3.0; rows.append(r)
+    r = base.copy(); r[5] = -np.inf; rows.append(r)
+    rows.append(base.copy())
+    x = np.concatenate(rows)
+    M = len(rows)
+    ref = oracle.run(fx.config2_module(M, K, 1), {0: x})[1]
+    art = hip.build(fx.config2_module(M, K, 1))
+    for v in art.step_variants(0):
+        art.set_step_variant(0, v)
+        got = art.run({0: x})[1]
+        assert np.array_equal(np.isnan(got), np.isnan(ref)), v
+        ok = ~np.isnan(ref)
+        assert max_rel(got[ok], ref[ok]) <= 1e-6, v
+    assert np.isnan(ref.reshape(M, K)[:4]).all() and ref.reshape(M, K)[4, K // 2] == 1.0
+
+
 # ------------------------------------------------------------------ C3 ----
 @pytest.mark.parametrize("rows,cols", [(4096, 4096), (37, 100), (3, 5)])
 def test_c3_broadcast_chain(hip, rows, cols):

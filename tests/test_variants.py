@@ -93,6 +93,7 @@ def _gemm_call_acc_case(m=256, k=128, n=512):
 CASES = {
     "gemm-f16-call-accumulate": _gemm_call_acc_case,
     "softmax-512x4096": _softmax_case,
+    "softmax-333x1000": lambda: _softmax_case(333, 1000),
     "gemm-f16-512x1024x512": _gemm_case,
     "score-2x512x128": _score_case,
     "score-1x2048x128": lambda: _score_case(1, 2048, 128),
@@ -114,6 +115,24 @@ def test_every_declared_form_meets_tolerance(hip, name):
         e = max_rel(bufs[out].to_numpy(), ref)
         say(f"variants {name} form {v} max_rel={e:.3e}")
         assert e <= tol, (name, v)
+
+
+@pytest.mark.parametrize("m,k", [(512, 4096), (333, 1000)])
+def test_softmax_forms_with_one_arithmetic_agree_bitwise(hip, m, k):
+    # Forms 5, 0 and 3 share the v_exp_f32 / grouped-sum row body and differ
+    # only in launch shape and store kind; forms 2, 4 and 1 share the expf /
+    # per-element-f64 body. Within each family the outputs are identical.
+    km, bufs, out, _, _ = _softmax_case(m, k)
+    art = hip.build(km)
+    got = {}
+    for v in art.step_variants(0):
+        art.set_step_variant(0, v)
+        bufs[out].fill_zero()
+        art.run_device(bufs)
+        got[v] = bufs[out].to_numpy().astype(np.float32).view(np.uint32)
+    for family in ([5, 0, 3], [2, 4, 1]):
+        for v in family[1:]:
+            assert np.array_equal(got[family[0]], got[v]), (m, k, family[0], v)
 
 
 def test_set_variant_outside_space_refused(hip):
