@@ -32,7 +32,18 @@
 //     access it cannot bound carries a run-time check, which reports through a
 //     status word (1 = negative store address, the walker's InvalidGraph;
 //     6 = outside a bound buffer) instead of touching memory out of bounds.
+//   * LDS slabs, the counterpart of the reference's shared-memory slabs
+//     (backends/cpu/src/slab_plan.cpp, contract in slab_plan.h:1-45): an input
+//     that no Store of the module targets, whose every read in the root is
+//     proven in bounds, is copied once per workgroup into LDS as the interval
+//     hull of those reads, and the reads are redirected there. The copy holds
+//     the buffer's own bits, so values and their order are unchanged. Unlike
+//     the reference, which stages whenever the hull fits, a slab is taken only
+//     when each workgroup is expected to read each staged element at least
+//     twice, so the copy cannot cost more than the reads it replaces; slabs
+//     share a 64 KiB budget per workgroup (two workgroups per CU).
 #include <algorithm>
+#include <cstdint>
 #include <cstdio>
 #include <string>
 #include <vector>
@@ -51,12 +62,15 @@ constexpr int kMaxChain = 8;         // collapsed loops
 constexpr int kMaxNodesVisited = 1 << 16;
 constexpr __int128 kIndexLimit = static_cast<__int128>(1) << 62;
 constexpr int64_t kMaxInstances = int64_t{1} << 40;
+constexpr int64_t kSlabBudget = 64 * 1024;   // LDS bytes of slabs per workgroup
+constexpr int64_t kSlabReuse = 2;            // reads per staged element per workgroup
 
 /// Inclusive range of one loop variable; `unbounded` when it depends on the
 /// run's element count (a dynamic loop end) and so is not known at build.
 struct Range {
     int64_t lo{0}, hi{0};
     bool unbounded{false};
+    bool steers{false};   // appears in the bounds of a deeper loop on the current path
 };
 
 /// off + sum c[p] * v[p] over stack positions p < min(|c|, depth).
@@ -309,9 +323,17 @@ void collect(Ctx& cx, const std::vector<uint32_t>& children, std::vector<Range>&
             bool dead = false, nonEmpty = false;
             if (!loopRange(cx, lb, r, vr, dead, nonEmpty)) return;
             if (dead) continue;
+            std::vector<size_t> marked;
+            for (size_t p = 0; p < r.size(); ++p) {
+                if (!r[p].steers && (coeffAt(lb.begin, p) != 0 || coeffAt(lb.endInc, p) != 0)) {
+                    r[p].steers = true;
+                    marked.push_back(p);
+                }
+            }
             r.push_back(vr);
             collect(cx, n.children, r, definite && nonEmpty, out, level + 1);
             r.pop_back();
+            for (const size_t p : marked) r[p].steers = false;
             continue;
         }
         if (n.op == KernelOp::Guard) {
@@ -375,6 +397,79 @@ bool provablyParallel(Ctx& cx, const KernelNode& loop, std::vector<Range>& r, co
     return true;
 }
 
+/// One LDS slab: elements [lo, lo + span) of buffer `buf`.
+struct Slab {
+    uint32_t buf{kInvalidId};
+    int64_t lo{0}, span{0};
+};
+
+/// Slabs for the root (buffer-id order), given the workgroups of its launch.
+/// Planning never fails the nest: anything it cannot prove leaves the buffer
+/// in global memory.
+std::vector<Slab> planSlabs(const KernelModule& km, uint32_t root, int64_t workgroups) {
+    std::vector<Slab> out;
+    std::vector<bool> stored(km.buffers.size(), false);
+    for (const KernelNode& n : km.nodes) {
+        if (n.op == KernelOp::Store && n.bufferOut < km.buffers.size()) stored[n.bufferOut] = true;
+    }
+    Ctx cx{km, false, ErrorCode::UnsupportedCapability, std::string(), 0};
+    std::vector<Range> r;
+    std::vector<Access> acc;
+    const std::vector<uint32_t> self{root};
+    collect(cx, self, r, true, acc, 0);
+    if (cx.failed) return out;
+    int64_t used = 0;
+    for (uint32_t b = 0; b < km.buffers.size(); ++b) {
+        const KernelBuffer& kb = km.buffers[b];
+        if (stored[b] || !kb.isInput || kb.isTemp) continue;
+        const int64_t elems = cx.staticElems(b);
+        if (elems <= 0) continue;
+        int64_t lo = INT64_MAX, hi = INT64_MIN;
+        // Reads over the loop hulls, and the distinct indices they can form:
+        // an element is re-read only through loops whose coefficient in the
+        // access is zero. A variable that steers a deeper loop's bounds (a
+        // tile index) only moves that loop's window, already counted in the
+        // deeper loop's hull, so it multiplies neither.
+        __int128 reads = 0, distinct = 0;
+        bool ok = true, any = false;
+        for (const Access& a : acc) {
+            if (a.buf != b || a.store) continue;
+            int64_t l = 0, h = 0;
+            bool u = false;
+            if (!bound(a.at, a.ranges, a.depth, l, h, u) || u || l < 0 || h >= elems) {
+                ok = false;
+                break;
+            }
+            any = true;
+            lo = std::min(lo, l);
+            hi = std::max(hi, h);
+            __int128 it = 1, dist = 1;
+            for (size_t p = 0; p < a.ranges.size(); ++p) {
+                const Range& x = a.ranges[p];
+                if (x.unbounded) {
+                    ok = false;
+                    break;
+                }
+                if (x.steers) continue;
+                const __int128 trips = static_cast<__int128>(x.hi - x.lo + 1);
+                it = std::min<__int128>(it * trips, kIndexLimit);
+                if (coeffAt(a.at, p) != 0) dist = std::min<__int128>(dist * trips, kIndexLimit);
+            }
+            reads += it;
+            distinct += dist;
+        }
+        if (!ok || !any) continue;
+        const int64_t span = hi - lo + 1;
+        const int64_t bytes = (span * dtypeBytes(kb.dtype) + 15) / 16 * 16;   // each slab 16-byte aligned
+        if (used + bytes > kSlabBudget) continue;
+        if (reads < static_cast<__int128>(kSlabReuse) * distinct) continue;
+        if (reads < static_cast<__int128>(kSlabReuse) * span * workgroups) continue;
+        used += bytes;
+        out.push_back(Slab{b, lo, span});
+    }
+    return out;
+}
+
 struct Reg {
     uint32_t buf;
     std::string name;
@@ -386,6 +481,7 @@ struct Emitter {
     std::vector<uint32_t> slots;      // slot -> buffer id
     std::vector<int> slotOf;          // buffer id -> slot
     std::vector<Reg> regs;            // register-held buffers in scope
+    std::vector<Slab> slabs;          // LDS-staged inputs
     std::vector<int> memReads, memStores, memAdds;
     std::string code;
     int nextReg{0};
@@ -470,6 +566,13 @@ struct Emitter {
         const std::string dt = std::to_string(dtypeCode(km.buffers[b].dtype));
         const std::string f = affineCode(at, r.size());
         ++memReads[b];
+        for (size_t k = 0; k < slabs.size(); ++k) {
+            // The slab's hull covers every read of the buffer in the root.
+            if (slabs[k].buf == b) {
+                return "mlk::loadOne<" + dt + ">(mlk_slab" + std::to_string(k) + ", " + f + " - " +
+                       intLit(slabs[k].lo) + ")";
+            }
+        }
         if (inBounds(b, at, r)) return "mlk::loadOne<" + dt + ">(mb" + std::to_string(s) + ", " + f + ")";
         checked = true;
         return "mlk_ld_chk<" + dt + ">(mb" + std::to_string(s) + ", " + f + ", a.n[" + std::to_string(s) +
@@ -747,6 +850,13 @@ Result<Step> planNest(const KernelModule& km, uint32_t root) {
     }
 
     Emitter em(cx);
+    const int64_t workgroups = std::min<int64_t>(std::max<int64_t>((static_cast<int64_t>(total) + 255) / 256, 1),
+                                                 16384);   // the launch grid (driver gridFor)
+    // Schedule parameter "hip_slabs" = 0 keeps every buffer in global memory
+    // (the reference's slabs are likewise an emitter option,
+    // slab_plan.h:51-62).
+    if (km.param("hip_slabs", 1) != 0) em.slabs = planSlabs(km, root, workgroups);
+    for (const Slab& sl : em.slabs) em.slot(sl.buf);
     // The thread body: the last chain loop's children, or the root itself.
     const int ind = 2;
     std::string chainCodeText;
@@ -790,6 +900,10 @@ Result<Step> planNest(const KernelModule& km, uint32_t root) {
     src += "// mlk-nest slots:";
     for (const uint32_t b : em.slots) src += " " + std::to_string(b);
     src += "\n// mlk-nest instances: " + std::to_string(static_cast<int64_t>(total)) + "\n";
+    for (const Slab& sl : em.slabs) {
+        src += "// mlk-nest slab: buffer " + std::to_string(sl.buf) + " elements [" + std::to_string(sl.lo) + ", " +
+               std::to_string(sl.lo + sl.span) + ")\n";
+    }
     src += deviceMathHeader();
     src += R"(
 struct mlk_nest_args {
@@ -798,6 +912,13 @@ struct mlk_nest_args {
     int* status;
     long long elements;
 };
+
+// The workgroup's threads share each slab's copy; a host harness that runs
+// one thread at a time defines these to copy the whole slab per thread.
+#ifndef MLK_SLAB_FIRST
+#define MLK_SLAB_FIRST static_cast<long long>(threadIdx.x)
+#define MLK_SLAB_STEP 256
+#endif
 
 template <int DT>
 __device__ __forceinline__ double mlk_ld_chk(const void* p, long long f, long long n, int* st, bool& bad) {
@@ -816,6 +937,17 @@ extern "C" __global__ __launch_bounds__(256) void mlk_nest(const mlk_nest_args a
     for (size_t s = 0; s < em.slots.size(); ++s) {
         src += "    void* const mb" + std::to_string(s) + " = a.p[" + std::to_string(s) + "];\n";
     }
+    for (size_t k = 0; k < em.slabs.size(); ++k) {
+        const Slab& sl = em.slabs[k];
+        const Dtype d = km.buffers[sl.buf].dtype;
+        const std::string ty = d == Dtype::F32 ? "float" : (d == Dtype::F16 ? "_Float16" : "double");
+        const std::string nm = "mlk_slab" + std::to_string(k);
+        const std::string mb = "mb" + std::to_string(em.slotOf[sl.buf]);
+        src += "    __shared__ __attribute__((aligned(16))) " + ty + " " + nm + "[" + intLit(sl.span) + "];\n";
+        src += "    for (long long i = MLK_SLAB_FIRST; i < " + intLit(sl.span) + "; i += MLK_SLAB_STEP) " + nm +
+               "[i] = static_cast<const " + ty + "*>(" + mb + ")[" + intLit(sl.lo) + " + i];\n";
+    }
+    if (!em.slabs.empty()) src += "    __syncthreads();\n";
     src += "    const long long stride = static_cast<long long>(gridDim.x) * 256;\n";
     src += "    for (long long g = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; g < total; g += stride) {\n";
     src += chainLen > 0 ? chainCodeText : "        (void)g;\n";

@@ -873,7 +873,8 @@ Result<Plan> planModule(const KernelModule& input) {
     // guarded bands folded back to their untiled shapes, canonical.cpp).
     // Two schedule parameters select the path for tests and variant search:
     // "hip_canonical" = 0 plans the module as written, "hip_generic" = 1 runs
-    // every multi-dim root on the generic loop-nest kernel.
+    // every multi-dim root on the generic loop-nest kernel. ("hip_slabs" = 0,
+    // read by planNest, turns that kernel's LDS slabs off.)
     const bool multiDim = isMultiDimModule(input);
     const bool canon = input.param("hip_canonical", 1) != 0;
     const bool genericOnly = input.param("hip_generic", 0) != 0;

@@ -12,6 +12,12 @@
 #define __global__
 #define __forceinline__ inline
 #define __launch_bounds__(...)
+// LDS slabs: one static copy stands for the workgroup's, and each thread the
+// harness runs copies the whole slab before reading it.
+#define __shared__ static
+#define MLK_SLAB_FIRST 0LL
+#define MLK_SLAB_STEP 1LL
+inline void __syncthreads() {}
 
 struct mlk_dim3 {
     unsigned x, y, z;

@@ -132,6 +132,40 @@ def triangular_module(n=37) -> KernelModule:
     return km
 
 
+def weighted_rows_module(M=24, N=40, K=19, off=5, dtype="f64", stored_w=False) -> KernelModule:
+    """i, j parallel; k in [0,K): y[i,j] += w[k + off] * x[i,k]. Every (i, j)
+    re-reads w[off, off + K), and every j re-reads row i of x. With
+    ``stored_w`` a first root rewrites the input w in place (w[t] = w[t] * 1),
+    so w is no longer read-only anywhere in the module."""
+    km = KernelModule()
+    nw = K + off + 3
+    w = km.add_buffer(KernelBuffer("w", dtype, True, False, False, nw, [nw]))
+    x = km.add_buffer(KernelBuffer("x", dtype, True, False, False, M * K, [M, K]))
+    y = km.add_buffer(KernelBuffer("y", dtype, False, True, False, M * N, [M, N]))
+    if stored_w:
+        c0 = km.add_node(KernelNode(op="compute", exprs=[KernelExpr("mul", elem_idx(w, [1]), const(1.0))]))
+        s0 = km.add_node(KernelNode(op="store", out=w, out_index_coeffs=[1]))
+        km.add_node(KernelNode(op="loop", var="t", begin=0, end=nw, children=[c0, s0]))
+    c = km.add_node(KernelNode(op="compute", exprs=[KernelExpr("mul", elem_idx(w, [0, 0, 1], off),
+                                                                elem_idx(x, [K, 0, 1]))]))
+    s = km.add_node(KernelNode(op="store", out=y, out_index_coeffs=[N, 1, 0], accum="add"))
+    kl = km.add_node(KernelNode(op="loop", var="k", begin=0, end=K, children=[c, s]))
+    jl = km.add_node(KernelNode(op="loop", var="j", begin=0, end=N, children=[kl], parallel=True))
+    km.add_node(KernelNode(op="loop", var="i", begin=0, end=M, children=[jl], parallel=True))
+    return km
+
+
+def weighted_rows_inputs(km):
+    # Multiples of 1/8 in [-4, 4): exact in f16, f32 and f64.
+    rng = np.random.default_rng(11)
+    return {b: rng.integers(-32, 32, km.buffers[b].elements).astype(np.float64) / 8.0 for b in (0, 1)}
+
+
+def slab_lines(km, step=0):
+    _, src = backend.compile_check(km, step)
+    return [ln for ln in src.splitlines() if ln.startswith("// mlk-nest slab:")]
+
+
 def host_vs_oracle(km, arrays, scalars=(), elements=0):
     st, cur = nesthost.run_module(km, arrays, scalars, elements, reverse=True)
     ref = oracle.run(km, {i: arrays[i] for i in km.input_ids()}, scalars, elements,
@@ -173,6 +207,47 @@ def test_tiled_elementwise_canonicalizes_to_template_class():
     assert backend.plan(km)[0] == "elementwise-nd"
     km = fx.tiled_elementwise_module(fx.lift_1d(fx.config1_module(n=1 << 20)), tile=32)
     assert backend.plan(km)[:2] == ("elementwise-nd", "tol-4ulp-f32-gfx950-v1")
+
+
+def test_slab_plan_follows_reuse_budget_and_stores():
+    # GEMM tiles re-read both operands within a workgroup: both staged whole.
+    km = generic(fx.tiled_gemm_module(70, 45, 37, "f32", tile=16, init="split", out_dtype="f32"))
+    assert slab_lines(km) == ["// mlk-nest slab: buffer 0 elements [0, 3150)",
+                              "// mlk-nest slab: buffer 1 elements [0, 1665)"]
+    # Hulls above the 64 KiB budget stay in global memory.
+    big = generic(fx.tiled_gemm_module(256, 160, 192, "f32", tile=32, init="split", out_dtype="f32"))
+    assert slab_lines(big) == []
+    # C3 tiled: the bias row is re-read by every row, x once. Tile indices
+    # only move the point loops' windows, so they are no reuse: x stays out.
+    c3 = generic(fx.tiled_elementwise_module(fx.config3_module(37, 100, tier=2), tile=32), False)
+    assert slab_lines(c3) == ["// mlk-nest slab: buffer 1 elements [0, 100)"]
+    # The hull starts where the reads start.
+    wr = generic(weighted_rows_module())
+    assert slab_lines(wr) == ["// mlk-nest slab: buffer 0 elements [5, 24)",
+                              "// mlk-nest slab: buffer 1 elements [0, 456)"]
+    # A buffer that any Store of the module targets is never staged, even in
+    # a root that only reads it.
+    ws = generic(weighted_rows_module(stored_w=True))
+    assert backend.plan(ws)[2] == 2
+    assert slab_lines(ws, 1) == ["// mlk-nest slab: buffer 1 elements [0, 456)"]
+    # The schedule parameter hip_slabs = 0 turns them off.
+    off = generic(weighted_rows_module())
+    off.schedule["hip_slabs"] = 0
+    assert slab_lines(off) == []
+
+
+@pytest.mark.parametrize("dtype", ["f64", "f32", "f16"])
+@pytest.mark.parametrize("stored_w", [False, True])
+def test_slabs_host(dtype, stored_w):
+    # Under AddressSanitizer every redirected read lands inside its slab's
+    # static copy; results stay bit-exact with the walker (inputs are exact
+    # in every dtype and the sums are held in f64).
+    km = generic(weighted_rows_module(dtype=dtype, stored_w=stored_w))
+    arrays = weighted_rows_inputs(km)
+    st, cur, ref = host_vs_oracle(km, arrays)
+    assert st == 0
+    want = ref[2].astype(np.float16).astype(np.float64) if dtype == "f16" else expected(ref[2], dtype)
+    assert nf.same_bits(cur[2], want)
 
 
 def test_tiled_gemm_collapses_all_parallel_levels():
@@ -294,6 +369,21 @@ def test_tiled_gemm_gpu(hip, init, shape):
         r = max_rel(got, ref)
         say(f"  {dtype} gemm-nest max_rel={r:.3e}")
         assert r <= 1e-5 * np.sqrt(k)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", ["f64", "f32", "f16"])
+def test_slabs_gpu(hip, dtype):
+    say(f"lds slabs weighted rows {dtype}")
+    for stored_w in (False, True):
+        km = weighted_rows_module(M=64, N=256, K=41, off=7, dtype=dtype, stored_w=stored_w)
+        g = generic(km)
+        assert any("buffer 1" in ln for ln in slab_lines(g, 1 if stored_w else 0))
+        arrays = weighted_rows_inputs(km)
+        ref = oracle.run(km, arrays)
+        got = hip.build(g).run(arrays)
+        want = ref[2].astype(np.float16).astype(np.float64) if dtype == "f16" else expected(ref[2], dtype)
+        assert nf.same_bits(got[2], want), (dtype, stored_w)
 
 
 @pytest.mark.gpu
