@@ -61,6 +61,7 @@ Result<std::unique_ptr<HipLoadedKernel>> buildHipKernelArtifact(const KernelModu
     if (!plan.has_value()) return err(plan.error().code, plan.error().message);
     k->plan_ = std::move(*plan);
     k->arch_ = config.arch;
+    k->cacheDir_ = config.cacheDir;
     k->bindIndex_.assign(km.buffers.size(), -1);
     for (uint32_t b = 0; b < km.buffers.size(); ++b) {
         const KernelBuffer& kb = km.buffers[b];
@@ -117,6 +118,7 @@ Result<std::unique_ptr<HipLoadedKernel>> buildHipKernelArtifact(const KernelModu
     k->scratchElems_.assign(km.buffers.size(), 0);
     k->stepScratch_.assign(k->plan_.steps.size(), nullptr);
     k->stepScratchBytes_.assign(k->plan_.steps.size(), 0);
+    k->noSlabFn_.assign(k->plan_.steps.size(), nullptr);
     return k;
 }
 
@@ -287,7 +289,22 @@ int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* 
                     }
                     na.status = static_cast<int*>(status_);
                 }
-                rc = mlkd_jit_launch_nest(st.fn, gridFor(st.threads), &na, &sc, st.threads, stream);
+                void* fn = st.fn;
+                if (st.variant == 1 && !st.sourceNoSlabs.empty()) {
+                    std::lock_guard<std::mutex> g(scratchLock_);
+                    if (noSlabFn_[si] == nullptr) {
+                        char log[4096] = {0};
+                        uint64_t fp = 0;
+                        if (mlkd_jit_build(st.sourceNoSlabs.data(), st.sourceNoSlabs.size(), "mlk_nest", arch_.c_str(),
+                                           cacheDir_.c_str(), &noSlabFn_[si], &fp, log, sizeof(log)) != 0) {
+                            noSlabFn_[si] = nullptr;
+                            why = std::string("loop-nest instance without slabs: ") + log;
+                            return MLKHIP_RUNTIME;
+                        }
+                    }
+                    fn = noSlabFn_[si];
+                }
+                rc = mlkd_jit_launch_nest(fn, gridFor(st.threads), &na, &sc, st.threads, stream);
                 if (rc == 0 && st.checked) {
                     int status = 0;
                     if (mlkd_rt_d2h(&status, status_, sizeof(status), stream) != 0 || mlkd_rt_sync(stream) != 0) {

@@ -75,6 +75,7 @@ private:
     KernelModule km_;
     Plan plan_;
     std::string arch_;
+    std::string cacheDir_;
     std::string fingerprint_;
     bool fromCache_{false};
     std::vector<uint32_t> bindables_;   // buffer ids in table order
@@ -90,6 +91,8 @@ private:
     // statistics), allocated on first use and kept.
     mutable std::vector<void*> stepScratch_;
     mutable std::vector<int64_t> stepScratchBytes_;
+    // Loop-nest launch form 1 (no LDS slabs), compiled on first use.
+    mutable std::vector<void*> noSlabFn_;
 };
 
 /// Essential work of a module (the reference's EssentialWork,

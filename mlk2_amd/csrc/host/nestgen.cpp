@@ -777,7 +777,7 @@ struct Emitter {
 
 }  // namespace
 
-Result<Step> planNest(const KernelModule& km, uint32_t root) {
+Result<Step> planNestWith(const KernelModule& km, uint32_t root, bool allowSlabs) {
     Ctx cx{km, false, ErrorCode::UnsupportedCapability, std::string(), 0};
     Step st;
     st.kind = StepKind::Nest;
@@ -852,11 +852,7 @@ Result<Step> planNest(const KernelModule& km, uint32_t root) {
     Emitter em(cx);
     const int64_t workgroups = std::min<int64_t>(std::max<int64_t>((static_cast<int64_t>(total) + 255) / 256, 1),
                                                  16384);   // the launch grid (driver gridFor)
-    // Schedule parameter "hip_slabs" = 0 keeps every buffer in global memory
-    // (the reference's slabs are likewise an emitter option,
-    // slab_plan.h:51-62).
-    if (km.param("hip_slabs", 1) != 0) em.slabs = planSlabs(km, root, workgroups);
-    for (const Slab& sl : em.slabs) em.slot(sl.buf);
+    if (allowSlabs) em.slabs = planSlabs(km, root, workgroups);
     // The thread body: the last chain loop's children, or the root itself.
     const int ind = 2;
     std::string chainCodeText;
@@ -893,6 +889,7 @@ Result<Step> planNest(const KernelModule& km, uint32_t root) {
         em.children(self, r, ind, 1);
     }
     if (cx.failed) return err(cx.code, cx.why);
+    for (const Slab& sl : em.slabs) em.slot(sl.buf);   // read by the emitted code, so already bound
 
     std::string src;
     src += "// generic loop nest: root node " + std::to_string(root) + ", " + std::to_string(chainLen) +
@@ -942,7 +939,7 @@ extern "C" __global__ __launch_bounds__(256) void mlk_nest(const mlk_nest_args a
         const Dtype d = km.buffers[sl.buf].dtype;
         const std::string ty = d == Dtype::F32 ? "float" : (d == Dtype::F16 ? "_Float16" : "double");
         const std::string nm = "mlk_slab" + std::to_string(k);
-        const std::string mb = "mb" + std::to_string(em.slotOf[sl.buf]);
+        const std::string mb = "mb" + std::to_string(em.slot(sl.buf));
         src += "    __shared__ __attribute__((aligned(16))) " + ty + " " + nm + "[" + intLit(sl.span) + "];\n";
         src += "    for (long long i = MLK_SLAB_FIRST; i < " + intLit(sl.span) + "; i += MLK_SLAB_STEP) " + nm +
                "[i] = static_cast<const " + ty + "*>(" + mb + ")[" + intLit(sl.lo) + " + i];\n";
@@ -955,6 +952,7 @@ extern "C" __global__ __launch_bounds__(256) void mlk_nest(const mlk_nest_args a
     src += "    }\n}\n";
 
     st.source = std::move(src);
+    st.slabs = static_cast<int>(em.slabs.size());
     st.nestBufs = em.slots;
     st.threads = static_cast<int64_t>(total);
     st.collapsed = static_cast<int>(chainLen);
@@ -968,6 +966,18 @@ extern "C" __global__ __launch_bounds__(256) void mlk_nest(const mlk_nest_args a
             st.narrowRoundTrip = true;
         }
     }
+    return st;
+}
+
+Result<Step> planNest(const KernelModule& km, uint32_t root) {
+    // Schedule parameter "hip_slabs" = 0 keeps every buffer in global memory
+    // (the reference's slabs are likewise an emitter option,
+    // slab_plan.h:51-62).
+    auto st = planNestWith(km, root, km.param("hip_slabs", 1) != 0);
+    if (!st.has_value() || st->slabs == 0) return st;
+    auto plain = planNestWith(km, root, false);
+    if (!plain.has_value() || plain->nestBufs != st->nestBufs) return st;   // same slots: one binding serves both
+    st->sourceNoSlabs = std::move(plain->source);
     return st;
 }
 

@@ -59,6 +59,10 @@ struct Step {
     // means some access carries a run-time bounds check whose status word is
     // read back after the launch.
     uint32_t root{kInvalidId};
+    // LDS slabs of the nest kernel, and the same kernel without them (empty
+    // when it has none): launch form 1 of the step, compiled on first use.
+    int slabs{0};
+    std::string sourceNoSlabs;
     std::vector<uint32_t> nestBufs;
     std::vector<uint32_t> nestWrites;
     int64_t threads{0};

@@ -381,6 +381,10 @@ std::vector<int> variantSpace(const KernelModule& km, const Step& st) {
                 return v;
             }
             return {};
+        case StepKind::Nest:
+            // 0: with the step's LDS slabs; 1: the same kernel without them.
+            if (!st.sourceNoSlabs.empty()) return {0, 1};
+            return {};
         default: return {};
     }
 }

@@ -12,6 +12,7 @@ import pytest
 
 from mlk2_amd import backend as be
 from mlk2_amd import fixtures as fx
+import test_nest as tn
 from mlk2_amd.kernel_ir import KernelExpr, const, elem_a, temp
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -128,6 +129,8 @@ def test_chain_codegen_exact_constants():
     (fx.config4_module(1024, 1024, 1024, "f32", 2), []),
     (fx.config1_module(1 << 12), []),
     (fx.config4_module(64, 64, 64, "f16", 1), []),     # below the 256-multiple tiles
+    (tn.generic(tn.weighted_rows_module()), [0, 1]),  # loop nest with LDS slabs, and without
+    (tn.generic(fx.lift_1d(fx.config1_module(n=1 << 12)), False), []),   # loop nest without slabs
 ])
 def test_declared_variant_space(km, space):
     assert be.plan_variants(km, 0) == space

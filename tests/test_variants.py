@@ -5,7 +5,8 @@ them without disturbing the caller's buffers; its choice is cached under the
 artifact's fingerprint and applied by a later build.
 
 Tolerances as in test_gpu_parity: softmax <= 1e-6 relative; f16 GEMM and
-score+softmax <= 1e-2 relative (|got-ref|/max(|ref|,1)).
+score+softmax <= 1e-2 relative (|got-ref|/max(|ref|,1)); the loop-nest
+kernel's forms (with and without LDS slabs) are bit-exact.
 """
 import math
 import sys
@@ -90,6 +91,18 @@ def _gemm_call_acc_case(m=256, k=128, n=512):
     return km, bufs, 2, ref, 1e-2
 
 
+def _nest_case(m=64, n=256, k=41):
+    # The generic loop-nest kernel with LDS slabs (form 0) and without (1):
+    # the same reads from another place, so both are bit-exact.
+    from test_nest import generic, weighted_rows_inputs, weighted_rows_module
+    km = generic(weighted_rows_module(M=m, N=n, K=k, off=7, dtype="f32"))
+    arr = weighted_rows_inputs(km)
+    ref = oracle.run(km, arr)[2].astype(np.float32).astype(np.float64)
+    bufs = {0: DeviceBuffer.from_array(arr[0], "f32"), 1: DeviceBuffer.from_array(arr[1], "f32"),
+            2: DeviceBuffer(m * n, "f32")}
+    return km, bufs, 2, ref, 0.0
+
+
 CASES = {
     "gemm-f16-call-accumulate": _gemm_call_acc_case,
     "softmax-512x4096": _softmax_case,
@@ -97,6 +110,7 @@ CASES = {
     "gemm-f16-512x1024x512": _gemm_case,
     "score-2x512x128": _score_case,
     "score-1x2048x128": lambda: _score_case(1, 2048, 128),
+    "nest-slabs-64x256x41": _nest_case,
 }
 
 
@@ -147,7 +161,8 @@ def test_set_variant_outside_space_refused(hip):
     assert art.step_variant(7) == -2
 
 
-@pytest.mark.parametrize("name", ["softmax-512x4096", "gemm-f16-512x1024x512", "score-2x512x128"])
+@pytest.mark.parametrize("name", ["softmax-512x4096", "gemm-f16-512x1024x512", "score-2x512x128",
+                                  "nest-slabs-64x256x41"])
 def test_autotune_certifies_restores_and_caches(hip, name, tmp_path):
     km, bufs, out, ref, tol = CASES[name]()
     # A sentinel in the output: the search must hand the buffer back as it was.
@@ -200,7 +215,8 @@ def test_autotune_certifies_restores_and_caches(hip, name, tmp_path):
     assert art2.step_variant(0) == step["chosen"]
     # Another shape has another fingerprint and ignores the entry.
     km3, _, _, _, _ = (_softmax_case(256, 4096) if name.startswith("softmax") else
-                       _gemm_case(256, 1024, 512) if name.startswith("gemm") else _score_case(1, 512, 128))
+                       _gemm_case(256, 1024, 512) if name.startswith("gemm") else
+                       _nest_case(32, 256, 41) if name.startswith("nest") else _score_case(1, 512, 128))
     art3 = hip.build(km3, cache_dir=str(tmp_path))
     assert art3.fingerprint != fp
     assert not art3.variants_from_cache
