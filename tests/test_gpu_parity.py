@@ -112,7 +112,10 @@ def test_scalar_param_and_two_inputs_1d(hip):
 
 # ------------------------------------------------------------------ C2 ----
 @pytest.mark.parametrize("shape,tier", [((8192, 4096), 1), ((512, 4096), 2), ((33, 100), 1),
-                                        ((7, 9000), 1), ((64, 256), 2)])
+                                        ((7, 9000), 1), ((64, 256), 2),
+                                        # odd row counts on the guard-free pair kernel
+                                        # (the last row pairs with itself)
+                                        ((3, 4096), 1), ((1, 256), 1), ((4097, 1024), 2)])
 def test_c2_softmax(hip, shape, tier):
     m, k = shape
     say(f"c2 softmax {m}x{k} tier{tier}")
