@@ -16,7 +16,7 @@ import oracle
 from mlk2_amd import fixtures as fx
 from mlk2_amd import inputs
 from mlk2_amd.backend import DeviceBuffer, MlkHipError
-from mlk2_amd.kernel_ir import KernelExpr, const, elem_a, elem_b, scalar, temp
+from mlk2_amd.kernel_ir import KernelExpr, elem_a, elem_b, scalar, temp
 from mlk2_amd.parity import max_rel, ulp_distance_f32
 
 pytestmark = pytest.mark.gpu

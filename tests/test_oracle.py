@@ -15,7 +15,7 @@ import pytest
 import oracle
 from mlk2_amd import fixtures as fx
 from mlk2_amd.kernel_ir import (KernelBuffer, KernelExpr, KernelModule, KernelNode,
-                                const, elem_idx, temp)
+                                const, elem_idx)
 from mlk2_amd.parity import ulp_distance_f64
 
 
