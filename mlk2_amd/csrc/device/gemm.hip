@@ -753,7 +753,6 @@ constexpr int kDmaBK = 32, kDmaStages = 4;
 constexpr int kDmaA = 256 * kDmaBK;                   // halves per A stage
 constexpr int kDmaStage = 2 * kDmaA;                  // A then B
 constexpr size_t kLdsDma = static_cast<size_t>(kDmaStages) * kDmaStage * sizeof(_Float16);   // 128 KiB
-constexpr int kDmaPerWave = 8;                        // direct loads per wave per stage
 
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef __fp16 fp16x4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
@@ -881,7 +880,8 @@ __global__ __launch_bounds__(256, 1) void gemmF16Dma(const _Float16* __restrict_
     };
 
     DmaFrag x, y;
-    // Stage 0 landed (stages 1 and 2 may be in flight).
+    // Stage 0 landed (stages 1 and 2, 8 direct loads each per wave, may be
+    // in flight).
     asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
     asm volatile("s_barrier" ::: "memory");
 #pragma unroll
@@ -889,8 +889,9 @@ __global__ __launch_bounds__(256, 1) void gemmF16Dma(const _Float16* __restrict_
     for (int s = 0; s < steps; ++s) {
         const uint32_t cb = ldsBase + 2u * static_cast<uint32_t>((s % kDmaStages) * kDmaStage);
         subStep(x, y, cb, 1);   // sub-step (s, 0); reads (s, 1)
-        // Stage s + 1 landed (one later stage may be in flight); after the
-        // barrier every wave is past step s - 1, so its slot can be refilled.
+        // Stage s + 1 landed (one later stage, 8 direct loads per wave, may be
+        // in flight); after the barrier every wave is past step s - 1, so its
+        // slot can be refilled.
         asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
         asm volatile("s_barrier" ::: "memory");
         issue(s + kDmaStages - 1);
@@ -930,8 +931,8 @@ constexpr int kFDepth = 2;   // K steps of global loads in flight ahead of the M
 template <bool ACC>
 __global__ __launch_bounds__(256) void gemmF32Mfma(const float* __restrict__ A,
                                                    const float* __restrict__ B,
-                                                   float* __restrict__ C, int M, int N, int K,
-                                                   int64_t lda, int64_t ldb, int64_t ldc,
+                                                   float* __restrict__ C, int /*M: the grid covers it*/, int N,
+                                                   int K, int64_t lda, int64_t ldb, int64_t ldc,
                                                    int /*accumulate: template ACC*/) {
     __shared__ float At[2][kFK][kFM + 4];   // transposed: [k][m]
     __shared__ float Bs[2][kFK][kFN + 4];   // as loaded: [k][n]

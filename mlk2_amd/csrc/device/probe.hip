@@ -97,29 +97,32 @@ extern "C" int mlkd_probe_environment(double* bytes_per_sec, double* f16_flops_p
         hipLaunchKernelGGL(probeFill, dim3(copyBlocks), dim3(256), 0, st, static_cast<f32x4p*>(x), n4);
         hipLaunchKernelGGL(probeCopy, dim3(copyBlocks), dim3(256), 0, st, static_cast<const f32x4p*>(x),
                            static_cast<f32x4p*>(y), n4);   // warm-up
+        if (hipGetLastError() != hipSuccess) break;
         constexpr int kReps = 5;
-        hipEventRecord(e0, st);
+        if (hipEventRecord(e0, st) != hipSuccess) break;
         for (int r = 0; r < kReps; ++r) {
             hipLaunchKernelGGL(probeCopy, dim3(copyBlocks), dim3(256), 0, st, static_cast<const f32x4p*>(x),
                                static_cast<f32x4p*>(y), n4);
         }
-        hipEventRecord(e1, st);
+        if (hipGetLastError() != hipSuccess || hipEventRecord(e1, st) != hipSuccess) break;
         float ms = 0.0f;
         if (hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess || ms <= 0.0f) break;
-        *bytes_per_sec = 2.0 * static_cast<double>(kBytes) * kReps / (1e-3 * ms);
+        const double bytesPerSec = 2.0 * static_cast<double>(kBytes) * kReps / (1e-3 * ms);
         hipLaunchKernelGGL(probeMfma, dim3(mfmaBlocks), dim3(256), 0, st, out, 10, 0.01f);
-        hipEventRecord(e0, st);
+        if (hipGetLastError() != hipSuccess || hipEventRecord(e0, st) != hipSuccess) break;
         hipLaunchKernelGGL(probeMfma, dim3(mfmaBlocks), dim3(256), 0, st, out, kIters, 0.01f);
-        hipEventRecord(e1, st);
+        if (hipGetLastError() != hipSuccess || hipEventRecord(e1, st) != hipSuccess) break;
         if (hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess || ms <= 0.0f) break;
         const double flops = static_cast<double>(mfmaBlocks) * 4 * kIters * 16 * (2.0 * 32 * 32 * 16);
+        *bytes_per_sec = bytesPerSec;
         *f16_flops_per_sec = flops / (1e-3 * ms);
-        rc = hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
+        rc = 0;
     } while (false);
-    if (e0 != nullptr) hipEventDestroy(e0);
-    if (e1 != nullptr) hipEventDestroy(e1);
-    if (out != nullptr) hipFree(out);
-    if (y != nullptr) hipFree(y);
-    if (x != nullptr) hipFree(x);
+    // Best-effort release: a failure here leaves nothing further to undo.
+    if (e0 != nullptr) (void)hipEventDestroy(e0);
+    if (e1 != nullptr) (void)hipEventDestroy(e1);
+    if (out != nullptr) (void)hipFree(out);
+    if (y != nullptr) (void)hipFree(y);
+    if (x != nullptr) (void)hipFree(x);
     return rc;
 }
