@@ -59,7 +59,7 @@ def normal(seed: int, n: int, mean: float = 0.0, std: float = 1.0, dtype: str = 
 
 
 def config_inputs(config: str, scale: dict | None = None) -> dict:
-    """Seeded inputs for a config at its BASELINE shape, or at the reduced
+    """Seeded inputs for a config at its benchmark shape, or at the reduced
     shape given by ``scale`` (same generators, fewer elements)."""
     s = scale or {}
     if config == "c1":
