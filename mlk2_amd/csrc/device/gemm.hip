@@ -25,6 +25,7 @@
 
 #include <stdint.h>
 
+#include "mlk_device_math.h"
 #include "runtime_abi.h"
 
 namespace {
@@ -1029,7 +1030,8 @@ __device__ __forceinline__ void stAny(void* p, int dt, int64_t i, T v) {
     if (dt == MLKD_F32) {
         static_cast<float*>(p)[i] = static_cast<float>(v);
     } else if (dt == MLKD_F16) {
-        static_cast<_Float16*>(p)[i] = static_cast<_Float16>(static_cast<float>(v));
+        if constexpr (sizeof(T) == sizeof(double)) static_cast<_Float16*>(p)[i] = mlk::toHalf(v);
+        else static_cast<_Float16*>(p)[i] = static_cast<_Float16>(v);
     } else {
         static_cast<double*>(p)[i] = static_cast<double>(v);
     }

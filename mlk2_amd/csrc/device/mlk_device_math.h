@@ -1,10 +1,12 @@
 // Device math shared by every hipRTC instance (the elementwise template and
-// the generic loop-nest kernels) and by nothing else: the poly7 sine of
+// the generic loop-nest kernels): the poly7 sine of
 // compiler/include/mlk/support/math_families.h:22-90 in its exact f64 form
 // and its split-precision form, the scalar-parameter block, and one-element
 // loads and stores of the three buffer dtypes with the rounding the artifact
-// ABI promises (f64 -> f32 RNE, f64 -> f16 with a single rounding).
-// Instances are compiled with -ffp-contract=off.
+// ABI promises (f64 -> f32 RNE, f64 -> f16 with a single rounding). The
+// static kernels' f64 paths (general softmax, general GEMM, unfused score)
+// include it for that f16 store. Instances are compiled with
+// -ffp-contract=off.
 #ifndef MLK_DEVICE_MATH_H
 #define MLK_DEVICE_MATH_H
 

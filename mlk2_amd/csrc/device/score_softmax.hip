@@ -16,6 +16,7 @@
 
 #include <stdint.h>
 
+#include "mlk_device_math.h"
 #include "runtime_abi.h"
 
 namespace {
@@ -924,7 +925,7 @@ __global__ __launch_bounds__(256) void scoresGeneral(mlkd_score_softmax p) {
         } else if (p.s_dtype == MLKD_F64) {
             static_cast<double*>(p.s)[t] = v;
         } else {
-            static_cast<_Float16*>(p.s)[t] = static_cast<_Float16>(static_cast<float>(v));
+            static_cast<_Float16*>(p.s)[t] = mlk::toHalf(v);
         }
     }
 }

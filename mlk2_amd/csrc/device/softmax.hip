@@ -19,6 +19,7 @@
 #include <math.h>
 #include <stdint.h>
 
+#include "mlk_device_math.h"
 #include "runtime_abi.h"
 
 namespace {
@@ -206,7 +207,7 @@ __device__ __forceinline__ void storeAny(void* p, int dt, int64_t i, double v) {
     if (dt == MLKD_F32) {
         static_cast<float*>(p)[i] = static_cast<float>(v);
     } else if (dt == MLKD_F16) {
-        static_cast<_Float16*>(p)[i] = static_cast<_Float16>(static_cast<float>(v));
+        static_cast<_Float16*>(p)[i] = mlk::toHalf(v);
     } else {
         static_cast<double*>(p)[i] = v;
     }

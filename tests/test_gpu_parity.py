@@ -16,7 +16,8 @@ import oracle
 from mlk2_amd import fixtures as fx
 from mlk2_amd import inputs
 from mlk2_amd.backend import DeviceBuffer, MlkHipError
-from mlk2_amd.kernel_ir import KernelExpr, elem_a, elem_b, scalar, temp
+from mlk2_amd.kernel_ir import (KernelBuffer, KernelExpr, KernelModule, KernelNode, elem_a, elem_b,
+                                 scalar, temp)
 from mlk2_amd.parity import max_rel, ulp_distance_f32
 
 pytestmark = pytest.mark.gpu
@@ -251,6 +252,23 @@ def test_c4b_gemm_f16(hip, m, k, n):
     assert e <= 1e-2
 
 
+@pytest.mark.parametrize("m,k,n", [(100, 70, 33), (128, 256, 64)])
+def test_gemm_f64_buffers(hip, m, k, n):
+    # f64 operands and output take the general tiled kernel in f64, k
+    # ascending per output element: 1e-12 relative, where an f32 accumulator
+    # anywhere would show near 1e-6. Both the Call and the poly.synth nest.
+    say(f"gemm f64 {m}x{k}x{n}")
+    A = inputs.normal(11, m * k).reshape(m, k)
+    B = inputs.normal(12, k * n).reshape(k, n)
+    ref = _gemm_ref(A, B)
+    call = fx.matmul_call_module(m, k, n, "f64", "f64")
+    for km in (call, fx.synth_gemm(call)):
+        got = hip.build(km).run({0: A, 1: B})[2].reshape(m, n)
+        e = max_rel(got, ref)
+        say(f"gemm f64 {m}x{k}x{n} max_rel={e:.3e}")
+        assert e <= 1e-12
+
+
 def test_c4b_full_size_sampled_rows(hip):
     # 4096^3 on the device; 32 sampled rows recomputed by the oracle's GEMM.
     m = k = n = 4096
@@ -295,6 +313,27 @@ def test_c5_score_softmax(hip, b, s, dm):
     e = max_rel(got, ref)
     say(f"c5 max_rel={e:.3e}")
     assert e <= 1e-2
+
+
+@pytest.mark.parametrize("b,s,dm", [(2, 128, 128), (1, 24, 8), (1, 300, 20)])
+def test_c5_score_softmax_f64_operands(hip, b, s, dm):
+    # Q and K held as f64 take the general score kernel (f64 dot products,
+    # one thread per score) and then the row softmax in place over S. S is
+    # an f32 buffer, so each score (|score| < 6 here) is rounded to f32
+    # before its exponential, about 1e-7 in the outputs. Held to 1e-5, where
+    # operands rounded to f16 would be off by about 1e-4.
+    say(f"c5 score softmax f64 operands b={b} s={s} d={dm}")
+    km = fx.score_softmax_module(b, s, dm, "f64")
+    Q = inputs.normal(21, b * s * dm)
+    K = inputs.normal(22, b * s * dm)
+    bias = inputs.uniform(23, s, -1, 1)
+    art = hip.build(km)
+    assert art.class_name == "score-softmax"
+    got = art.run({0: Q, 1: K, 2: bias})[3]
+    ref = oracle.run(km, {0: Q, 1: K, 2: bias.astype(np.float32).astype(np.float64)}, hw_threads=8)[3]
+    e = max_rel(got, ref)
+    say(f"c5 f64 operands max_rel={e:.3e}")
+    assert e <= 1e-5
 
 
 def _score_ref(Q, K, bias, rows=None):
@@ -382,3 +421,72 @@ def test_reducesum_call_and_nest(hip):
         got = hip.build(km).run({0: x})[1]
         ref = oracle.run(fx.reducesum_call_module(M, K), {0: x})[1]
         assert max_rel(got, ref) <= 1e-6
+
+
+@pytest.mark.parametrize("dtype", ["f64", "f16"])
+@pytest.mark.parametrize("m,k", [(37, 300), (5, 9001), (16, 4096)])
+def test_softmax_and_rowsum_on_f64_and_f16_buffers(hip, dtype, m, k):
+    # Buffers other than f32 take the general block-per-row softmax and the
+    # wave row sum, both in f64 like the reference (kernel_buffers.cpp:237-340).
+    # The device rounds inputs to the buffer dtype on upload and outputs once
+    # on store, so the oracle sees the rounded inputs and its outputs are
+    # rounded the same way. f64 buffers are held to 1e-12 (an f32 intermediate
+    # anywhere would show at 1e-7). f16 outputs must equal the oracle's f64
+    # result rounded once: an f64 -> f32 -> f16 store misrounds about one
+    # value in 8192, which these shapes hit.
+    say(f"softmax/rowsum {dtype} {m}x{k}")
+    x = inputs.normal(inputs.SEEDS["c2_x"], m * k, 0.0, 2.0)
+    if dtype == "f16":
+        x = x.astype(np.float16).astype(np.float64)
+    tol = 1e-12 if dtype == "f64" else 0.0
+
+    def rounded(v):
+        return v.astype(np.float16).astype(np.float64) if dtype == "f16" else v
+
+    call = fx.softmax_call_module(m, k, dtype)
+    ref = rounded(oracle.run(fx.softmax_call_module(m, k, "f64"), {0: x})[1])
+    for km in (call, fx.synth_softmax(call)):
+        got = hip.build(km).run({0: x})[1]
+        e = max_rel(got, ref)
+        say(f"softmax {dtype} {m}x{k} max_rel={e:.3e}")
+        assert e <= tol
+    rs = fx.reducesum_call_module(m, k, dtype)
+    ref = rounded(oracle.run(fx.reducesum_call_module(m, k, "f64"), {0: x})[1])
+    for km in (rs, fx.synth_reducesum(rs)):
+        got = hip.build(km).run({0: x})[1]
+        e = max_rel(got, ref)
+        say(f"rowsum {dtype} {m}x{k} max_rel={e:.3e}")
+        assert e <= tol
+
+
+def _tie_neighbours():
+    # Values just above, just below and exactly on the midpoint between f16
+    # neighbours (normal, smallest-normal and subnormal). Rounding f64 -> f32
+    # -> f16 lands 11 of them on the tie and then rounds to even, the wrong way.
+    h = np.array([1.0, 1.0009765625, 3.140625, 1000.0, 6.103515625e-05, 1.7881393432617188e-07,
+                  0.25 + 2.0 ** -12], dtype=np.float16)
+    lo = h.astype(np.float64)
+    hi = np.nextafter(h, np.float16(np.inf)).astype(np.float64)
+    t = (lo + hi) / 2
+    v = np.concatenate([t * (1 + 2.0 ** -40), t * (1 - 2.0 ** -40), t, -t * (1 + 2.0 ** -40)])
+    assert (v.astype(np.float16) != v.astype(np.float32).astype(np.float16)).sum() == 11
+    return v
+
+
+def test_f64_results_stored_to_f16_round_once(hip):
+    # The artifact ABI's f64 -> f16 store is one round-to-nearest-even of the
+    # f64 value (numpy's astype(float16) is that rounding). A k = 1 GEMM
+    # (C = A * 1) and a one-column row sum hand each value to the store as is.
+    say("f16 stores round once")
+    v = _tie_neighbours()
+    m = len(v)
+    want = v.astype(np.float16).astype(np.float64)
+    km = fx.matmul_call_module(m, 1, 1, "f64", "f16")
+    got = hip.build(km).run({0: v, 1: np.ones(1)})[2]
+    assert np.array_equal(got, want), np.c_[v, got, want][got != want]
+    km = KernelModule()
+    x = km.add_buffer(KernelBuffer("X", "f64", True, False, False, m, [m, 1]))
+    y = km.add_buffer(KernelBuffer("Y", "f16", False, True, False, m, [m]))
+    km.add_node(KernelNode(op="call", math="reduce_sum", a=x, out=y))
+    got = hip.build(km).run({0: v})[1]
+    assert np.array_equal(got, want), np.c_[v, got, want][got != want]
