@@ -59,7 +59,7 @@ __device__ __forceinline__ double mlk_p7_sin(double x) {
 }
 
 /// poly7 sin for a value rounded to f32 right after (the planner uses it
-/// only when sin is the chain's last op and the output is f32/f16). The
+/// only when sin is the chain's last op and the output is f32). The
 /// reduction r = (x - n*hi) - n*lo stays in f64; the residual polynomials run
 /// in f32 on r rounded to f32 (|r| <= pi/4: ~1 f32 ULP, plus r's own 0.5 ULP
 /// relative rounding). n = floor(x*2/pi + 0.5) can differ from the

@@ -320,7 +320,11 @@ Result<Step> elementwiseNest(const KernelModule& km, const NestInfo& ni) {
         return static_cast<int>(ins.size() - 1);
     };
     const Dtype od = km.buffers[so.bufferOut].dtype;
-    const bool f32Out = (od == Dtype::F32 || od == Dtype::F16) && so.accum == AccumMode::None;
+    // Split-precision sin only where its result is rounded to f32. An f16
+    // output keeps the exact f64 form: its one rounding then gives the
+    // reference's f16 value bit for bit, where a few f32 ULP of error would
+    // move about one value in a thousand to the neighbouring f16.
+    const bool f32Out = od == Dtype::F32 && so.accum == AccumMode::None;
     auto body = chainCode(cp.exprs, cp.family == "poly7", f32Out, streamCode(streamOf), "return ");
     if (!body.has_value()) return err(body.error().code, body.error().message);
     if (bad) return err(ErrorCode::UnsupportedCapability, "more than 4 distinct element streams");
@@ -410,8 +414,8 @@ Result<std::vector<Step>> tier1Loop(const KernelModule& km, const KernelNode& lo
             return -1;  // ElemIdx is a multi-dim operand
         };
         const Dtype od = km.buffers[so.bufferOut].dtype;
-        auto body = chainCode(exprs, c.family == "poly7", od == Dtype::F32 || od == Dtype::F16,
-                              streamCode(streamOf), "return ");
+        // Split-precision sin for f32 outputs only, as in the n-D path.
+        auto body = chainCode(exprs, c.family == "poly7", od == Dtype::F32, streamCode(streamOf), "return ");
         if (!body.has_value()) return err(body.error().code, body.error().message);
         st.chainBody = *body;
         st.out = ref(so.bufferOut);

@@ -77,6 +77,21 @@ def test_c1_f64_buffers_bit_exact(hip):
     assert np.array_equal(got.view(np.int64), ref.view(np.int64))
 
 
+@pytest.mark.parametrize("n", [1000, 1 << 20])
+def test_c1_f16_buffers_bit_exact(hip, n):
+    # An f16 output keeps the exact f64 chain, so its one rounding gives the
+    # reference's value rounded to f16, bit for bit. The split-precision sine
+    # would move about one value in a thousand to the neighbouring f16.
+    say(f"c1 f16 bit-exact n={n}")
+    x = inputs.uniform(inputs.SEEDS["c1_x"], n, -40.0, 40.0, "f64").astype(np.float16).astype(np.float64)
+    km = fx.config1_module(n=n, dtype="f16")
+    art = hip.build(km)
+    assert art.policy == "bitexact-rne-gfx950-v1"
+    got = art.run({0: x})[1]
+    want = oracle.run(fx.config1_module(n=n, dtype="f64"), {0: x})[1].astype(np.float16).astype(np.float64)
+    assert np.array_equal(got, want), int((got != want).sum())
+
+
 def test_c1_dynamic_bound_legacy_form(hip):
     # loop end = kKernelLoopDynamicBound: the extent comes from io.elements
     # (kernel_buffers.cpp:966-969), through the legacy 1-D ABI.
@@ -194,6 +209,34 @@ def test_c3_broadcast_chain(hip, rows, cols):
     u = ulp_distance_f32(got.astype(np.float32), ref)
     say(f"c3 max_rel={e:.3e} max_ulp={u.max()}")
     assert e <= 1e-6
+
+
+def test_elementwise_nd_f16_buffers(hip):
+    # The n-D template on f16 buffers: the poly7 chain lifted to a nest and
+    # the C3 broadcast chain. Each keeps its f64 chain and rounds once to
+    # f16, so the outputs equal the oracle's f64 values rounded to f16 (the
+    # exp chain within one f64 ULP before that rounding, which moves no f16
+    # value at these sizes).
+    say("elementwise n-D f16 buffers")
+    n = 1 << 16
+    x = inputs.uniform(inputs.SEEDS["c1_x"], n, -40.0, 40.0, "f64").astype(np.float16).astype(np.float64)
+    km = fx.lift_1d(fx.config1_module(n=n, dtype="f16"))
+    art = hip.build(km)
+    assert art.class_name == "elementwise-nd" and art.policy == "bitexact-rne-gfx950-v1"
+    want = oracle.run(fx.config1_module(n=n, dtype="f64"), {0: x})[1].astype(np.float16).astype(np.float64)
+    got = art.run({0: x})[1]
+    assert np.array_equal(got, want), int((got != want).sum())
+    rows, cols = 300, 1000
+    d = inputs.config_inputs("c3", {"rows": rows, "cols": cols})
+    xs = d["x"].astype(np.float16).astype(np.float64)
+    bs = d["b"].astype(np.float16).astype(np.float64)
+    km = fx.synth_elementwise(fx.config3_tier1_module(rows, cols, "f16"))
+    art = hip.build(km)
+    assert art.class_name == "elementwise-nd"
+    got = art.run({0: xs, 1: bs})[2]
+    want = oracle.run(fx.synth_elementwise(fx.config3_tier1_module(rows, cols, "f64")), {0: xs, 1: bs},
+                      hw_threads=4)[2].astype(np.float16).astype(np.float64)
+    assert np.array_equal(got, want), int((got != want).sum())
 
 
 def test_c3_tier1_form_refused(hip):

@@ -42,6 +42,8 @@ def test_valid_arch():
 @pytest.mark.parametrize("name,km,cls,policy", [
     ("c1", fx.config1_module(1 << 12), "elementwise-1d", "tol-4ulp-f32-gfx950-v1"),
     ("c1f64", fx.config1_module(1 << 12, dtype="f64"), "elementwise-1d", "bitexact-rne-gfx950-v1"),
+    # f16 output: the exact f64 sine, rounded once.
+    ("c1f16", fx.config1_module(1 << 12, dtype="f16"), "elementwise-1d", "bitexact-rne-gfx950-v1"),
     ("c2-call", fx.config2_module(64, 128, 1), "softmax-call", "tol-rel1e-6-gfx950-v1"),
     ("c2-nest", fx.config2_module(64, 128, 2), "softmax-nest", "tol-rel1e-6-gfx950-v1"),
     ("c2-full-nest", fx.config2_module(8192, 4096, 2), "softmax-nest", "tol-rel1e-6-gfx950-v1"),
