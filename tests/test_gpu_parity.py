@@ -131,7 +131,11 @@ def test_scalar_param_and_two_inputs_1d(hip):
                                         ((7, 9000), 1), ((64, 256), 2),
                                         # odd row counts on the guard-free pair kernel
                                         # (the last row pairs with itself)
-                                        ((3, 4096), 1), ((1, 256), 1), ((4097, 1024), 2)])
+                                        ((3, 4096), 1), ((1, 256), 1), ((4097, 1024), 2),
+                                        # more rows than the capped grid has waves (each
+                                        # wave walks several pairs); a row length that is
+                                        # not a multiple of 4 (block-per-row kernel)
+                                        ((70001, 8), 1), ((33, 101), 2)])
 def test_c2_softmax(hip, shape, tier):
     m, k = shape
     say(f"c2 softmax {m}x{k} tier{tier}")

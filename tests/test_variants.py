@@ -107,6 +107,7 @@ CASES = {
     "gemm-f16-call-accumulate": _gemm_call_acc_case,
     "softmax-512x4096": _softmax_case,
     "softmax-333x1000": lambda: _softmax_case(333, 1000),
+    "softmax-70001x8": lambda: _softmax_case(70001, 8),
     "gemm-f16-512x1024x512": _gemm_case,
     "score-2x512x128": _score_case,
     "score-1x2048x128": lambda: _score_case(1, 2048, 128),
@@ -131,7 +132,7 @@ def test_every_declared_form_meets_tolerance(hip, name):
         assert e <= tol, (name, v)
 
 
-@pytest.mark.parametrize("m,k", [(512, 4096), (333, 1000)])
+@pytest.mark.parametrize("m,k", [(512, 4096), (333, 1000), (70001, 8)])
 def test_softmax_forms_with_one_arithmetic_agree_bitwise(hip, m, k):
     # Forms 5, 0 and 3 share the v_exp_f32 / grouped-sum row body and differ
     # only in launch shape and store kind; forms 2, 4 and 1 share the expf /
