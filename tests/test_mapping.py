@@ -125,9 +125,11 @@ def test_c2_full_shape_row_mapping_every_form(hip):
 
 def _perm_gemm(m, k, n, dtype):
     # A = a row permutation (A[i, p(i)] = 1), B encodes (k, n): C = B[p, :]
-    # exactly (one nonzero product per sum).
+    # exactly (one nonzero product per sum). With m > k the indices wrap
+    # modulo k: rows that share a source row are interchangeable, but a
+    # misplaced tile of 64 or 256 rows still shows.
     rng = np.random.default_rng(5)
-    p = rng.permutation(k)[:m]
+    p = (rng.permutation(max(m, k)) % k)[:m]
     A = np.zeros((m, k), dtype=np.float32)
     A[np.arange(m), p] = 1.0
     kk, nn = np.meshgrid(np.arange(k), np.arange(n), indexing="ij")
@@ -145,7 +147,13 @@ def test_gemm_expected_values_match_oracle():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("m,k,n,dtype", [(1024, 1024, 1024, "f32"), (4096, 4096, 4096, "f16")])
+@pytest.mark.parametrize("m,k,n,dtype", [(1024, 1024, 1024, "f32"), (4096, 4096, 4096, "f16"),
+                                         # non-square grids: f32 tiles of 64, f16 tiles of 256
+                                         # row-major (3 x 5) and in XCD groups of 4 x 8
+                                         # (8 x 32 and 32 x 8 tiles)
+                                         (192, 256, 320, "f32"), (2048, 128, 512, "f32"),
+                                         (768, 1024, 1280, "f16"), (2048, 2048, 8192, "f16"),
+                                         (8192, 256, 2048, "f16")])
 def test_gemm_full_shape_mapping_every_form(hip, m, k, n, dtype):
     A, B, want = _perm_gemm(m, k, n, dtype)
     art = hip.build(fx.config4_module(m, k, n, dtype, 2))
