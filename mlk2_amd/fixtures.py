@@ -297,21 +297,22 @@ def config4_module(m: int, k: int, n: int, dtype_in: str, tier: int = 2) -> Kern
 
 # ------------------------------------------------------ score + softmax --
 def score_softmax_module(batch: int, seq: int, dim: int, dtype_in: str = "f16",
-                         scale_div: Optional[float] = None) -> KernelModule:
+                         scale_div: Optional[float] = None, dtype_out: str = "f32") -> KernelModule:
     """Config 5 as a Kernel IR composition of reference pieces (no single
     reference class covers it): a batched QK^T init+accumulate nest written
     like buildGemmNodes (:58-147) with the K operand read transposed through
     its ElemIdx coefficients, then the broadcast elementwise chain
     Add(Div(S, sqrt(dim)), bias[j]) as buildElementwiseNodes emits it
     (:231-353), then the stable softmax nest of buildSoftmaxNodes (:363-523)
-    over the [batch*seq, seq] score rows. The score matrix is a temp."""
+    over the [batch*seq, seq] score rows into S (`dtype_out`). The score
+    matrix is a temp."""
     c = float(math.sqrt(dim)) if scale_div is None else scale_div
     R = batch * seq
     km = KernelModule()
     q = km.add_buffer(KernelBuffer("Q", dtype_in, True, False, False, batch * seq * dim, [batch, seq, dim]))
     kb = km.add_buffer(KernelBuffer("K", dtype_in, True, False, False, batch * seq * dim, [batch, seq, dim]))
     bias = km.add_buffer(KernelBuffer("bias", "f32", True, False, False, seq, [seq]))
-    y = km.add_buffer(KernelBuffer("S", "f32", False, True, False, R * seq, [R, seq]))
+    y = km.add_buffer(KernelBuffer("S", dtype_out, False, True, False, R * seq, [R, seq]))
     sc = km.add_buffer(KernelBuffer("scores", "f32", is_temp=True, elements=R * seq, dims=[R, seq]))
     # Root 1: b{ i{ j{ SC=0; k{ SC += Q[b,i,k] * K[b,j,k] } } } }
     n = []

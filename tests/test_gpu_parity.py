@@ -385,6 +385,32 @@ def test_c5_score_softmax_f64_operands(hip, b, s, dm):
     assert e <= 1e-5
 
 
+@pytest.mark.parametrize("dtype_in", ["f16", "f64"])
+def test_c5_score_softmax_f16_output(hip, dtype_in):
+    # S held as f16 takes the general score kernel, which stores each score
+    # to S with one rounding, then the row softmax in place over S (f64
+    # arithmetic, one rounding per output). Rounding the scores to f16
+    # first moves the outputs by about 2^-11 of a score times the output;
+    # the score+softmax bound of 1e-2 holds.
+    b, s, dm = 2, 96, 32
+    say(f"c5 score softmax f16 S, {dtype_in} operands")
+    km = fx.score_softmax_module(b, s, dm, dtype_in, dtype_out="f16")
+    Q = inputs.normal(31, b * s * dm)
+    K = inputs.normal(32, b * s * dm)
+    if dtype_in == "f16":
+        Q = Q.astype(np.float16).astype(np.float64)
+        K = K.astype(np.float16).astype(np.float64)
+    bias = inputs.uniform(33, s, -1, 1).astype(np.float32).astype(np.float64)
+    art = hip.build(km)
+    assert art.class_name == "score-softmax"
+    got = art.run({0: Q, 1: K, 2: bias})[3]
+    ref = oracle.run(km, {0: Q, 1: K, 2: bias}, hw_threads=8)[3]
+    e = max_rel(got, ref)
+    say(f"c5 f16 S max_rel={e:.3e}")
+    assert e <= 1e-2
+    assert np.abs(got.reshape(b * s, s).sum(axis=1) - 1.0).max() < 0.05
+
+
 def _score_ref(Q, K, bias, rows=None):
     """Config-5 reference composed from oracle pieces: k-ascending f64 GEMM
     Q_b K_b^T (Call(MatMul) with K^T materialized, as Transpose is rank-2),
