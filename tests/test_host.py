@@ -141,3 +141,20 @@ def test_declared_variant_space(km, space):
 def test_variant_space_step_out_of_range():
     with pytest.raises(be.MlkHipError):
         be.plan_variants(fx.config2_module(64, 128, 2), 3)
+
+
+@pytest.mark.parametrize("lift", [False, True])
+def test_split_precision_sine_only_for_f32_outputs(lift):
+    # The split-precision poly7 sine is chosen only where its result is
+    # rounded to f32; f16 and f64 outputs keep the exact f64 form, in the
+    # 1-D template and the n-D one alike.
+    for dtype, split in (("f32", True), ("f16", False), ("f64", False)):
+        km = fx.config1_module(1 << 12, dtype=dtype)
+        if lift:
+            km = fx.lift_1d(km)
+        _, src = be.compile_check(km)
+        # The instance's chain is the prelude, ahead of the template text
+        # (whose comments show an example chain).
+        body = [line for line in src.splitlines() if "mlk_p7_sin" in line and "const double" in line]
+        assert body, dtype
+        assert ("mlk_p7_sin_f32out(" in body[0]) == split, (dtype, body[0])
