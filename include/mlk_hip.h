@@ -77,12 +77,38 @@ int mlkhip_build(const char* module_json, size_t len, const char* arch, const ch
 int mlkhip_plan(const char* module_json, size_t len, char* class_name, size_t class_cap,
                 char* policy, size_t policy_cap, int* n_steps);
 
+/* The hipRTC options every instance is compiled with for `arch` (target,
+ * -O3, -std=c++17, -ffp-contract=off, packed FP32 instructions disabled),
+ * space-separated into `buf`; returns the option count. No device needed. */
+int mlkhip_jit_options(const char* arch, char* buf, size_t cap);
+
 /* Instantiates the hipRTC source of step `step` (elementwise and generic
  * loop-nest steps) and compiles it for `arch` without loading; returns the
  * code-object size, 0 for steps that use precompiled kernels, or -1.
  * `source` may be NULL. */
 long long mlkhip_compile_check(const char* module_json, size_t len, int step, const char* arch,
                                char* source, size_t source_cap);
+
+/* Replaces buildGpuKernelArtifactInDir (backend_driver.h:218-228) in its
+ * file-backed form: writes <dir>/mlk_kernel.cpp, a per-module artifact that
+ * exports `mlk_kernel` exactly as LoadedKernel::run binds it (dlsym at
+ * backend_driver.cpp:427, typed call at :932-1042; docs/kernel_abi.md:25-40):
+ *   multi-dim:  int mlk_kernel(<T0> p0, const int64_t* p0_dims, ...,
+ *                              const double* mlk_scalars, int64_t mlk_n_scalars)
+ *   legacy 1-D: void mlk_kernel(<T0> p0, ..., int64_t n,
+ *                               const double* mlk_scalars, int64_t mlk_n_scalars)
+ * (<Ti> = double* for stored, output and temp buffers, const double*
+ * otherwise; one entry per bindable buffer in table order; temp slots are
+ * ignored) plus `int mlk_kernel_status(void)`, the calling thread's last
+ * status (the legacy form's side channel). Each call forwards to
+ * mlkhip_kernel / mlkhip_kernel_1d of this library; the first call builds
+ * the embedded module for the embedded `arch`. The source is compiled out of
+ * process with `compiler` (NULL or "": c++) into <dir>/libmlk_kernel.so,
+ * linked against this library; its path goes to `path_out`. The module is
+ * planned first, so what mlkhip_build refuses is refused here
+ * (MLKHIP_REFUSED, see mlkhip_last_error). No device needed. */
+int mlkhip_emit_artifact(const char* module_json, size_t len, const char* arch, const char* compiler,
+                         const char* dir, char* path_out, size_t cap);
 
 void mlkhip_release(mlkhip_artifact* a);
 
@@ -156,6 +182,11 @@ int mlkhip_step_variants(const mlkhip_artifact* a, int step, int* out, int cap);
 /* The same without a device: plans the module and lists step `step`'s
  * variant space. */
 int mlkhip_plan_variants(const char* module_json, size_t len, int step, int* out, int cap);
+
+/* Kernel symbol of step `step` when the step is a hipRTC instance (an
+ * elementwise chain: mlk_elementwise_<12 hex digits of its source hash>; a
+ * generic loop nest: mlk_nest), else "". Profiles name kernels by it. */
+const char* mlkhip_step_kernel_name(const mlkhip_artifact* a, int step);
 
 /* Form step `step` launches with (-1 = the kernel's default); -2 when the
  * step does not exist. */

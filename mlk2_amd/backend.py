@@ -111,6 +111,11 @@ def lib():
     L.mlkhip_fill32.argtypes = [c.c_void_p, c.c_uint32, c.c_size_t]
     L.mlkhip_stream_create.argtypes = [c.POINTER(c.c_void_p)]
     L.mlkhip_stream_destroy.argtypes = [c.c_void_p]
+    L.mlkhip_emit_artifact.argtypes = [c.c_char_p, c.c_size_t, c.c_char_p, c.c_char_p, c.c_char_p, c.c_char_p,
+                                       c.c_size_t]
+    L.mlkhip_jit_options.argtypes = [c.c_char_p, c.c_char_p, c.c_size_t]
+    L.mlkhip_step_kernel_name.argtypes = [c.c_void_p, c.c_int]
+    L.mlkhip_step_kernel_name.restype = c.c_char_p
     _lib = L
     return L
 
@@ -385,6 +390,10 @@ class LoadedKernel:
             raise MlkHipError(BAD_BINDING, last_error())
         return list(out[:n])
 
+    def step_kernel_name(self, step: int) -> str:
+        """hipRTC kernel symbol of step `step` ("" for precompiled kernels)."""
+        return lib().mlkhip_step_kernel_name(self._h, step).decode()
+
     def step_variant(self, step: int) -> int:
         return int(lib().mlkhip_step_variant(self._h, step))
 
@@ -423,10 +432,13 @@ def _numel(b, elements: int) -> int:
 
 
 def build_hip_kernel_artifact(km: KernelModule,
-                              config: Optional[HipBackendDriverConfig] = None) -> LoadedKernel:
-    """buildGpuKernelArtifact analogue (backend_driver.h:218-228)."""
+                              config: Optional[HipBackendDriverConfig] = None,
+                              reference_document: bool = False) -> LoadedKernel:
+    """buildGpuKernelArtifact analogue (backend_driver.h:218-228). With
+    ``reference_document`` the module crosses the boundary exactly as the
+    reference's writer serializes it (KernelModule.to_reference_json)."""
     cfg = config or HipBackendDriverConfig()
-    data = km.to_json().encode()
+    data = (km.to_reference_json() if reference_document else km.to_json()).encode()
     h = ctypes.c_void_p()
     rc = lib().mlkhip_build(data, len(data), cfg.arch.encode(),
                             (cfg.cache_dir or "").encode(), ctypes.byref(h))
@@ -444,5 +456,6 @@ class HipBackend:
     def device_available(self) -> bool:
         return bool(lib().mlkhip_device_available(self.arch.encode()))
 
-    def build(self, km: KernelModule, cache_dir: Optional[str] = None) -> LoadedKernel:
-        return build_hip_kernel_artifact(km, HipBackendDriverConfig(self.arch, cache_dir))
+    def build(self, km: KernelModule, cache_dir: Optional[str] = None,
+              reference_document: bool = False) -> LoadedKernel:
+        return build_hip_kernel_artifact(km, HipBackendDriverConfig(self.arch, cache_dir), reference_document)

@@ -30,7 +30,8 @@ HIPCC = os.path.join(ROCM, "bin", "hipcc")
 CLANG = os.path.join(ROCM, "llvm", "bin", "clang++")
 
 DEVICE_SOURCES = ["runtime.hip", "jit.hip", "softmax.hip", "gemm.hip", "score_softmax.hip", "probe.hip"]
-HOST_SOURCES = ["kernel_ir.cpp", "planner.cpp", "codegen.cpp", "nestgen.cpp", "canonical.cpp", "driver.cpp", "tune.cpp"]
+HOST_SOURCES = ["kernel_ir.cpp", "planner.cpp", "codegen.cpp", "nestgen.cpp", "canonical.cpp", "driver.cpp", "tune.cpp",
+                "artifact.cpp"]
 
 HIP_FLAGS = [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
              "-Wall", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]

@@ -26,6 +26,12 @@
 #include "mlk_device_math.h"
 #endif
 
+// Each instance's kernel symbol is mlk_elementwise_<hash of its source>, so
+// profiles tell instances apart; the standalone build keeps the plain name.
+#ifndef MLK_KERNEL_NAME
+#define MLK_KERNEL_NAME mlk_elementwise
+#endif
+
 #ifndef MLK_GENERATED
 #define MLK_NIN 1
 constexpr int kRank = 1;
@@ -174,7 +180,7 @@ __device__ __forceinline__ void loadAll(const void* const (&ptr)[4], const long 
 
 }  // namespace mlk
 
-extern "C" __global__ __launch_bounds__(256) void mlk_elementwise(const void* p0, const void* p1,
+extern "C" __global__ __launch_bounds__(256) void MLK_KERNEL_NAME(const void* p0, const void* p1,
                                                                   const void* p2, const void* p3,
                                                                   void* out, const mlk_scalars sc,
                                                                   long long dynExtent) {

@@ -1038,7 +1038,9 @@ __device__ __forceinline__ void stAny(void* p, int dt, int64_t i, T v) {
 }
 
 /// 64x64 output tile per 256 threads, 4x4 per thread, K slabs of 16 through
-/// LDS; k ascending per output element.
+/// LDS; k ascending per output element, starting from C's old value in the
+/// accumulate form (the reference's order, kernel_buffers.cpp:406-432). With
+/// skip_zero_a the products of A[i,p] == 0 are left out, as there (:422).
 template <typename T>
 __global__ __launch_bounds__(256) void gemmGeneral(mlkd_gemm p) {
     __shared__ T As[16][64 + 1];
@@ -1051,8 +1053,12 @@ __global__ __launch_bounds__(256) void gemmGeneral(mlkd_gemm p) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = T(0);
+        for (int j = 0; j < 4; ++j) {
+            const int64_t r = row0 + ty * 4 + i, c = col0 + tx * 4 + j;
+            acc[i][j] = (p.accumulate && r < p.m && c < p.n) ? ldAny<T>(p.c, p.c_dtype, r * p.ldc + c) : T(0);
+        }
     }
+    const bool skip = p.skip_zero_a != 0;
     for (int64_t k0 = 0; k0 < p.k; k0 += 16) {
         for (int e = threadIdx.x; e < 16 * 64; e += 256) {
             const int kk = e / 64, mm = e % 64;
@@ -1071,6 +1077,7 @@ __global__ __launch_bounds__(256) void gemmGeneral(mlkd_gemm p) {
             for (int j = 0; j < 4; ++j) b[j] = Bs[kk][tx * 4 + j];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
+                if (skip && a[i] == T(0)) continue;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) acc[i][j] += a[i] * b[j];
             }
@@ -1082,11 +1089,7 @@ __global__ __launch_bounds__(256) void gemmGeneral(mlkd_gemm p) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int64_t r = row0 + ty * 4 + i, c = col0 + tx * 4 + j;
-            if (r < p.m && c < p.n) {
-                const int64_t at = r * p.ldc + c;
-                const T old = p.accumulate ? ldAny<T>(p.c, p.c_dtype, at) : T(0);
-                stAny<T>(p.c, p.c_dtype, at, old + acc[i][j]);
-            }
+            if (r < p.m && c < p.n) stAny<T>(p.c, p.c_dtype, r * p.ldc + c, acc[i][j]);
         }
     }
 }
@@ -1111,7 +1114,8 @@ extern "C" int mlkd_launch_gemm(const mlkd_gemm* p, void* stream) {
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int variant = p->variant >= 0 ? p->variant : gGemmF16Variant;
     const bool fits32 = p->m < (1LL << 31) && p->n < (1LL << 31) && p->k < (1LL << 31);
-    if (p->k > 0 && fits32 && p->a_dtype == MLKD_F16 && p->b_dtype == MLKD_F16 &&
+    const bool mfma = p->skip_zero_a == 0;  // the skip runs on the general kernel only
+    if (mfma && p->k > 0 && fits32 && p->a_dtype == MLKD_F16 && p->b_dtype == MLKD_F16 &&
         p->c_dtype == MLKD_F32 && p->m % kBM == 0 && p->n % kBN == 0 && p->k % kBK == 0 &&
         p->lda % 8 == 0 && p->ldb % 8 == 0 && aligned16(p->a) && aligned16(p->b)) {
         const int tiles = static_cast<int>((p->m / kBM) * (p->n / kBN));
@@ -1218,7 +1222,7 @@ extern "C" int mlkd_launch_gemm(const mlkd_gemm* p, void* stream) {
                            static_cast<int>(p->k), p->lda, p->ldb, p->ldc, p->accumulate);
         return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
     }
-    if (p->k > 0 && fits32 && p->a_dtype == MLKD_F32 && p->b_dtype == MLKD_F32 &&
+    if (mfma && p->k > 0 && fits32 && p->a_dtype == MLKD_F32 && p->b_dtype == MLKD_F32 &&
         p->c_dtype == MLKD_F32 && p->m % kFM == 0 && p->n % kFN == 0 && p->k % kFK == 0 &&
         p->lda % 4 == 0 && p->ldb % 4 == 0 && aligned16(p->a) && aligned16(p->b)) {
         const int tiles = static_cast<int>((p->m / kFM) * (p->n / kFN));

@@ -81,9 +81,41 @@ void writeFileAtomic(const std::string& path, const std::vector<char>& data) {
     }
 }
 
+/// hipRTC options of every instance: the declared target, -O3, C++17, no
+/// floating-point contraction (f64 chains round like the reference's x86-64
+/// build) and no packed FP32 instructions, as for the precompiled kernels.
+struct JitOptions {
+    std::string arch;
+    const char* v[8];
+    int n{0};
+    explicit JitOptions(const char* target) : arch(std::string("--offload-arch=") + target) {
+        v[n++] = arch.c_str();
+        v[n++] = "-O3";
+        v[n++] = "-std=c++17";
+        v[n++] = "-ffp-contract=off";
+        v[n++] = "-Xclang";
+        v[n++] = "-target-feature";
+        v[n++] = "-Xclang";
+        v[n++] = "-packed-fp32-ops";
+    }
+};
+
 }  // namespace
 
 extern "C" {
+
+/// The hipRTC option list (for inspection by tests): writes the options
+/// separated by single spaces into `buf`; returns their count.
+int mlkd_jit_options(const char* arch, char* buf, size_t cap) {
+    const JitOptions o(arch != nullptr ? arch : "gfx950");
+    std::string s;
+    for (int i = 0; i < o.n; ++i) {
+        if (i) s += ' ';
+        s += o.v[i];
+    }
+    setLog(buf, cap, s);
+    return o.n;
+}
 
 /// hipRTC's version (part of the variant-cache fingerprint).
 int mlkd_jit_version(int* major, int* minor) {
@@ -98,9 +130,9 @@ int mlkd_jit_build(const char* src, size_t len, const char* name, const char* ar
     *fn_out = nullptr;
     int major = 0, minor = 0;
     hiprtcVersion(&major, &minor);
-    const std::string archOpt = std::string("--offload-arch=") + arch;
-    const char* opts[] = {archOpt.c_str(), "-O3", "-std=c++17", "-ffp-contract=off"};
-    const int nopts = 4;
+    JitOptions jo(arch);
+    const char** opts = jo.v;
+    const int nopts = jo.n;
     uint64_t h = 0xCBF29CE484222325ull;
     h = fnv1a(h, src, len);
     h = fnv1a(h, name, strlen(name));
@@ -166,8 +198,7 @@ int mlkd_jit_build(const char* src, size_t len, const char* name, const char* ar
 /// hosts without a device). Returns the code-object size in bytes or -1.
 long long mlkd_jit_compile_only(const char* src, size_t len, const char* arch, char* log,
                                 size_t cap) {
-    const std::string archOpt = std::string("--offload-arch=") + arch;
-    const char* opts[] = {archOpt.c_str(), "-O3", "-std=c++17", "-ffp-contract=off"};
+    JitOptions jo(arch);
     hiprtcProgram prog;
     std::string text(src, len);
     if (hiprtcCreateProgram(&prog, text.c_str(), "mlk_instance.hip", 0, nullptr, nullptr) !=
@@ -175,7 +206,7 @@ long long mlkd_jit_compile_only(const char* src, size_t len, const char* arch, c
         setLog(log, cap, "hiprtcCreateProgram failed");
         return -1;
     }
-    const hiprtcResult rc = hiprtcCompileProgram(prog, 4, opts);
+    const hiprtcResult rc = hiprtcCompileProgram(prog, jo.n, jo.v);
     size_t logSize = 0;
     hiprtcGetProgramLogSize(prog, &logSize);
     std::string clog(logSize + 1, '\0');

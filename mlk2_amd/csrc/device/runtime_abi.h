@@ -31,6 +31,9 @@ int mlkd_rt_h2d(void* dst, const void* src, size_t bytes, void* stream);
 int mlkd_rt_d2h(void* dst, const void* src, size_t bytes, void* stream);
 int mlkd_rt_d2d(void* dst, const void* src, size_t bytes, void* stream);
 int mlkd_rt_fill32(void* p, uint32_t value, size_t bytes, void* stream);
+/// Sets *flag (which the caller zeroes) to 1 when any of the n elements of
+/// `p` (dtype MLKD_F32 / F16 / F64) is an infinity or a NaN.
+int mlkd_rt_scan_nonfinite(const void* p, int dtype, int64_t n, uint32_t* flag, void* stream);
 int mlkd_rt_sync(void* stream);
 int mlkd_rt_device_sync(void);
 int mlkd_rt_stream_create(void** s);
@@ -43,6 +46,9 @@ const char* mlkd_rt_last_error(void);
 
 /// hipRTC instances of kernel templates (jit.hip).
 int mlkd_jit_version(int* major, int* minor);
+/// The hipRTC option list every instance is compiled with, space-separated
+/// into `buf`; returns the option count.
+int mlkd_jit_options(const char* arch, char* buf, size_t cap);
 int mlkd_jit_build(const char* src, size_t len, const char* name, const char* arch,
                    const char* cache_dir, void** fn_out, uint64_t* fingerprint_out, char* log,
                    size_t cap);

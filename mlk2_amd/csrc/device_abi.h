@@ -43,7 +43,10 @@ typedef struct mlkd_gemm {
     int64_t m, n, k;
     int64_t lda, ldb, ldc;
     int32_t variant;      /* launch form; -1: the process default */
-    int32_t pad;
+    /* 1: skip the products of A[i,p] == 0, the reference's gemmRowBlock
+       (kernel_buffers.cpp:422), with C[i,j] = C_in + sum over p ascending;
+       runs the exact general kernel. */
+    int32_t skip_zero_a;
 } mlkd_gemm;
 
 /// S[b*seq + i, j] = softmax_j((Q[b,i,:] . K[b,j,:]) / div + bias[j]).

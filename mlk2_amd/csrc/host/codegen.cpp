@@ -25,7 +25,20 @@ std::string list(const int64_t* v, int n) {
 }
 }  // namespace
 
-std::string elementwiseSource(const KernelModule& km, const Step& st) {
+/// mlk_elementwise_ followed by 12 hex digits of the FNV-1a hash of the
+/// instance source.
+std::string elementwiseKernelName(const std::string& source) {
+    uint64_t h = 0xCBF29CE484222325ull;  // FNV-1a
+    for (const char c : source) {
+        h ^= static_cast<unsigned char>(c);
+        h *= 0x100000001B3ull;
+    }
+    char buf[48];
+    std::snprintf(buf, sizeof(buf), "mlk_elementwise_%012llx", static_cast<unsigned long long>(h >> 16));
+    return buf;
+}
+
+std::string elementwiseSource(const KernelModule& km, const Step& st, std::string* kernelName) {
     const int nin = st.inputs.empty() ? 1 : static_cast<int>(st.inputs.size());
     std::string p;
     p += "#define MLK_GENERATED 1\n";
@@ -70,7 +83,10 @@ std::string elementwiseSource(const KernelModule& km, const Step& st) {
         start = nl + 1;
     }
     p += joined + "\n";
-    return p + kDeviceMathHeader + kElementwiseTemplate;
+    const std::string text = p + kDeviceMathHeader + kElementwiseTemplate;
+    const std::string name = elementwiseKernelName(text);
+    if (kernelName != nullptr) *kernelName = name;
+    return "#define MLK_KERNEL_NAME " + name + "\n" + text;
 }
 
 const char* deviceMathHeader() { return kDeviceMathHeader; }

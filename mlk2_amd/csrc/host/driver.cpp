@@ -99,11 +99,15 @@ Result<std::unique_ptr<HipLoadedKernel>> buildHipKernelArtifact(const KernelModu
     for (Step& st : k->plan_.steps) {
         if (st.kind != StepKind::Elementwise && st.kind != StepKind::Nest) continue;
         const bool nest = st.kind == StepKind::Nest;
-        if (!nest) st.source = elementwiseSource(k->km_, st);
+        if (nest) {
+            st.kernelName = "mlk_nest";
+        } else {
+            st.source = elementwiseSource(k->km_, st, &st.kernelName);
+        }
         char log[4096] = {0};
         void* fn = nullptr;
         uint64_t fp = 0;
-        const int rc = mlkd_jit_build(st.source.data(), st.source.size(), nest ? "mlk_nest" : "mlk_elementwise",
+        const int rc = mlkd_jit_build(st.source.data(), st.source.size(), st.kernelName.c_str(),
                                       config.arch.c_str(), config.cacheDir.c_str(), &fn, &fp, log,
                                       sizeof(log));
         if (rc != 0) {
@@ -114,22 +118,34 @@ Result<std::unique_ptr<HipLoadedKernel>> buildHipKernelArtifact(const KernelModu
     }
     k->fingerprint_ = artifactFingerprint(k->km_, k->plan_, config.arch);
     k->fromCache_ = applyCachedVariants(config.cacheDir, k->fingerprint_, k->km_, k->plan_);
-    k->scratch_.assign(km.buffers.size(), nullptr);
-    k->scratchElems_.assign(km.buffers.size(), 0);
-    k->stepScratch_.assign(k->plan_.steps.size(), nullptr);
-    k->stepScratchBytes_.assign(k->plan_.steps.size(), 0);
     k->noSlabFn_.assign(k->plan_.steps.size(), nullptr);
     return k;
 }
 
 HipLoadedKernel::~HipLoadedKernel() {
-    for (void* p : scratch_) {
-        if (p != nullptr) mlkd_rt_free(p);
+    for (auto& [stream, rs] : scratchByStream_) {
+        (void)stream;
+        for (void* p : rs->temp) {
+            if (p != nullptr) mlkd_rt_free(p);
+        }
+        if (rs->status != nullptr) mlkd_rt_free(rs->status);
+        for (void* p : rs->step) {
+            if (p != nullptr) mlkd_rt_free(p);
+        }
     }
-    if (status_ != nullptr) mlkd_rt_free(status_);
-    for (void* p : stepScratch_) {
-        if (p != nullptr) mlkd_rt_free(p);
+}
+
+HipLoadedKernel::RunScratch& HipLoadedKernel::scratchFor(void* stream) const {
+    for (auto& [s, rs] : scratchByStream_) {
+        if (s == stream) return *rs;
     }
+    std::unique_ptr<RunScratch> rs(new RunScratch());
+    rs->temp.assign(km_.buffers.size(), nullptr);
+    rs->tempElems.assign(km_.buffers.size(), 0);
+    rs->step.assign(plan_.steps.size(), nullptr);
+    rs->stepBytes.assign(plan_.steps.size(), 0);
+    scratchByStream_.emplace_back(stream, std::move(rs));
+    return *scratchByStream_.back().second;
 }
 
 int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* scalars,
@@ -139,6 +155,16 @@ int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* 
         why = "expected " + std::to_string(bindables_.size()) + " bindings, got " + std::to_string(n);
         return MLKHIP_BAD_BINDING;
     }
+    RunScratch* rs = nullptr;
+    {
+        std::lock_guard<std::mutex> g(scratchLock_);
+        rs = &scratchFor(stream);
+    }
+    auto statusWord = [&]() -> void* {
+        std::lock_guard<std::mutex> g(scratchLock_);
+        if (rs->status == nullptr && mlkd_rt_malloc(&rs->status, 256) != 0) rs->status = nullptr;
+        return rs->status;
+    };
     std::vector<void*> ptr(km_.buffers.size(), nullptr);
     for (int i = 0; i < n; ++i) {
         const uint32_t b = bindables_[static_cast<size_t>(i)];
@@ -147,16 +173,17 @@ int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* 
         if (kb.isTemp && binds[i].ptr == nullptr) {
             if (!plan_.tempNeeded[b]) continue;
             std::lock_guard<std::mutex> g(scratchLock_);
-            if (scratch_[b] == nullptr || scratchElems_[b] < need) {
-                if (scratch_[b] != nullptr) mlkd_rt_free(scratch_[b]);
-                scratch_[b] = nullptr;
-                if (mlkd_rt_malloc(&scratch_[b], static_cast<size_t>(need) * dtypeBytes(kb.dtype) + 16) != 0) {
+            if (rs->temp[b] == nullptr || rs->tempElems[b] < need) {
+                if (rs->temp[b] != nullptr) mlkd_rt_free(rs->temp[b]);
+                rs->temp[b] = nullptr;
+                if (mlkd_rt_malloc(&rs->temp[b], static_cast<size_t>(need) * dtypeBytes(kb.dtype) + 16) != 0) {
+                    rs->temp[b] = nullptr;
                     why = "temp scratch allocation failed";
                     return MLKHIP_RUNTIME;
                 }
-                scratchElems_[b] = need;
+                rs->tempElems[b] = need;
             }
-            ptr[b] = scratch_[b];
+            ptr[b] = rs->temp[b];
         } else {
             if (binds[i].dtype != dtypeCode(kb.dtype)) {
                 why = "binding " + std::to_string(i) + " (" + kb.name + ") has the wrong dtype";
@@ -247,7 +274,7 @@ int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* 
             case StepKind::Gemm: {
                 mlkd_gemm p;
                 p.variant = st.variant;
-                p.pad = 0;
+                p.skip_zero_a = 0;
                 p.a = ptr[st.a];
                 p.b = ptr[st.b];
                 p.c = ptr[st.c];
@@ -261,6 +288,24 @@ int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* 
                 p.lda = st.lda;
                 p.ldb = st.ldb;
                 p.ldc = st.ldc;
+                if (st.skipZeroA && st.k > 0) {
+                    // 0 * inf and 0 * NaN are the only products whose skip
+                    // changes C beyond the sign of a zero sum, so the MFMA
+                    // forms run unless B holds a non-finite value.
+                    void* flag = statusWord();
+                    uint32_t any = 0;
+                    if (flag == nullptr) {
+                        why = "status word allocation failed";
+                        return MLKHIP_RUNTIME;
+                    }
+                    if (mlkd_rt_fill32(flag, 0u, 4, stream) != 0 ||
+                        mlkd_rt_scan_nonfinite(p.b, p.b_dtype, st.k * st.n, static_cast<uint32_t*>(flag), stream) != 0 ||
+                        mlkd_rt_d2h(&any, flag, sizeof(any), stream) != 0 || mlkd_rt_sync(stream) != 0) {
+                        why = "non-finite scan of B failed";
+                        return MLKHIP_LAUNCH;
+                    }
+                    p.skip_zero_a = any != 0 ? 1 : 0;
+                }
                 rc = mlkd_launch_gemm(&p, stream);
                 break;
             }
@@ -276,18 +321,18 @@ int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* 
                                    : binds[bi].elements;
                 }
                 na.elements = elements;
+                void* status = nullptr;
                 if (st.checked) {
-                    std::lock_guard<std::mutex> g(scratchLock_);
-                    if (status_ == nullptr && mlkd_rt_malloc(&status_, 256) != 0) {
-                        status_ = nullptr;
+                    status = statusWord();
+                    if (status == nullptr) {
                         why = "status word allocation failed";
                         return MLKHIP_RUNTIME;
                     }
-                    if (mlkd_rt_fill32(status_, 0u, 4, stream) != 0) {
+                    if (mlkd_rt_fill32(status, 0u, 4, stream) != 0) {
                         why = "status word clear failed";
                         return MLKHIP_LAUNCH;
                     }
-                    na.status = static_cast<int*>(status_);
+                    na.status = static_cast<int*>(status);
                 }
                 void* fn = st.fn;
                 if (st.variant == 1 && !st.sourceNoSlabs.empty()) {
@@ -306,15 +351,15 @@ int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* 
                 }
                 rc = mlkd_jit_launch_nest(fn, gridFor(st.threads), &na, &sc, st.threads, stream);
                 if (rc == 0 && st.checked) {
-                    int status = 0;
-                    if (mlkd_rt_d2h(&status, status_, sizeof(status), stream) != 0 || mlkd_rt_sync(stream) != 0) {
+                    int code = 0;
+                    if (mlkd_rt_d2h(&code, status, sizeof(code), stream) != 0 || mlkd_rt_sync(stream) != 0) {
                         why = "status word read-back failed";
                         return MLKHIP_LAUNCH;
                     }
-                    if (status != 0) {
-                        why = status == MLKHIP_NEG_STORE ? "walker: negative store address"
-                                                         : "loop nest reaches outside a bound buffer";
-                        return status;
+                    if (code != 0) {
+                        why = code == MLKHIP_NEG_STORE ? "walker: negative store address"
+                                                       : "loop nest reaches outside a bound buffer";
+                        return code;
                     }
                 }
                 break;
@@ -341,18 +386,18 @@ int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* 
                 p.scratch_bytes = 0;
                 if (const int64_t need = mlkd_score_scratch_bytes(&p); need > 0) {
                     std::lock_guard<std::mutex> g(scratchLock_);
-                    if (stepScratch_[si] == nullptr || stepScratchBytes_[si] < need) {
-                        if (stepScratch_[si] != nullptr) mlkd_rt_free(stepScratch_[si]);
-                        stepScratch_[si] = nullptr;
-                        if (mlkd_rt_malloc(&stepScratch_[si], static_cast<size_t>(need)) != 0) {
-                            stepScratch_[si] = nullptr;
+                    if (rs->step[si] == nullptr || rs->stepBytes[si] < need) {
+                        if (rs->step[si] != nullptr) mlkd_rt_free(rs->step[si]);
+                        rs->step[si] = nullptr;
+                        if (mlkd_rt_malloc(&rs->step[si], static_cast<size_t>(need)) != 0) {
+                            rs->step[si] = nullptr;
                             why = "score-softmax scratch allocation failed";
                             return MLKHIP_RUNTIME;
                         }
-                        stepScratchBytes_[si] = need;
+                        rs->stepBytes[si] = need;
                     }
-                    p.scratch = stepScratch_[si];
-                    p.scratch_bytes = stepScratchBytes_[si];
+                    p.scratch = rs->step[si];
+                    p.scratch_bytes = rs->stepBytes[si];
                 }
                 rc = mlkd_launch_score_softmax(&p, stream);
                 break;
@@ -499,6 +544,8 @@ void copyOut(char* dst, size_t cap, const std::string& s) {
 }
 }  // namespace
 
+int mlk::hip::setLastError(int code, const std::string& message) { return setError(code, message); }
+
 extern "C" {
 
 const char* mlkhip_last_error(void) { return gLastError.c_str(); }
@@ -561,6 +608,8 @@ long long mlkhip_compile_check(const char* module_json, size_t len, int step, co
     if (n < 0) return setError(-1, log);
     return n;
 }
+
+int mlkhip_jit_options(const char* arch, char* buf, size_t cap) { return mlkd_jit_options(arch, buf, cap); }
 
 void mlkhip_release(mlkhip_artifact* a) { delete a; }
 
@@ -694,6 +743,11 @@ int mlkhip_plan_variants(const char* module_json, size_t len, int step, int* out
     auto plan = mlk::hip::planModule(dm);
     if (!plan.has_value()) return setError(-1, plan.error().message);
     return listVariants(dm, *plan, step, out, cap);
+}
+
+const char* mlkhip_step_kernel_name(const mlkhip_artifact* a, int step) {
+    if (a == nullptr || step < 0 || static_cast<size_t>(step) >= a->k->plan().steps.size()) return "";
+    return a->k->plan().steps[static_cast<size_t>(step)].kernelName.c_str();
 }
 
 int mlkhip_step_variant(const mlkhip_artifact* a, int step) {

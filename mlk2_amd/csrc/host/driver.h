@@ -34,7 +34,7 @@ struct DeviceBinding {
 
 class HipLoadedKernel {
 public:
-    ~HipLoadedKernel();  // frees the artifact-owned scratch (temps, status word)
+    ~HipLoadedKernel();  // frees the artifact-owned scratch of every stream
 
     const KernelModule& module() const { return km_; }
     const Plan& plan() const { return plan_; }
@@ -80,17 +80,23 @@ private:
     bool fromCache_{false};
     std::vector<uint32_t> bindables_;   // buffer ids in table order
     std::vector<int> bindIndex_;        // buffer id -> bindable index or -1
-    // Artifact-owned temp scratch (allocated on first use, kept; zeroed on
-    // every run like the reference's fresh temp storage).
+    // Artifact-owned device scratch of the runs on one stream: temps (zeroed
+    // on every run like the reference's fresh temp storage), the status word
+    // of loop-nest steps with run-time bounds checks and of the non-finite
+    // scan, and per-step scratch a launcher asks for (score-softmax row
+    // statistics). Allocated on first use and kept until the artifact is
+    // released. Each stream gets its own set, so runs on different streams
+    // never share device memory; runs on one stream are ordered by it.
+    struct RunScratch {
+        std::vector<void*> temp;
+        std::vector<int64_t> tempElems;
+        void* status{nullptr};
+        std::vector<void*> step;
+        std::vector<int64_t> stepBytes;
+    };
+    RunScratch& scratchFor(void* stream) const;  // caller holds scratchLock_
     mutable std::mutex scratchLock_;
-    mutable std::vector<void*> scratch_;
-    mutable std::vector<int64_t> scratchElems_;
-    // Status word of loop-nest steps with run-time bounds checks.
-    mutable void* status_{nullptr};
-    // Per-step device scratch a launcher asks for (score-softmax row
-    // statistics), allocated on first use and kept.
-    mutable std::vector<void*> stepScratch_;
-    mutable std::vector<int64_t> stepScratchBytes_;
+    mutable std::vector<std::pair<void*, std::unique_ptr<RunScratch>>> scratchByStream_;
     // Loop-nest launch form 1 (no LDS slabs), compiled on first use.
     mutable std::vector<void*> noSlabFn_;
 };
@@ -139,6 +145,19 @@ std::string artifactFingerprint(const KernelModule& km, const Plan& plan, const 
 /// variant space; returns whether it applied.
 bool applyCachedVariants(const std::string& dir, const std::string& fingerprint, const KernelModule& km,
                          Plan& plan);
+
+/// C++ source of the per-module artifact libmlk_kernel.so (artifact.cpp):
+/// `mlk_kernel` in the module's ABI form, forwarding to this library.
+Result<std::string> artifactSource(const std::string& moduleJson, const KernelModule& km, const Plan& plan,
+                                   const std::string& arch);
+
+/// Writes <dir>/mlk_kernel.cpp and compiles it out of process with
+/// `compiler` (empty: c++) into <dir>/libmlk_kernel.so; returns its path.
+Result<std::string> emitArtifact(const std::string& moduleJson, const std::string& arch, const std::string& compiler,
+                                 const std::string& dir);
+
+/// Records `message` as this thread's mlkhip_last_error and returns `code`.
+int setLastError(int code, const std::string& message);
 
 /// Plans, instantiates and loads (buildGpuKernelArtifact analogue).
 Result<std::unique_ptr<HipLoadedKernel>> buildHipKernelArtifact(const KernelModule& km,

@@ -266,6 +266,13 @@ struct Decoder {
         if (k == "const") {
             o.kind = K::Const;
             o.constValue = number(r.member(v, "value"), 0.0);
+            // KernelModule::toJson spells +-inf as +-1e308 (serializeDouble,
+            // compiler/src/core/json.cpp:301-312); read that spelling back as
+            // the infinity it stands for. A module that literally holds
+            // +-1e308 is indistinguishable and is read as +-inf too.
+            if (o.constValue == 1e308 || o.constValue == -1e308) {
+                o.constValue = o.constValue > 0 ? INFINITY : -INFINITY;
+            }
         } else if (k == "elem_a") {
             o.kind = K::ElemA;
         } else if (k == "elem_b") {
@@ -318,6 +325,7 @@ Result<KernelModule> parseKernelModule(const char* text, size_t len) {
         kb.dims = d.ints(rd.member(b, "dims"));
         km.buffers.push_back(std::move(kb));
     }
+    std::vector<uint32_t> callMath;  // Call nodes written without "math"
     for (const uint32_t n : rd.at(nodes).items) {
         KernelNode kn;
         if (!opFromName(d.text(rd.member(n, "op")), kn.op)) {
@@ -325,6 +333,7 @@ Result<KernelModule> parseKernelModule(const char* text, size_t len) {
         }
         const uint32_t mth = rd.member(n, "math");
         if (mth != kInvalidId) kn.math = mathFromName(d.text(mth));
+        const bool mathAbsent = mth == kInvalidId;
         kn.family = d.text(rd.member(n, "family"));
         kn.var = d.text(rd.member(n, "var"));
         kn.begin = d.integer(rd.member(n, "begin"), 0);
@@ -366,7 +375,24 @@ Result<KernelModule> parseKernelModule(const char* text, size_t len) {
         for (const int64_t c : d.ints(rd.member(n, "children"))) {
             kn.children.push_back(static_cast<uint32_t>(c));
         }
+        if (kn.op == KernelOp::Call && mathAbsent) callMath.push_back(static_cast<uint32_t>(km.nodes.size()));
         km.nodes.push_back(std::move(kn));
+    }
+    // KernelModule::toJson writes "math" on Compute nodes only
+    // (compiler/src/support/kernel_ir.cpp:130-135), so a Call's target comes
+    // from its operands, as the reference builds them (tools/mlk-poly/
+    // poly_bench.cpp:121-158, lower.to_kernel_ir.cpp:114-144): a bound B is
+    // MatMul; otherwise a rank-1 output is ReduceSum (rank-2 in, rank-1 out)
+    // and any other output Softmax (rank-2 in and out).
+    for (const uint32_t id : callMath) {
+        KernelNode& c = km.nodes[id];
+        if (c.bufferB != kInvalidId) {
+            c.math = MathOp::MatMul;
+        } else if (c.bufferOut < km.buffers.size() && km.buffers[c.bufferOut].dims.size() == 1) {
+            c.math = MathOp::ReduceSum;
+        } else {
+            c.math = MathOp::Softmax;
+        }
     }
     const uint32_t sched = rd.member(root, "schedule");
     if (sched != kInvalidId && rd.at(sched).type == JNode::Object) {

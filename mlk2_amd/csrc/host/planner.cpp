@@ -463,6 +463,7 @@ Result<Step> callStep(const KernelModule& km, const KernelNode& top, bool walker
         st.ldb = n;
         st.ldc = n;
         st.accumulate = true;  // gemmRowBlock accumulates into C (:406-432)
+        st.skipZeroA = true;   // ... and skips A[i,p] == 0 (:422)
         return st;
     }
     if (top.math == MathOp::Softmax || top.math == MathOp::ReduceSum) {
@@ -542,6 +543,46 @@ bool isPassThrough(const KernelExpr& e, uint32_t buf, std::initializer_list<int6
            elemIs(e.a, buf, coeffs);
 }
 
+/// True when a node outside the subtrees of `own` reads or writes one of
+/// `bufs` (an ElemIdx operand, a legacy Compute operand, a Store or Call
+/// target). A fused class that keeps those buffers on chip must own every
+/// access to them: the walker would hand any other access the values the
+/// statements stored (kernel_buffers.cpp:902-920), where a fused launch never
+/// materializes them.
+bool touchedOutside(const KernelModule& km, std::initializer_list<uint32_t> own,
+                    std::initializer_list<uint32_t> bufs) {
+    std::vector<bool> inside(km.nodes.size(), false);
+    std::vector<uint32_t> work(own.begin(), own.end());
+    while (!work.empty()) {
+        const uint32_t id = work.back();
+        work.pop_back();
+        if (id >= km.nodes.size() || inside[id]) continue;
+        inside[id] = true;
+        for (const uint32_t c : km.nodes[id].children) work.push_back(c);
+    }
+    auto hit = [&](int64_t b) {
+        for (const uint32_t t : bufs) {
+            if (b == static_cast<int64_t>(t)) return true;
+        }
+        return false;
+    };
+    for (uint32_t id = 0; id < km.nodes.size(); ++id) {
+        if (inside[id]) continue;
+        const KernelNode& n = km.nodes[id];
+        if (n.op == KernelOp::Compute || n.op == KernelOp::Store || n.op == KernelOp::Call) {
+            for (const uint32_t b : {n.bufferA, n.bufferB, n.bufferOut}) {
+                if (b != kInvalidId && hit(b)) return true;
+            }
+        }
+        for (const KernelExpr& e : n.exprs) {
+            for (const KernelOperand* o : {&e.a, &e.b}) {
+                if (o->kind == K::ElemIdx && hit(o->index)) return true;
+            }
+        }
+    }
+    return false;
+}
+
 /// poly.synth softmax nest (:363-523): m{ RM=-inf; k{RM max= x}; k{E=exp(x-RM)};
 /// S=0; k{S += E}; k{Y = E/S} }.
 bool matchSoftmaxNest(const KernelModule& km, uint32_t root, Step& st) {
@@ -599,14 +640,16 @@ bool matchSoftmaxNest(const KernelModule& km, uint32_t root, Step& st) {
     if (s5 == nullptr || s5->op != KernelOp::Store) return false;
     const uint32_t y = s5->bufferOut;
     if (!storeIs(s5, y, {K, 1}, AccumMode::None)) return false;
-    // The three scratch buffers must be temps private to this nest, sized as
-    // the statements address them; x and y must hold M*K elements.
+    // The three scratch buffers must be temps, sized as the statements
+    // address them, that no other root touches; x and y must hold M*K
+    // elements.
     for (const uint32_t t : {rm, eb, sm}) {
         if (t >= km.buffers.size() || !km.buffers[t].isTemp) return false;
     }
     if (bufElems(km.buffers[rm]) < M || bufElems(km.buffers[sm]) < M || bufElems(km.buffers[eb]) < M * K) return false;
     if (y >= km.buffers.size() || bufElems(km.buffers[x]) < M * K || bufElems(km.buffers[y]) < M * K) return false;
     if (x == rm || x == eb || x == sm || y == rm || y == eb || y == sm) return false;
+    if (touchedOutside(km, {root}, {rm, eb, sm})) return false;
     st.kind = StepKind::Softmax;
     st.what = "softmax-nest";
     st.x = x;
@@ -759,7 +802,8 @@ bool matchScoreSoftmax(const KernelModule& km, const std::vector<uint32_t>& root
     // Root 3: softmax over SC rows.
     Step soft;
     if (!matchSoftmaxNest(km, roots[at + 2], soft) || soft.x != sc || soft.rows != B * S || soft.cols != S) return false;
-    // SC must not be read anywhere else in the module.
+    // SC lives on chip only: no other root may read or write it.
+    if (touchedOutside(km, {roots[at], roots[at + 1], roots[at + 2]}, {sc})) return false;
     if (bufElems(km.buffers[q]) < B * S * D || bufElems(km.buffers[kb]) < B * S * D ||
         bufElems(km.buffers[bias]) < S || bufElems(km.buffers[soft.y]) < B * S * S) {
         return false;

@@ -36,6 +36,7 @@ struct Step {
     AccumMode accum{AccumMode::None};
     std::string chainBody;
     std::string source;
+    std::string kernelName;           // hipRTC symbol (elementwise and nest steps)
     void* fn{nullptr};
 
     // Softmax / RowSum: rows x cols from buffer x into y.
@@ -47,6 +48,11 @@ struct Step {
     int64_t m{0}, n{0}, k{0};
     int64_t lda{0}, ldb{0}, ldc{0};
     bool accumulate{false};
+    // Call(MatMul) skips A[i,p] == 0 (gemmRowBlock, kernel_buffers.cpp:422):
+    // before the launch B is scanned for non-finite values, and when it holds
+    // any the exact general kernel with the skip runs instead of the MFMA
+    // forms (0 * inf would make NaN where the reference adds nothing).
+    bool skipZeroA{false};
 
     // ScoreSoftmax: S = softmax(Q K^T / div + bias) per batch.
     uint32_t q{kInvalidId}, kk{kInvalidId}, bias{kInvalidId}, s{kInvalidId};
@@ -95,8 +101,10 @@ struct Plan {
 /// hand-written kernel covers.
 Result<Plan> planModule(const KernelModule& km);
 
-/// Full hipRTC source of an elementwise step (prelude + template).
-std::string elementwiseSource(const KernelModule& km, const Step& st);
+/// Full hipRTC source of an elementwise step (prelude + template); its
+/// kernel symbol, mlk_elementwise_<12 hex digits of the source's FNV-1a>, goes
+/// to `kernelName` when given.
+std::string elementwiseSource(const KernelModule& km, const Step& st, std::string* kernelName = nullptr);
 
 /// The device math header text every hipRTC instance starts with.
 const char* deviceMathHeader();

@@ -348,6 +348,36 @@ def score_softmax_module(batch: int, seq: int, dim: int, dtype_in: str = "f16",
     return km
 
 
+def _append_copy_root(km: KernelModule, src: int, dims: Sequence[int], name: str) -> KernelModule:
+    """Appends an output buffer of `dims` and a last root that copies temp
+    `src` into it (Add(src[...], 0) over a perfect nest): a later reader of
+    a temp that a fused class would otherwise keep on chip."""
+    out = km.add_buffer(KernelBuffer(name, "f32", False, True, False, _numel(dims), list(dims)))
+    coeffs = [_stride_of(dims, d) for d in range(len(dims))]
+    c = km.add_node(KernelNode(op="compute", exprs=[KernelExpr("add", elem_idx(src, coeffs), const(0.0))]))
+    st = km.add_node(KernelNode(op="store", out=out, out_index_coeffs=coeffs))
+    child = [c, st]
+    for d in range(len(dims) - 1, -1, -1):
+        child = [km.add_node(KernelNode(op="loop", var=f"r{d}", begin=0, end=dims[d], children=child))]
+    return km
+
+
+def softmax_rowmax_reader_module(m: int, k: int) -> KernelModule:
+    """Config 2's synthesized softmax followed by a root that copies the
+    row-max temp into an output."""
+    km = config2_module(m, k, tier=2)
+    rm = next(i for i, b in enumerate(km.buffers) if b.name == "softmax_rowmax")
+    return _append_copy_root(km, rm, [m], "rowmax_out")
+
+
+def score_reader_module(batch: int, seq: int, dim: int) -> KernelModule:
+    """Config 5's composition followed by a root that copies the scaled
+    score temp into an output."""
+    km = score_softmax_module(batch, seq, dim)
+    sc = next(i for i, b in enumerate(km.buffers) if b.name == "scores")
+    return _append_copy_root(km, sc, [batch * seq, seq], "scores_out")
+
+
 def _softmax_over(km: KernelModule, x: int, y: int, rows: int, cols: int) -> KernelModule:
     view = KernelModule(buffers=list(km.buffers))
     view.nodes = [KernelNode(op="call", math="softmax", a=x, out=y)]

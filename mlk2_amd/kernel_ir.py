@@ -6,14 +6,14 @@ as plain Python objects, and serializes them to the "mlk-kernel" JSON document
 that ``KernelModule::toJson`` writes (``compiler/src/support/kernel_ir.cpp:97-254``).
 That document is the module interchange of the HIP backend's C ABI.
 
-Two deliberate extensions of the reference writer, both needed to carry a
-module losslessly:
-
-* Call nodes carry ``"math"`` (the reference writer emits it for Compute nodes
-  only, so ``Call(MatMul)`` and ``Call(Softmax)`` would be indistinguishable).
-* Non-finite constants are written as the tokens ``Infinity`` / ``-Infinity``
-  / ``NaN`` (the reference writer clamps +/-inf to +/-1e308 and NaN to null,
-  ``compiler/src/core/json.cpp:300-312``; both readers accept those too).
+``to_json`` writes two extensions of the reference writer that carry a module
+losslessly: Call nodes carry ``"math"`` (the reference writer emits it for
+Compute nodes only), and non-finite constants are written as the tokens
+``Infinity`` / ``-Infinity`` / ``NaN`` (the reference writer clamps +/-inf to
++/-1e308 and NaN to null, ``compiler/src/core/json.cpp:300-312``).
+``to_reference_json`` writes the reference writer's own document, which the
+backend's reader takes unchanged: it infers a Call's target from its operands
+and reads +/-1e308 back as +/-inf.
 """
 from __future__ import annotations
 
@@ -217,6 +217,21 @@ class KernelModule:
         # non-finite constants (see module docstring).
         return json.dumps(self.to_dict(), separators=(",", ":"), allow_nan=True)
 
+    def to_reference_json(self) -> str:
+        """The document exactly as the reference's writer produces it
+        (``KernelModule::toJson``, ``compiler/src/support/kernel_ir.cpp:97-254``,
+        serialized by ``compiler/src/core/json.cpp:301-312``): ``"math"`` and
+        ``"family"`` only on Compute nodes, +/-inf constants clamped to
+        +/-1e308, NaN written as null, doubles printed with 17 significant
+        digits. The backend's reader accepts it unchanged: a Call's target is
+        inferred from its operands and +/-1e308 reads back as +/-inf."""
+        d = self.to_dict()
+        for n in d["nodes"]:
+            if n["op"] != "compute":
+                n.pop("math", None)
+                n.pop("family", None)
+        return _reference_serialize(d)
+
     # --- binding helpers (KernelBufferBindings layout, execution.h:117-130)
     def input_ids(self) -> List[int]:
         return [i for i, b in enumerate(self.buffers) if b.is_input]
@@ -237,5 +252,48 @@ class KernelModule:
         return [i for i in range(len(self.nodes)) if i not in referenced]
 
 
+def is_multidim_module(km: KernelModule) -> bool:
+    """isMultiDimModule (backends/cpu/src/cpp_emitter.cpp:667-687): selects
+    the artifact ABI form (multi-dim int return vs legacy 1-D void)."""
+    for n in km.nodes:
+        if n.accum != "none" or n.begin_coeffs or n.end_coeffs or n.out_index_coeffs:
+            return True
+        if n.end == DYNAMIC and n.end_buf != INVALID_ID:
+            return True
+        if n.op == "guard" and n.guard_coeffs:
+            return True
+        for e in n.exprs:
+            if e.a.kind == "elem_idx" or e.b.kind == "elem_idx":
+                return True
+    return False
+
+
 def is_finite_const(v: float) -> bool:
     return math.isfinite(v)
+
+
+def _reference_double(v: float) -> str:
+    """serializeDouble (compiler/src/core/json.cpp:301-312)."""
+    if math.isnan(v):
+        return "null"
+    if math.isinf(v):
+        return "1e308" if v > 0 else "-1e308"
+    return "%.17g" % v
+
+
+def _reference_serialize(v) -> str:
+    if v is True:
+        return "true"
+    if v is False:
+        return "false"
+    if v is None:
+        return "null"
+    if isinstance(v, int):
+        return str(v)
+    if isinstance(v, float):
+        return _reference_double(v)
+    if isinstance(v, str):
+        return json.dumps(v)
+    if isinstance(v, list):
+        return "[" + ",".join(_reference_serialize(x) for x in v) + "]"
+    return "{" + ",".join(json.dumps(k) + ":" + _reference_serialize(x) for k, x in v.items()) + "}"

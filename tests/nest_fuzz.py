@@ -21,6 +21,10 @@ from mlk2_amd.kernel_ir import (KernelBuffer, KernelExpr, KernelModule, KernelNo
 
 BINARY = ["add", "sub", "mul", "div"]
 UNARY = ["neg"]
+# With exact_ops=False the chains also draw the device-libm operations and
+# the guarded ones (kernel_buffers.cpp:130-160).
+TRANS_BINARY = ["pow"]
+TRANS_UNARY = ["exp", "log", "sin", "cos", "tan", "tanh", "sqrt", "rsqrt", "erf", "gelu"]
 
 
 class _Gen:
@@ -65,11 +69,14 @@ class _Gen:
     def pair(self, ranges):
         n = self.ri(1, 3)
         exprs = []
+        unary = UNARY if self.exact_ops else UNARY + TRANS_UNARY
+        binary = BINARY if self.exact_ops else BINARY + TRANS_BINARY
+        p_unary = 0.15 if self.exact_ops else 0.45
         for k in range(n):
-            if self.rng.random() < 0.15:
-                exprs.append(KernelExpr(str(self.rng.choice(UNARY)), self.operand(ranges, k), const(0.0)))
+            if self.rng.random() < p_unary:
+                exprs.append(KernelExpr(str(self.rng.choice(unary)), self.operand(ranges, k), const(0.0)))
             else:
-                exprs.append(KernelExpr(str(self.rng.choice(BINARY)), self.operand(ranges, k),
+                exprs.append(KernelExpr(str(self.rng.choice(binary)), self.operand(ranges, k),
                                         self.operand(ranges, k)))
         c = self.km.add_node(KernelNode(op="compute", math=exprs[-1].op, exprs=exprs))
         b = int(self.rng.choice(self.writable))
@@ -149,8 +156,8 @@ class _Gen:
         return self.km
 
 
-def random_module(seed: int) -> KernelModule:
-    g = _Gen(seed)
+def random_module(seed: int, exact_ops: bool = True) -> KernelModule:
+    g = _Gen(seed, exact_ops)
     for _ in range(g.ri(1, 3)):
         g.loop([], 0)
     return g.finish()

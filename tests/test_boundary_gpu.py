@@ -1,0 +1,188 @@
+"""Executor semantics at the boundary, on the device, against the oracle.
+
+* Call(MatMul) skips A[i,p] == 0 (gemmRowBlock, runtime/src/execution/
+  kernel_buffers.cpp:422): 0 * inf or 0 * NaN in B must not reach C. The
+  backend scans B for non-finite values and runs the exact skip kernel when
+  there are any; otherwise the MFMA forms.
+* A fused class keeps its temps on chip only when no other root reads them;
+  a later root that reads the softmax row max, or the scaled scores, makes
+  the nest run with the walker's materialized temps (kernel_buffers.cpp:
+  902-920).
+* Modules serialized exactly as the reference's writer does them (Call
+  targets without "math", -inf as -1e308, NaN as null) run like the
+  lossless document, all-(-inf) softmax rows included.
+* Each stream gets its own artifact scratch, so runs of one artifact on two
+  streams at once do not share temps.
+"""
+import math
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from mlk2_amd import backend
+from mlk2_amd import fixtures as fx
+from mlk2_amd import inputs
+from mlk2_amd.backend import DeviceBuffer
+from mlk2_amd.parity import max_rel
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(f"[boundary] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def same_class_close(got, ref, tol):
+    """Same NaN positions, same infinities, |got-ref|/max(|ref|,1) <= tol."""
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    assert np.array_equal(np.isnan(got), np.isnan(ref)), "NaN positions differ"
+    inf = np.isinf(ref)
+    assert np.array_equal(got[inf], ref[inf]), "infinities differ"
+    fin = np.isfinite(ref)
+    return max_rel(got[fin], ref[fin]) <= tol
+
+
+def test_skip_zero_a_reference_fixture(hip):
+    # The oracle's own fixture (2x2, f64): C stays finite where A[i,p] == 0
+    # meets B[p,j] = inf, and is inf where A[i,p] != 0 does.
+    A = np.array([0.0, 1.0, 2.0, 3.0])
+    B = np.array([np.inf, 1.0, 1.0, 1.0])
+    C0 = np.array([10.0, 20.0, 30.0, 40.0])
+    call = fx.matmul_call_module(2, 2, 2, "f64", "f64")
+    got = hip.build(call).run({0: A, 1: B, 2: C0})[2]
+    ref = oracle.run(call, {0: A, 1: B}, init={2: C0})[2]
+    say(f"skip-zero-A 2x2 f64: {got.tolist()} (oracle {ref.tolist()})")
+    assert got.tolist() == [11.0, 21.0, np.inf, 45.0]
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("dt_in,dt_out,m,k,n", [("f32", "f32", 256, 64, 256), ("f16", "f32", 256, 256, 256),
+                                                ("f64", "f64", 70, 33, 65), ("f32", "f32", 1024, 1024, 1024)])
+def test_skip_zero_a_with_nonfinite_b(hip, dt_in, dt_out, m, k, n):
+    # Shapes that take the MFMA forms when B is finite. A holds zeros in some
+    # columns p whose B rows hold inf, -inf or NaN; the rows of A that are
+    # non-zero there make those C entries non-finite, the rest stay finite.
+    rng = np.random.default_rng(5)
+    A = rng.uniform(-1, 1, (m, k))
+    B = rng.uniform(-1, 1, (k, n))
+    for p, bad in ((3, np.inf), (k // 2, -np.inf), (k - 1, np.nan)):
+        B[p, rng.integers(0, n, 8)] = bad
+        A[:, p] = 0.0
+        A[rng.integers(0, m, 2), p] = 0.5     # two rows read the non-finite values
+    np_dt = {"f32": np.float32, "f16": np.float16, "f64": np.float64}[dt_in]
+    A = A.astype(np_dt).astype(np.float64)
+    B = B.astype(np_dt).astype(np.float64)
+    C0 = rng.uniform(-1, 1, m * n)
+    call = fx.matmul_call_module(m, k, n, dt_in, dt_out)
+    ref = oracle.run(call, {0: A.reshape(-1), 1: B.reshape(-1)}, init={2: C0})[2]
+    got = hip.build(call).run({0: A, 1: B, 2: C0})[2]
+    nonfinite = int((~np.isfinite(ref)).sum())
+    tol = 1e-12 if dt_in == "f64" else (1e-5 * math.sqrt(k) if dt_in == "f32" else 1e-2)
+    ok = same_class_close(got, ref, tol)
+    say(f"skip-zero-A {dt_in} {m}x{k}x{n}: {nonfinite} non-finite outputs, all finite ones within {tol:g}: {ok}")
+    assert 0 < nonfinite < m * n // 4 and ok
+    # The same inputs with B finite run the MFMA forms and still match.
+    Bf = np.where(np.isfinite(B), B, 0.25)
+    ref2 = oracle.run(call, {0: A.reshape(-1), 1: Bf.reshape(-1)}, init={2: C0})[2]
+    got2 = hip.build(call).run({0: A, 1: Bf, 2: C0})[2]
+    assert np.isfinite(got2).all() and max_rel(got2, ref2) <= tol
+
+
+def test_fused_softmax_temps_read_by_a_later_root(hip):
+    km = fx.softmax_rowmax_reader_module(32, 256)
+    x = inputs.config_inputs("c2", {"m": 32, "k": 256})["x"]
+    art = hip.build(km)
+    say(f"softmax + row-max reader: {art.class_name}")
+    assert not art.class_name.startswith("softmax-nest")
+    got = art.run({0: x})
+    ref = oracle.run(km, {0: x})
+    ids = km.output_ids()
+    assert max_rel(got[ids[0]], ref[ids[0]]) <= 1e-6
+    # The row max read back is the walker's, bit for bit (an f32 buffer's max).
+    assert np.array_equal(got[ids[1]], ref[ids[1]])
+    assert np.array_equal(got[ids[1]], x.astype(np.float64).max(axis=1))
+
+
+def test_fused_score_temps_read_by_a_later_root(hip):
+    km = fx.score_reader_module(1, 256, 128)
+    d = inputs.config_inputs("c5", {"batch": 1, "seq": 256, "dim": 128})
+    arrays = {0: d["Q"], 1: d["K"], 2: d["bias"]}
+    art = hip.build(km)
+    say(f"score-softmax + score reader: {art.class_name}")
+    assert "score-softmax" not in art.class_name
+    got = art.run(arrays)
+    ref = oracle.run(km, arrays)
+    for i in km.output_ids():
+        assert max_rel(got[i], ref[i]) <= 1e-5, (i, max_rel(got[i], ref[i]))
+
+
+@pytest.mark.parametrize("km_name", ["c2_call", "c2_synth", "c4_call", "c5", "rowsum_call"])
+def test_reference_documents_run_like_lossless_ones(hip, km_name):
+    m, k = 64, 512
+    x = inputs.config_inputs("c2", {"m": m, "k": k})["x"].astype(np.float64)
+    x[3, :] = -np.inf                              # all -inf row: NaN in the walker (-inf - -inf)
+    x[7, :] = np.nan
+    x[9, 5] = np.inf
+    if km_name == "c2_call":
+        km, arrays = fx.config2_module(m, k, 1), {0: x}
+    elif km_name == "c2_synth":
+        km, arrays = fx.config2_module(m, k, 2), {0: x}
+    elif km_name == "rowsum_call":
+        km, arrays = fx.reducesum_call_module(m, k), {0: x}
+    elif km_name == "c4_call":
+        d = inputs.config_inputs("c4a", {"m": 256, "k": 128, "n": 256})
+        km, arrays = fx.config4_module(256, 128, 256, "f32", 1), {0: d["A"], 1: d["B"]}
+    else:
+        d = inputs.config_inputs("c5", {"batch": 2, "seq": 256, "dim": 128})
+        km, arrays = fx.score_softmax_module(2, 256, 128), {0: d["Q"], 1: d["K"], 2: d["bias"]}
+    a_ref = hip.build(km, reference_document=True)
+    a_ext = hip.build(km)
+    assert a_ref.class_name == a_ext.class_name
+    got = a_ref.run(arrays)
+    ext = a_ext.run(arrays)
+    ref = oracle.run(km, {i: arrays[i] for i in km.input_ids()})
+    tol = {"c2_call": 1e-6, "c2_synth": 1e-6, "rowsum_call": 1e-12, "c4_call": 1e-5 * math.sqrt(128),
+           "c5": 1e-2}[km_name]
+    for i in km.output_ids():
+        assert np.array_equal(got[i], ext[i], equal_nan=True)
+        assert same_class_close(got[i], ref[i], tol), (km_name, i)
+    say(f"reference document {km_name}: {a_ref.class_name}, same bits as the lossless document")
+
+
+def test_runs_on_two_streams_use_separate_scratch(hip):
+    # The generic loop-nest path materializes the softmax temps; two runs of
+    # one artifact in flight on two streams must not share them.
+    km = fx.softmax_rowmax_reader_module(256, 512)
+    art = hip.build(km)
+    assert art.class_name.startswith("loop-nest")
+    xs = [inputs.config_inputs("c2", {"m": 256, "k": 512})["x"], None]
+    xs[1] = (xs[0][::-1] * 0.5).copy()
+    lib = backend.lib()
+    import ctypes
+    streams = []
+    for _ in range(2):
+        s = ctypes.c_void_p()
+        assert lib.mlkhip_stream_create(ctypes.byref(s)) == 0
+        streams.append(s.value)
+    ids = km.output_ids()
+    bufs = []
+    for x in xs:
+        b = {0: DeviceBuffer.from_array(x, "f32")}
+        for i in ids:
+            b[i] = DeviceBuffer(km.buffers[i].elements, "f32")
+        bufs.append(b)
+    for rep in range(3):
+        for b, s in zip(bufs, streams):
+            art.run_device(b, stream=s, sync=False)
+    assert lib.mlkhip_synchronize() == 0
+    for x, b in zip(xs, bufs):
+        ref = oracle.run(km, {0: x})
+        assert max_rel(b[ids[0]].to_numpy(), ref[ids[0]]) <= 1e-6
+        assert np.array_equal(b[ids[1]].to_numpy().astype(np.float64), ref[ids[1]])
+    for s in streams:
+        lib.mlkhip_stream_destroy(s)
+    say("two streams, separate scratch: both runs match the oracle")

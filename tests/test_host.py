@@ -13,7 +13,10 @@ import pytest
 from mlk2_amd import backend as be
 from mlk2_amd import fixtures as fx
 import test_nest as tn
-from mlk2_amd.kernel_ir import KernelExpr, const, elem_a, temp
+import numpy as np
+
+from mlk2_amd.kernel_ir import (INVALID_ID, KernelBuffer, KernelExpr, KernelModule, KernelNode, const,
+                                elem_a, temp)
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
@@ -85,23 +88,98 @@ def test_unrecognized_nest_takes_generic_path():
         be.plan(km)
 
 
-def test_reference_writer_quirks_parse():
-    # The reference writer clamps -inf to -1e308 and writes NaN as null
-    # (compiler/src/core/json.cpp:300-312); both must parse.
-    km = fx.config2_module(4, 8, 2)
-    doc = json.loads(km.to_json())
-    for n in doc["nodes"]:
-        for e in n.get("exprs", []):
-            if e["a"]["kind"] == "const" and math.isinf(e["a"]["value"]):
-                e["a"]["value"] = -1e308
-    text = json.dumps(doc).encode()
+def _plan_text(text: bytes):
     cls = ctypes.create_string_buffer(256)
     pol = ctypes.create_string_buffer(64)
     n = ctypes.c_int()
     rc = be.lib().mlkhip_plan(text, len(text), cls, 256, pol, 64, ctypes.byref(n))
-    # -1e308 is not -inf: the softmax class needs the exact init, so the
-    # module runs on the generic loop-nest path with the walker's semantics.
-    assert rc == 0 and cls.value.decode() == "loop-nest"
+    return rc, cls.value.decode(), pol.value.decode(), n.value
+
+
+def test_reference_writer_quirks_parse():
+    # The reference writer clamps -inf to -1e308 and writes NaN as null
+    # (compiler/src/core/json.cpp:300-312). The synthesized softmax's -inf
+    # init therefore arrives as -1e308 and must still be the softmax class.
+    km = fx.config2_module(4, 8, 2)
+    text = km.to_reference_json()
+    assert '"value":-1e308' in text and "Infinity" not in text
+    rc, cls, _, _ = _plan_text(text.encode())
+    assert rc == 0 and cls == "softmax-nest"
+
+
+@pytest.mark.parametrize("km", [
+    fx.config1_module(1 << 12), fx.config2_module(64, 128, 1), fx.config2_module(64, 128, 2),
+    fx.config3_module(64, 128, 2),
+    fx.config4_module(64, 32, 48, "f32", 1), fx.config4_module(256, 64, 256, "f16", 2),
+    fx.reducesum_call_module(8, 16), fx.synth_reducesum(fx.reducesum_call_module(8, 16)),
+    fx.score_softmax_module(2, 256, 128),
+])
+def test_reference_document_plans_like_the_extended_one(km):
+    # Every configuration's module, serialized exactly as the reference
+    # writer would (no Call "math", clamped infinities, null NaN), plans to
+    # the same class and policy as the lossless document.
+    ref = _plan_text(km.to_reference_json().encode())
+    ext = _plan_text(km.to_json().encode())
+    assert ref[0] == 0 and ref == ext
+
+
+@pytest.mark.parametrize("math_name,with_b,out_rank", [("matmul", True, 2), ("softmax", False, 2),
+                                                       ("reduce_sum", False, 1)])
+def test_call_target_inferred_from_operands(math_name, with_b, out_rank):
+    # tools/mlk-poly/poly_bench.cpp:121-158: MatMul binds B; Softmax is rank-2
+    # in and out; ReduceSum is rank-2 in, rank-1 out.
+    km = KernelModule()
+    a = km.add_buffer(KernelBuffer("A", "f32", is_input=True, elements=8 * 4, dims=[8, 4]))
+    b = km.add_buffer(KernelBuffer("B", "f32", is_input=True, elements=4 * 6, dims=[4, 6])) if with_b else INVALID_ID
+    dims = [8, 6] if with_b else ([8, 4] if out_rank == 2 else [8])
+    o = km.add_buffer(KernelBuffer("Y", "f32", is_output=True, elements=int(np.prod(dims)), dims=dims))
+    km.add_node(KernelNode(op="call", math=math_name, a=a, b=b, out=o))
+    rc, cls, _, _ = _plan_text(km.to_reference_json().encode())
+    assert '"math"' not in km.to_reference_json()
+    want = {"matmul": "gemm-call", "softmax": "softmax-call", "reduce_sum": "reducesum-call"}[math_name]
+    assert rc == 0 and cls == want
+
+
+def test_fused_softmax_refused_when_a_later_root_reads_its_temps():
+    # The softmax class keeps the row max, exponentials and sum on chip. A
+    # later root that reads the row-max temp makes the nest run on the
+    # generic loop-nest path, whose temps are materialized as the walker's.
+    km = fx.softmax_rowmax_reader_module(4, 8)
+    cls, _, _ = be.plan(km)
+    assert not cls.startswith("softmax-nest"), cls
+    assert cls.startswith("loop-nest"), cls
+    # Without the reader the same nest is the softmax class.
+    cls2, _, _ = be.plan(fx.config2_module(4, 8, 2))
+    assert cls2 == "softmax-nest"
+
+
+def test_fused_score_softmax_refused_when_a_later_root_reads_the_scores():
+    km = fx.score_softmax_module(1, 256, 128)
+    cls, _, _ = be.plan(km)
+    assert cls == "score-softmax"
+    km2 = fx.score_reader_module(1, 256, 128)
+    cls2, _, _ = be.plan(km2)
+    assert "score-softmax" not in cls2, cls2
+
+
+def test_hiprtc_options_disable_packed_fp32():
+    buf = ctypes.create_string_buffer(512)
+    n = be.lib().mlkhip_jit_options(b"gfx950", buf, 512)
+    opts = buf.value.decode().split(" ")
+    assert n == len(opts)
+    assert opts[0] == "--offload-arch=gfx950"
+    assert "-ffp-contract=off" in opts
+    i = opts.index("-packed-fp32-ops")
+    assert opts[i - 3:i + 1] == ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+
+
+def test_elementwise_instances_have_distinct_kernel_names():
+    _, s1 = be.compile_check(fx.config1_module(1 << 12), 0, "gfx950")
+    _, s3 = be.compile_check(fx.config3_module(64, 128, 2), 0, "gfx950")
+    n1 = [l for l in s1.splitlines() if l.startswith("#define MLK_KERNEL_NAME ")][0].split()[-1]
+    n3 = [l for l in s3.splitlines() if l.startswith("#define MLK_KERNEL_NAME ")][0].split()[-1]
+    assert n1.startswith("mlk_elementwise_") and n3.startswith("mlk_elementwise_")
+    assert len(n1) == len("mlk_elementwise_") + 12 and n1 != n3
 
 
 @pytest.mark.parametrize("km", [fx.config1_module(1 << 24), fx.config3_module(4096, 4096, 2),

@@ -431,6 +431,37 @@ def test_fuzz_gpu(hip, seed):
             assert nf.same_bits(got[i], ref[i]), (seed, i)
 
 
+def close_to_walker(got, ref, tol):
+    """NaN where the walker has NaN, the same infinities, and
+    |got - ref| / max(|ref|, 1) <= tol elsewhere."""
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    if not np.array_equal(np.isnan(got), np.isnan(ref)):
+        return False
+    inf = np.isinf(ref)
+    if not np.array_equal(got[inf], ref[inf]):
+        return False
+    return max_rel(got, ref) <= tol
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(24))
+def test_fuzz_transcendental_gpu(hip, seed):
+    # The fuzz forests with chains that also draw exp, log, sin, cos, tan,
+    # tanh, sqrt, rsqrt, erf, gelu and pow: device libm against the host's,
+    # within 1e-9 of the reference's relative measure (a few f64 ULP per op,
+    # grown through at most three ops per pair and the accumulations).
+    km = nf.random_module(seed, exact_ops=False)
+    say(f"transcendental fuzz seed {seed}: {backend.plan(km)[0]}")
+    arrays, scalars = nf.random_inputs(km, seed)
+    ref = oracle.run(km, {i: arrays[i] for i in km.input_ids()}, scalars,
+                     init={i: arrays[i] for i in km.output_ids()})
+    for mod in (km, generic(km, canonical=False)):
+        got = hip.build(mod).run(arrays, scalars)
+        for i in km.output_ids():
+            assert close_to_walker(got[i], ref[i], 1e-9), (seed, i, max_rel(got[i], ref[i]))
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("seed", range(24))
 def test_tiled_fuzz_gpu(hip, seed):

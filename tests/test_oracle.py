@@ -285,3 +285,69 @@ def test_score_softmax_composition_matches_numpy():
     e = np.exp(sc)
     want = e / e.sum(axis=1, keepdims=True)
     assert np.abs(out - want).max() < 1e-14
+
+
+# Op table of the evaluator (kernel_buffers.cpp:130-160): each op name maps to
+# the host libm function of that name, which Python's math module calls too,
+# so the oracle must agree with it bit for bit (a swapped or mis-dispatched
+# op fails). Guard arms are covered above and below.
+_LIBM = {"exp": math.exp, "cos": math.cos, "tan": math.tan, "tanh": math.tanh, "erf": math.erf}
+
+
+def _oracle_unary(op, xs, family=None):
+    km = fx.lower_elementwise([("x", [len(xs)], "f64")], [KernelExpr(op, fx.elem_a(), const(0.0))],
+                              [len(xs)], "f64", family=family)
+    return oracle.run(km, {0: np.asarray(xs, dtype=np.float64)})[1]
+
+
+@pytest.mark.parametrize("op", sorted(_LIBM))
+def test_transcendental_ops_dispatch_to_libm(op):
+    xs = np.linspace(-3.0, 3.0, 97)
+    got = _oracle_unary(op, xs)
+    want = np.array([_LIBM[op](x) for x in xs])
+    assert np.array_equal(got.view(np.int64), want.view(np.int64)), op
+
+
+def test_log_sqrt_rsqrt_sin_libm_family_dispatch():
+    xs = np.geomspace(1e-3, 1e3, 61)
+    assert np.array_equal(_oracle_unary("log", xs), np.log(xs))
+    assert np.array_equal(_oracle_unary("sqrt", xs), np.sqrt(xs))
+    assert np.array_equal(_oracle_unary("rsqrt", xs), 1.0 / np.sqrt(xs))
+    # Without the poly7 family, Sin is the libm sine (kernel_buffers.cpp:143).
+    ys = np.linspace(-20.0, 20.0, 81)
+    assert np.array_equal(_oracle_unary("sin", ys), np.array([math.sin(y) for y in ys]))
+    # And with it, the polynomial, which differs from libm somewhere here.
+    assert not np.array_equal(_oracle_unary("sin", ys, "poly7"), _oracle_unary("sin", ys))
+
+
+def test_pow_general_arm_and_fast_form():
+    # Pow: (2, 2) -> a * a, otherwise std::pow, including its special cases.
+    pairs = [(2.0, 2.0, 4.0), (2.0, 0.5, math.sqrt(2.0)), (-2.0, 3.0, -8.0), (0.0, -1.0, math.inf),
+             (9.0, 0.5, 3.0), (4.0, -0.5, 0.5)]
+    for a, b, want in pairs:
+        km = fx.lower_elementwise([], [KernelExpr("pow", const(a), const(b))], [1], "f64")
+        assert oracle.run(km, {})[0][0] == want, (a, b)
+    km = fx.lower_elementwise([], [KernelExpr("pow", const(-2.0), const(0.5))], [1], "f64")
+    assert math.isnan(oracle.run(km, {})[0][0])
+
+
+def test_gelu_closed_forms():
+    # Gelu is the tanh form 0.5 a (1 + tanh(sqrt(2/pi) (a + 0.044715 a^3)))
+    # (kernel_buffers.cpp:152-154). Closed forms it must satisfy:
+    xs = np.linspace(-6.0, 6.0, 241)
+    g = _oracle_unary("gelu", xs)
+    gm = _oracle_unary("gelu", -xs)
+    # gelu(0) = 0 exactly.
+    assert _oracle_unary("gelu", [0.0])[0] == 0.0
+    # The tanh is odd, so gelu(x) - gelu(-x) = x (to rounding).
+    assert np.max(np.abs((g - gm) - xs)) <= 8 * np.finfo(np.float64).eps * 6.0
+    # Limits: the tanh saturates to +-1 in f64, so gelu(x) = x and gelu(-x) = 0.
+    big = _oracle_unary("gelu", [10.0, 30.0, -10.0, -30.0])
+    assert big[0] == 10.0 and big[1] == 30.0 and big[2] == 0.0 and big[3] == 0.0
+    # It approximates x * Phi(x) (the erf form) within 4.8e-4, the accuracy of
+    # the tanh approximation; 0.8 in place of sqrt(2/pi) gives 6.4e-4 and a
+    # dropped cubic term 2e-2.
+    exact = np.array([0.5 * x * (1.0 + math.erf(x / math.sqrt(2.0))) for x in xs])
+    assert np.max(np.abs(g - exact)) < 4.8e-4
+    wrong_cubic = np.array([0.5 * x * (1.0 + math.tanh(0.7978845608028654 * x)) for x in xs])
+    assert np.max(np.abs(wrong_cubic - exact)) > 1e-2 > np.max(np.abs(g - exact))
