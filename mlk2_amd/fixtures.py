@@ -297,7 +297,8 @@ def config4_module(m: int, k: int, n: int, dtype_in: str, tier: int = 2) -> Kern
 
 # ------------------------------------------------------ score + softmax --
 def score_softmax_module(batch: int, seq: int, dim: int, dtype_in: str = "f16",
-                         scale_div: Optional[float] = None, dtype_out: str = "f32") -> KernelModule:
+                         scale_div: Optional[float] = None, dtype_out: str = "f32",
+                         reader_output: bool = False) -> KernelModule:
     """Config 5 as a Kernel IR composition of reference pieces (no single
     reference class covers it): a batched QK^T init+accumulate nest written
     like buildGemmNodes (:58-147) with the K operand read transposed through
@@ -313,6 +314,8 @@ def score_softmax_module(batch: int, seq: int, dim: int, dtype_in: str = "f16",
     kb = km.add_buffer(KernelBuffer("K", dtype_in, True, False, False, batch * seq * dim, [batch, seq, dim]))
     bias = km.add_buffer(KernelBuffer("bias", "f32", True, False, False, seq, [seq]))
     y = km.add_buffer(KernelBuffer("S", dtype_out, False, True, False, R * seq, [R, seq]))
+    if reader_output:  # a second output, filled by a root the caller appends
+        km.add_buffer(KernelBuffer("scores_out", "f32", False, True, False, R * seq, [R, seq]))
     sc = km.add_buffer(KernelBuffer("scores", "f32", is_temp=True, elements=R * seq, dims=[R, seq]))
     # Root 1: b{ i{ j{ SC=0; k{ SC += Q[b,i,k] * K[b,j,k] } } } }
     n = []
@@ -348,11 +351,10 @@ def score_softmax_module(batch: int, seq: int, dim: int, dtype_in: str = "f16",
     return km
 
 
-def _append_copy_root(km: KernelModule, src: int, dims: Sequence[int], name: str) -> KernelModule:
-    """Appends an output buffer of `dims` and a last root that copies temp
-    `src` into it (Add(src[...], 0) over a perfect nest): a later reader of
-    a temp that a fused class would otherwise keep on chip."""
-    out = km.add_buffer(KernelBuffer(name, "f32", False, True, False, _numel(dims), list(dims)))
+def _append_copy_root(km: KernelModule, src: int, dims: Sequence[int], out: int) -> KernelModule:
+    """Appends a last root that copies temp `src` into output buffer `out`
+    (Add(src[...], 0) over a perfect nest): a later reader of a temp that a
+    fused class would otherwise keep on chip."""
     coeffs = [_stride_of(dims, d) for d in range(len(dims))]
     c = km.add_node(KernelNode(op="compute", exprs=[KernelExpr("add", elem_idx(src, coeffs), const(0.0))]))
     st = km.add_node(KernelNode(op="store", out=out, out_index_coeffs=coeffs))
@@ -364,18 +366,23 @@ def _append_copy_root(km: KernelModule, src: int, dims: Sequence[int], name: str
 
 def softmax_rowmax_reader_module(m: int, k: int) -> KernelModule:
     """Config 2's synthesized softmax followed by a root that copies the
-    row-max temp into an output."""
-    km = config2_module(m, k, tier=2)
+    row-max temp into a second output. Outputs precede the temps in the
+    table, as the reference's binding requires (an output id indexes the
+    outputs after the input count, kernel_buffers.cpp:200-230)."""
+    km = softmax_call_module(m, k, "f32")
+    r = km.add_buffer(KernelBuffer("rowmax_out", "f32", False, True, False, m, [m]))
+    km = synth_softmax(km)
     rm = next(i for i, b in enumerate(km.buffers) if b.name == "softmax_rowmax")
-    return _append_copy_root(km, rm, [m], "rowmax_out")
+    return _append_copy_root(km, rm, [m], r)
 
 
 def score_reader_module(batch: int, seq: int, dim: int) -> KernelModule:
     """Config 5's composition followed by a root that copies the scaled
-    score temp into an output."""
-    km = score_softmax_module(batch, seq, dim)
+    score temp into a second output (placed before the temps)."""
+    km = score_softmax_module(batch, seq, dim, reader_output=True)
     sc = next(i for i, b in enumerate(km.buffers) if b.name == "scores")
-    return _append_copy_root(km, sc, [batch * seq, seq], "scores_out")
+    out = next(i for i, b in enumerate(km.buffers) if b.name == "scores_out")
+    return _append_copy_root(km, sc, [batch * seq, seq], out)
 
 
 def _softmax_over(km: KernelModule, x: int, y: int, rows: int, cols: int) -> KernelModule:

@@ -145,7 +145,7 @@ def test_reference_documents_run_like_lossless_ones(hip, km_name):
     got = a_ref.run(arrays)
     ext = a_ext.run(arrays)
     ref = oracle.run(km, {i: arrays[i] for i in km.input_ids()})
-    tol = {"c2_call": 1e-6, "c2_synth": 1e-6, "rowsum_call": 1e-12, "c4_call": 1e-5 * math.sqrt(128),
+    tol = {"c2_call": 1e-6, "c2_synth": 1e-6, "rowsum_call": 1e-6, "c4_call": 1e-5 * math.sqrt(128),
            "c5": 1e-2}[km_name]
     for i in km.output_ids():
         assert np.array_equal(got[i], ext[i], equal_nan=True)

@@ -128,7 +128,7 @@ def check(op, dtype, family, got, ref):
         assert d <= 4.0, (op, dtype, d)
         return f"{d:g} f32 ULP (split-precision poly7, bound 4)"
     if op == "gelu":
-        r = max_rel(got, ref)
+        r = max_rel(got[finite_ref], ref[finite_ref])
         tol = 1e-14 if dtype == "f64" else 1e-7
         assert r <= tol, (op, dtype, r)
         return f"rel {r:.2e} (bound {tol:g})"
@@ -187,8 +187,10 @@ def test_guard_arms_gpu(hip, dtype):
         ref = oracle.run(km, arrays)[2 if y is not None else 1]
         # The oracle states the reference's arms; NaN compared as NaN.
         assert np.array_equal(ref, np.asarray(want), equal_nan=True), (op, ref)
-        assert np.array_equal(got.view(np.int64), ref.view(np.int64)) or \
-            np.array_equal(got, ref, equal_nan=True), (op, dtype, got, ref)
+        if dtype == "f32":
+            ref = ref.astype(np.float32).astype(np.float64)   # one rounding of the f64 value
+        same = (got.view(np.int64) == ref.view(np.int64)) | (np.isnan(got) & np.isnan(ref))
+        assert same.all(), (op, dtype, got, ref)
         say(f"guard {op} {dtype}: {got.tolist()}")
     km = fx.lower_elementwise([("x", [4], dtype), ("y", [4], dtype)], [KernelExpr("pow", elem_a(), elem_b())],
                               [4], dtype)
