@@ -148,6 +148,29 @@ int mlkhip_kernel_1d(const mlkhip_artifact* a, double* const* ptrs, int n_ptrs, 
 int mlkhip_run_device(const mlkhip_artifact* a, const mlkhip_binding* binds, int n_binds,
                       const double* scalars, int64_t n_scalars, int64_t elements, void* stream);
 
+/* No counterpart in the reference: the allocation-free variant of
+ * mlkhip_run_device, for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). The caller passes inputs and outputs as for mlkhip_run_device;
+ * every scratch buffer the run needs (materialized temps, zeroed on every
+ * run, and the score-softmax row statistics) is carved out of one
+ * file-scope device array of mlkhip_noalloc_scratch_bytes() bytes (32 MiB)
+ * that each GPU holds until the process ends. A run that needs more is
+ * refused (MLKHIP_REFUSED, see mlkhip_last_error) before anything is
+ * launched, as is a step that needs a host read-back (a loop nest with
+ * run-time bounds checks). A Call(MatMul) step always runs the exact
+ * skip-zero-A kernel here (the non-finite scan of B needs a read-back). Calls
+ * no hipMalloc or hipFree. Every call on one GPU shares that GPU's array,
+ * which keeps the last call's contents: calls that overlap on one GPU (on
+ * different streams, or from different threads) race. Enqueued on `stream`,
+ * asynchronous. */
+int mlkhip_run_device_noalloc(const mlkhip_artifact* a, const mlkhip_binding* binds, int n_binds,
+                              const double* scalars, int64_t n_scalars, int64_t elements, void* stream);
+
+/* Size in bytes of the allocation-free entry's device array (0 without a
+ * device). */
+size_t mlkhip_noalloc_scratch_bytes(void);
+
 /* Times `reps` back-to-back launches of the device entry after `warmup`
  * untimed ones, with HIP events on `stream`; writes per-launch milliseconds
  * (reps values) into `ms_out`. */

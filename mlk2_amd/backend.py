@@ -111,6 +111,10 @@ def lib():
     L.mlkhip_fill32.argtypes = [c.c_void_p, c.c_uint32, c.c_size_t]
     L.mlkhip_stream_create.argtypes = [c.POINTER(c.c_void_p)]
     L.mlkhip_stream_destroy.argtypes = [c.c_void_p]
+    L.mlkhip_run_device_noalloc.argtypes = [c.c_void_p, c.POINTER(Binding), c.c_int, _PD, c.c_int64,
+                                            c.c_int64, c.c_void_p]
+    L.mlkhip_noalloc_scratch_bytes.argtypes = []
+    L.mlkhip_noalloc_scratch_bytes.restype = c.c_size_t
     L.mlkhip_emit_artifact.argtypes = [c.c_char_p, c.c_size_t, c.c_char_p, c.c_char_p, c.c_char_p, c.c_char_p,
                                        c.c_size_t]
     L.mlkhip_jit_options.argtypes = [c.c_char_p, c.c_char_p, c.c_size_t]
@@ -352,6 +356,17 @@ class LoadedKernel:
         sc, nsc = self._scalars(scalars)
         _check(lib().mlkhip_run_device(self._h, arr, n, sc.ctypes.data_as(_PD), nsc,
                                        int(elements), stream))
+        if sync:
+            _check(lib().mlkhip_synchronize())
+
+    def run_device_noalloc(self, bufs: Dict[int, DeviceBuffer], scalars: Sequence[float] = (),
+                           elements: int = 0, stream: Optional[int] = None, sync: bool = True) -> None:
+        """mlkhip_run_device_noalloc: scratch from the library's file-scope
+        device array, nothing allocated."""
+        arr, n = self._bindings(bufs)
+        sc, nsc = self._scalars(scalars)
+        _check(lib().mlkhip_run_device_noalloc(self._h, arr, n, sc.ctypes.data_as(_PD), nsc,
+                                               int(elements), stream))
         if sync:
             _check(lib().mlkhip_synchronize())
 

@@ -7,9 +7,22 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "runtime_abi.h"
 
 namespace {
+
+/// Device scratch of the allocation-free entry (mlkhip_run_device_noalloc):
+/// one file-scope array that each GPU the library runs on holds until the
+/// process ends. Host code never uses the name as an address: it takes the
+/// address hipGetSymbolAddress reports for the current device.
+constexpr size_t kNoAllocScratchBytes = size_t{32} << 20;
+__device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex gScratchLock;
+void* gScratchPtr[kMaxDevices] = {};
 
 int mapErr(hipError_t e, int code) { return e == hipSuccess ? 0 : code; }
 
@@ -34,6 +47,24 @@ __global__ void nonfiniteKernel(const T* p, int64_t n, uint32_t* flag) {
 }  // namespace
 
 extern "C" {
+
+int mlkd_rt_noalloc_scratch(void** ptr, size_t* bytes) {
+    *ptr = nullptr;
+    *bytes = 0;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return MLKD_RT_NO_DEVICE;
+    std::lock_guard<std::mutex> g(gScratchLock);
+    if (gScratchPtr[dev] == nullptr) {
+        // Once per device, with that device current: this device's copy of
+        // the array.
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) return MLKD_RT_LAUNCH;
+        gScratchPtr[dev] = p;
+    }
+    *ptr = gScratchPtr[dev];
+    *bytes = kNoAllocScratchBytes;
+    return 0;
+}
 
 int mlkd_rt_scan_nonfinite(const void* p, int dtype, int64_t n, uint32_t* flag, void* stream) {
     if (n <= 0) return 0;

@@ -31,6 +31,10 @@ int mlkd_rt_h2d(void* dst, const void* src, size_t bytes, void* stream);
 int mlkd_rt_d2h(void* dst, const void* src, size_t bytes, void* stream);
 int mlkd_rt_d2d(void* dst, const void* src, size_t bytes, void* stream);
 int mlkd_rt_fill32(void* p, uint32_t value, size_t bytes, void* stream);
+/// The allocation-free entry's device scratch on the current device: its
+/// address (hipGetSymbolAddress of the file-scope array, taken once per
+/// device) and size. Allocates nothing.
+int mlkd_rt_noalloc_scratch(void** ptr, size_t* bytes);
 /// Sets *flag (which the caller zeroes) to 1 when any of the n elements of
 /// `p` (dtype MLKD_F32 / F16 / F64) is an infinity or a NaN.
 int mlkd_rt_scan_nonfinite(const void* p, int dtype, int64_t n, uint32_t* flag, void* stream);

@@ -148,15 +148,86 @@ HipLoadedKernel::RunScratch& HipLoadedKernel::scratchFor(void* stream) const {
     return *scratchByStream_.back().second;
 }
 
+namespace {
+size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
+}  // namespace
+
+void HipLoadedKernel::fillScoreParams(const Step& st, const std::vector<void*>& ptr, mlkd_score_softmax& p) const {
+    p.variant = st.variant;
+    p.q = ptr[st.q];
+    p.k = ptr[st.kk];
+    p.bias = ptr[st.bias];
+    p.s = ptr[st.s];
+    p.qk_dtype = dtypeCode(km_.buffers[st.q].dtype);
+    p.bias_dtype = dtypeCode(km_.buffers[st.bias].dtype);
+    p.s_dtype = dtypeCode(km_.buffers[st.s].dtype);
+    p.batch = st.batch;
+    p.seq = st.seq;
+    p.dim = st.dim;
+    p.div = st.div;
+    p.scratch = nullptr;
+    p.scratch_bytes = 0;
+}
+
+int HipLoadedKernel::arenaLayout(const DeviceBinding* binds, int64_t elements, const ScratchArena& arena,
+                                 std::vector<size_t>& tempOff, std::vector<size_t>& stepOff,
+                                 std::string& why) const {
+    size_t used = 0;
+    tempOff.assign(km_.buffers.size(), 0);
+    stepOff.assign(plan_.steps.size(), 0);
+    for (size_t i = 0; i < bindables_.size(); ++i) {
+        const uint32_t b = bindables_[i];
+        const KernelBuffer& kb = km_.buffers[b];
+        if (!kb.isTemp || binds[i].ptr != nullptr || !plan_.tempNeeded[b]) continue;
+        tempOff[b] = used;
+        used += align256(static_cast<size_t>(bufferElements(kb, elements)) * dtypeBytes(kb.dtype));
+    }
+    std::vector<void*> ptr(km_.buffers.size(), nullptr);
+    for (size_t i = 0; i < bindables_.size(); ++i) ptr[bindables_[i]] = binds[i].ptr;
+    for (size_t si = 0; si < plan_.steps.size(); ++si) {
+        const Step& st = plan_.steps[si];
+        if (st.kind == StepKind::Nest && st.checked) {
+            why = "step " + std::to_string(si) + " (loop nest) reports run-time bounds checks through a host "
+                  "read-back, which the allocation-free entry does not do";
+            return MLKHIP_REFUSED;
+        }
+        if (st.kind == StepKind::Nest && st.variant == 1 && !st.sourceNoSlabs.empty() && noSlabFn_[si] == nullptr) {
+            why = "step " + std::to_string(si) + " pins the loop nest's no-slab form, which is not loaded yet";
+            return MLKHIP_REFUSED;
+        }
+        if (st.kind == StepKind::ScoreSoftmax) {
+            mlkd_score_softmax p;
+            fillScoreParams(st, ptr, p);
+            const int64_t need = mlkd_score_scratch_bytes(&p);
+            if (need > 0) {
+                stepOff[si] = used;
+                used += align256(static_cast<size_t>(need));
+            }
+        }
+    }
+    if (used > arena.bytes) {
+        why = "the run needs " + std::to_string(used) + " bytes of device scratch; the allocation-free entry holds " +
+              std::to_string(arena.bytes);
+        return MLKHIP_REFUSED;
+    }
+    return MLKHIP_OK;
+}
+
 int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* scalars,
                                int64_t nScalars, int64_t elements, void* stream,
-                               std::string& why) const {
+                               std::string& why, const ScratchArena* arena) const {
     if (n != static_cast<int>(bindables_.size())) {
         why = "expected " + std::to_string(bindables_.size()) + " bindings, got " + std::to_string(n);
         return MLKHIP_BAD_BINDING;
     }
+    // Scratch comes from the caller's arena (the allocation-free entry), laid
+    // out before anything is launched, or from this stream's own allocations.
+    std::vector<size_t> tempOff, stepOff;
+    if (arena != nullptr) {
+        if (const int rc = arenaLayout(binds, elements, *arena, tempOff, stepOff, why); rc != MLKHIP_OK) return rc;
+    }
     RunScratch* rs = nullptr;
-    {
+    if (arena == nullptr) {
         std::lock_guard<std::mutex> g(scratchLock_);
         rs = &scratchFor(stream);
     }
@@ -172,18 +243,22 @@ int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* 
         const int64_t need = bufferElements(kb, elements);
         if (kb.isTemp && binds[i].ptr == nullptr) {
             if (!plan_.tempNeeded[b]) continue;
-            std::lock_guard<std::mutex> g(scratchLock_);
-            if (rs->temp[b] == nullptr || rs->tempElems[b] < need) {
-                if (rs->temp[b] != nullptr) mlkd_rt_free(rs->temp[b]);
-                rs->temp[b] = nullptr;
-                if (mlkd_rt_malloc(&rs->temp[b], static_cast<size_t>(need) * dtypeBytes(kb.dtype) + 16) != 0) {
+            if (arena != nullptr) {
+                ptr[b] = arena->base + tempOff[b];
+            } else {
+                std::lock_guard<std::mutex> g(scratchLock_);
+                if (rs->temp[b] == nullptr || rs->tempElems[b] < need) {
+                    if (rs->temp[b] != nullptr) mlkd_rt_free(rs->temp[b]);
                     rs->temp[b] = nullptr;
-                    why = "temp scratch allocation failed";
-                    return MLKHIP_RUNTIME;
+                    if (mlkd_rt_malloc(&rs->temp[b], static_cast<size_t>(need) * dtypeBytes(kb.dtype) + 16) != 0) {
+                        rs->temp[b] = nullptr;
+                        why = "temp scratch allocation failed";
+                        return MLKHIP_RUNTIME;
+                    }
+                    rs->tempElems[b] = need;
                 }
-                rs->tempElems[b] = need;
+                ptr[b] = rs->temp[b];
             }
-            ptr[b] = rs->temp[b];
         } else {
             if (binds[i].dtype != dtypeCode(kb.dtype)) {
                 why = "binding " + std::to_string(i) + " (" + kb.name + ") has the wrong dtype";
@@ -288,7 +363,10 @@ int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* 
                 p.lda = st.lda;
                 p.ldb = st.ldb;
                 p.ldc = st.ldc;
-                if (st.skipZeroA && st.k > 0) {
+                if (st.skipZeroA && st.k > 0 && arena != nullptr) {
+                    // No host read-back here: always the exact skip kernel.
+                    p.skip_zero_a = 1;
+                } else if (st.skipZeroA && st.k > 0) {
                     // 0 * inf and 0 * NaN are the only products whose skip
                     // changes C beyond the sign of a zero sum, so the MFMA
                     // forms run unless B holds a non-finite value.
@@ -365,26 +443,16 @@ int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* 
                 break;
             }
             case StepKind::ScoreSoftmax: {
-                mlkd_score_softmax p;
-                p.variant = st.variant;
-                p.q = ptr[st.q];
-                p.k = ptr[st.kk];
-                p.bias = ptr[st.bias];
-                p.s = ptr[st.s];
-                p.qk_dtype = dtypeCode(km_.buffers[st.q].dtype);
                 if (km_.buffers[st.kk].dtype != km_.buffers[st.q].dtype) {
                     why = "score-softmax needs Q and K of one dtype";
                     return MLKHIP_REFUSED;
                 }
-                p.bias_dtype = dtypeCode(km_.buffers[st.bias].dtype);
-                p.s_dtype = dtypeCode(km_.buffers[st.s].dtype);
-                p.batch = st.batch;
-                p.seq = st.seq;
-                p.dim = st.dim;
-                p.div = st.div;
-                p.scratch = nullptr;
-                p.scratch_bytes = 0;
-                if (const int64_t need = mlkd_score_scratch_bytes(&p); need > 0) {
+                mlkd_score_softmax p;
+                fillScoreParams(st, ptr, p);
+                if (const int64_t need = mlkd_score_scratch_bytes(&p); need > 0 && arena != nullptr) {
+                    p.scratch = arena->base + stepOff[si];
+                    p.scratch_bytes = need;
+                } else if (need > 0) {
                     std::lock_guard<std::mutex> g(scratchLock_);
                     if (rs->step[si] == nullptr || rs->stepBytes[si] < need) {
                         if (rs->step[si] != nullptr) mlkd_rt_free(rs->step[si]);
@@ -667,6 +735,33 @@ int mlkhip_run_device(const mlkhip_artifact* a, const mlkhip_binding* binds, int
     const int rc = a->k->runDevice(b.data(), n_binds, scalars, n_scalars, elements, stream, why);
     if (rc != MLKHIP_OK) setError(rc, why);
     return rc;
+}
+
+int mlkhip_run_device_noalloc(const mlkhip_artifact* a, const mlkhip_binding* binds, int n_binds,
+                              const double* scalars, int64_t n_scalars, int64_t elements, void* stream) {
+    if (a == nullptr) return setError(MLKHIP_BAD_BINDING, "null artifact");
+    mlk::hip::ScratchArena arena;
+    void* base = nullptr;
+    if (const int rc = mlkd_rt_noalloc_scratch(&base, &arena.bytes); rc != 0) {
+        return setError(rc, "allocation-free scratch is not available on the current device");
+    }
+    arena.base = static_cast<char*>(base);
+    std::vector<mlk::hip::DeviceBinding> b(static_cast<size_t>(n_binds > 0 ? n_binds : 0));
+    for (int i = 0; i < n_binds; ++i) {
+        b[static_cast<size_t>(i)].ptr = binds[i].ptr;
+        b[static_cast<size_t>(i)].elements = binds[i].elements;
+        b[static_cast<size_t>(i)].dtype = binds[i].dtype;
+    }
+    std::string why;
+    const int rc = a->k->runDevice(b.data(), n_binds, scalars, n_scalars, elements, stream, why, &arena);
+    if (rc != MLKHIP_OK) setError(rc, why);
+    return rc;
+}
+
+size_t mlkhip_noalloc_scratch_bytes(void) {
+    void* base = nullptr;
+    size_t bytes = 0;
+    return mlkd_rt_noalloc_scratch(&base, &bytes) == 0 ? bytes : 0;
 }
 
 int mlkhip_time_device(const mlkhip_artifact* a, const mlkhip_binding* binds, int n_binds, const double* scalars,

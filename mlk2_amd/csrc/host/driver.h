@@ -12,6 +12,7 @@
 #include <string>
 #include <vector>
 
+#include "../device_abi.h"
 #include "planner.h"
 
 namespace mlk::hip {
@@ -32,6 +33,13 @@ struct DeviceBinding {
     int32_t dtype{0};
 };
 
+/// Device memory a run takes all of its scratch from instead of allocating:
+/// the allocation-free entry's file-scope array on the current device.
+struct ScratchArena {
+    char* base{nullptr};
+    size_t bytes{0};
+};
+
 class HipLoadedKernel {
 public:
     ~HipLoadedKernel();  // frees the artifact-owned scratch of every stream
@@ -41,9 +49,12 @@ public:
     const std::vector<uint32_t>& bindables() const { return bindables_; }
 
     /// Device-resident run on `stream`; returns an ABI status code and sets
-    /// `why` on failure.
+    /// `why` on failure. With `arena`, every scratch buffer (temps, launcher
+    /// scratch) is carved out of it and nothing is allocated; steps that
+    /// need a host read-back are refused (checked loop nests), and a
+    /// Call(MatMul) step runs the exact skip kernel without the scan.
     int runDevice(const DeviceBinding* binds, int n, const double* scalars, int64_t nScalars,
-                  int64_t elements, void* stream, std::string& why) const;
+                  int64_t elements, void* stream, std::string& why, const ScratchArena* arena = nullptr) const;
 
     /// Host f64 run (the mlk_kernel artifact ABI): converts, uploads, runs,
     /// downloads, synchronously.
@@ -95,6 +106,11 @@ private:
         std::vector<int64_t> stepBytes;
     };
     RunScratch& scratchFor(void* stream) const;  // caller holds scratchLock_
+    /// Offsets of a run's scratch in `arena`; refuses what does not fit or
+    /// needs a host read-back.
+    int arenaLayout(const DeviceBinding* binds, int64_t elements, const ScratchArena& arena,
+                    std::vector<size_t>& tempOff, std::vector<size_t>& stepOff, std::string& why) const;
+    void fillScoreParams(const Step& st, const std::vector<void*>& ptr, mlkd_score_softmax& p) const;
     mutable std::mutex scratchLock_;
     mutable std::vector<std::pair<void*, std::unique_ptr<RunScratch>>> scratchByStream_;
     // Loop-nest launch form 1 (no LDS slabs), compiled on first use.

@@ -1,0 +1,111 @@
+"""mlkhip_run_device_noalloc: the allocation-free variant of mlkhip_run_device.
+
+Its scratch (materialized temps, score-softmax row statistics) comes from one
+file-scope device array. Each case runs twice in a row on that array, the
+second time on a smaller input, and must match mlkhip_run_device on the same
+buffers: bit for bit where both run the same kernels, and within the path's
+tolerance for Call(MatMul), which the allocation-free entry always runs on the
+exact skip-zero-A kernel (relative |got-ref|/max(|ref|,1) <= 1e-5*sqrt(K)).
+"""
+import math
+import sys
+
+import numpy as np
+import pytest
+
+from mlk2_amd import backend
+from mlk2_amd import fixtures as fx
+from mlk2_amd import inputs
+from mlk2_amd.backend import DeviceBuffer
+from mlk2_amd.parity import max_rel
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(f"[noalloc] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def _device_bufs(km, host):
+    bufs = {}
+    for bid in km.bindable_ids():
+        b = km.buffers[bid]
+        if b.is_temp:
+            continue
+        n = int(np.prod(b.dims)) if b.dims else b.elements
+        a = host.get(bid, np.zeros(n))
+        bufs[bid] = DeviceBuffer.from_array(np.asarray(a, dtype=np.float64).reshape(-1), b.dtype)
+    return bufs
+
+
+def _both(hip, km, host):
+    """Outputs of run_device and of run_device_noalloc on fresh buffers."""
+    art = hip.build(km)
+    ref_bufs = _device_bufs(km, host)
+    art.run_device(ref_bufs)
+    na_bufs = _device_bufs(km, host)
+    art.run_device_noalloc(na_bufs)
+    outs = km.output_ids()
+    return art, {i: ref_bufs[i].to_numpy() for i in outs}, {i: na_bufs[i].to_numpy() for i in outs}
+
+
+def test_scratch_array_size(hip):
+    assert backend.lib().mlkhip_noalloc_scratch_bytes() == 32 << 20
+
+
+@pytest.mark.parametrize("m,k", [(256, 512), (64, 256)])
+def test_noalloc_materialized_temps(hip, m, k):
+    # The generic loop-nest path materializes the softmax temps (row max,
+    # exponentials, sums); the smaller second case reuses the array, whose
+    # temps must be cleared again.
+    km = fx.softmax_rowmax_reader_module(m, k)
+    x = inputs.config_inputs("c2", {"m": m, "k": k})["x"]
+    art, ref, got = _both(hip, km, {0: x})
+    assert art.class_name.startswith("loop-nest")
+    for i in ref:
+        assert np.array_equal(ref[i].view(np.uint32), got[i].view(np.uint32)), (m, k, i)
+    say(f"materialized temps {m}x{k} ({art.class_name}): bit-identical to run_device")
+
+
+@pytest.mark.parametrize("b,s", [(2, 512), (1, 256)])
+def test_noalloc_score_softmax_statistics(hip, b, s):
+    km = fx.score_softmax_module(b, s, 128)
+    d = inputs.config_inputs("c5", {"batch": b, "seq": s, "dim": 128})
+    art, ref, got = _both(hip, km, {0: d["Q"], 1: d["K"], 2: d["bias"]})
+    assert art.class_name == "score-softmax"
+    for i in ref:
+        assert np.array_equal(ref[i].view(np.uint32), got[i].view(np.uint32)), (b, s, i)
+    say(f"score-softmax {b}x{s}: bit-identical to run_device")
+
+
+@pytest.mark.parametrize("m,k,n", [(256, 64, 256), (128, 32, 128)])
+def test_noalloc_matmul_call(hip, m, k, n):
+    km = fx.config4_module(m, k, n, "f32", tier=1)
+    d = inputs.config_inputs("c4a", {"m": m, "k": k, "n": n})
+    c0 = inputs.uniform(9, m * n, -1, 1)
+    art, ref, got = _both(hip, km, {0: d["A"], 1: d["B"], 2: c0})
+    for i in ref:
+        r = max_rel(got[i].astype(np.float64), ref[i].astype(np.float64))
+        assert r <= 1e-5 * math.sqrt(k), (m, k, n, r)
+    say(f"Call(MatMul) {m}x{k}x{n}: within {1e-5 * math.sqrt(k):g} of run_device")
+
+
+def test_noalloc_refusals(hip):
+    # More scratch than the array holds: refused before anything runs.
+    km = fx.softmax_rowmax_reader_module(4096, 1024)
+    art = hip.build(km)
+    x = np.zeros(4096 * 1024)
+    bufs = _device_bufs(km, {0: x})
+    with pytest.raises(backend.MlkHipError) as e:
+        art.run_device_noalloc(bufs)
+    assert e.value.code == backend.REFUSED and "device scratch" in e.value.message
+    # A loop nest whose bounds checks report through a host read-back.
+    import test_nest as tn
+    km = tn.dynamic_end_module()
+    art = hip.build(km)
+    bufs = _device_bufs(km, {0: np.arange(8.0)})
+    with pytest.raises(backend.MlkHipError) as e:
+        art.run_device_noalloc(bufs, elements=7)
+    assert e.value.code == backend.REFUSED and "read-back" in e.value.message
+    say("refusals: oversized scratch, checked loop nest")
