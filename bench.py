@@ -29,6 +29,17 @@ PEAK_F32_TFLOPS = 157.3        # FP32 matrix
 PROFILE_PMC = os.path.join(ROOT, "profiles", "softmax_c2_8192x4096_pmc.txt")
 
 
+def _cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), or the machine type."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
 def _stats(ms: np.ndarray) -> dict:
     return {"median_ms": float(np.median(ms)), "mean_ms": float(ms.mean()), "min_ms": float(ms.min())}
 
@@ -114,7 +125,8 @@ def bench_config(be, name: str, steps: int, warmup: int) -> dict:
     st = _stats(art.time_device(bufs, reps=steps, warmup=1))
     scale = 1e9 if unit == "GB/s" else 1e12
     achieved = work / (span_ms * 1e-3) / scale
-    return {"workload": wl, "class": art.class_name, "policy": art.policy, "unit": unit,
+    kernels = [art.step_kernel_name(i) or art.class_name.split("+")[i] for i in range(art.num_steps())]
+    return {"workload": wl, "class": art.class_name, "policy": art.policy, "kernels": kernels, "unit": unit,
             "bound": bound, "algorithmic_work": work, "achieved": round(achieved, 2),
             "peak": peak, "frac": round(achieved / peak, 4), "kernel_ms": round(span_ms, 5),
             "per_launch_event": {k: round(v, 5) for k, v in st.items()}}
@@ -143,7 +155,7 @@ def cpu_baseline_softmax() -> dict:
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"oracle Call(Softmax) f64, {rows}x{k} rows of the config-2 input, "
                       f"median of {len(reps)} reps ({med * 1e3:.1f} ms), bytes counted as f32 read+write",
-            "host": platform.processor() or platform.machine(), "nproc": os.cpu_count()}
+            "host": _cpu_model(), "nproc": os.cpu_count()}
 
 
 def _time_cpu(fn, budget_s: float = 3.0, max_reps: int = 10):
@@ -168,7 +180,7 @@ def cpu_baseline_config(name: str) -> dict:
     from mlk2_amd import inputs
     nproc = os.cpu_count() or 1
     default_threads = min(nproc, 4)
-    out = {"kind": "port", "nproc": nproc}
+    out = {"kind": "port", "nproc": nproc, "host": _cpu_model()}
 
     def run(km, ins, outs, threads):
         text = km.to_json()
@@ -304,7 +316,10 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
                      "traffic": _pmc_traffic(), "kernel_ms": round(kernel_ms, 5),
-                     "algorithmic_bytes": bytes_alg},
+                     "algorithmic_bytes": bytes_alg,
+                     "traffic_source": "profiles/softmax_c2_8192x4096_pmc.txt (rocprofv3 FETCH_SIZE and "
+                                       "WRITE_SIZE runs of this workload, copy-calibrated); not measured "
+                                       "in this run"},
         "cpu_baseline": None if args.no_cpu else cpu_baseline_softmax(),
         "configs": configs,
     }
