@@ -342,11 +342,11 @@ std::string launchCoverage(const KernelModule& km, const Step& st, int64_t eleme
             // Output scores; the two-pass form (dim 128, seq % 256 == 0)
             // gives each workgroup of a pass 128 rows x half the keys.
             instances = st.batch * st.seq * st.seq;
-            const bool twoPass = st.dim == 128 && st.seq % 256 == 0;
-            workgroups = twoPass ? st.batch * (st.seq / 128) * 2 : st.batch * ((st.seq + 31) / 32);
-            perGroup = twoPass ? 64 * st.seq : 32 * st.seq;
+            const bool twoPass = st.dim == 128 && st.seq % 256 == 0 && st.seq <= 8192 && st.variant != 1;
+            workgroups = twoPass ? st.batch * (st.seq / 128) * 2 : st.batch * ((st.seq + 63) / 64) * ((st.seq + 127) / 128);
+            perGroup = twoPass ? 64 * st.seq : 64 * 128;
             covered = workgroups * perGroup >= instances;
-            form = twoPass ? "128-row blocks x key halves, per pass" : "32-row blocks";
+            form = twoPass ? "128-row blocks x key halves, per pass" : "64 x 128 score tiles, then row softmax";
             break;
         }
         case StepKind::Fail:
@@ -373,12 +373,11 @@ std::vector<int> variantSpace(const KernelModule& km, const Step& st) {
             }
             return {};
         case StepKind::ScoreSoftmax:
+            // 0: two-pass query-stationary (the default); 1: scores, then the
+            // softmax kernel over S.
             if (dt(st.q) == Dtype::F16 && dt(st.kk) == Dtype::F16 && dt(st.bias) == Dtype::F32 &&
-                dt(st.s) == Dtype::F32 && st.dim == 128 && st.seq % 256 == 0) {
-                std::vector<int> v{0, 3};
-                if (st.seq <= 2048) v.push_back(2);
-                v.push_back(1);
-                return v;
+                dt(st.s) == Dtype::F32 && st.dim == 128 && st.seq % 256 == 0 && st.seq <= 8192) {
+                return {0, 1};
             }
             return {};
         case StepKind::Nest:

@@ -565,3 +565,34 @@ def test_f64_results_stored_to_f16_round_once(hip):
     km.add_node(KernelNode(op="call", math="reduce_sum", a=x, out=y))
     got = hip.build(km).run({0: v})[1]
     assert np.array_equal(got, want), np.c_[v, got, want][got != want]
+
+
+@pytest.mark.parametrize("s", [512, 384])
+def test_c5_masked_keys_every_form(hip, s):
+    # An attention-style mask: bias = -inf over whole key ranges (a full
+    # 64/128-key panel and a ragged span). Those scores contribute exp(-inf)
+    # = 0 and the other keys' softmax is unchanged; with every key masked
+    # each row is NaN, as the reference's exp(-inf - -inf) makes it. Every
+    # declared launch form is held to the oracle, NaN positions included.
+    b, dm = 2, 128
+    d = inputs.config_inputs("c5", {"batch": b, "seq": s, "dim": dm})
+    km = fx.score_softmax_module(b, s, dm)
+    art = hip.build(km)
+    forms = art.step_variants(0) or [-1]
+    for label, bias in (("masked spans", d["bias"].astype(np.float32).copy()), ("all masked", None)):
+        if bias is None:
+            bias = np.full(s, -np.inf, dtype=np.float32)
+        else:
+            bias[0:128] = -np.inf
+            bias[200:230] = -np.inf
+        arrays = {0: d["Q"], 1: d["K"], 2: bias}
+        ref = oracle.run(km, arrays, hw_threads=8)[3]
+        for form in forms:
+            art.set_step_variant(0, form)
+            got = art.run(arrays)[3]
+            assert np.array_equal(np.isnan(got), np.isnan(ref)), (s, label, form)
+            fin = np.isfinite(ref)
+            e = max_rel(got[fin], ref[fin]) if fin.any() else 0.0
+            say(f"c5 {label} seq={s} form {form}: NaN positions match, max_rel={e:.3e}")
+            assert e <= 1e-2, (s, label, form, e)
+    art.set_step_variant(0, -1)
