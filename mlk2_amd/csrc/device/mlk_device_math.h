@@ -28,13 +28,23 @@ constexpr double kC[6] = {-1.13585365213876817300e-11, 2.08757530072652689750e-9
                           -2.75573142103085808917e-7, 2.48015872890001867312e-5,
                           -1.38888888888783992457e-3, 4.16666666666666435770e-2};
 
+/// fmod(n, 4) taken into [0, 4) for the integral n of the reduction
+/// (math_families.h:71-72): n - 4 * floor(n / 4). Every step is exact for any
+/// finite n (the scalings are by powers of two, and the difference is an
+/// integer in [0, 3], or 0 once ulp(n) >= 8), so it gives the reference's
+/// quadrant with four f64 operations and no fmod.
 __device__ __forceinline__ int quadrantOf(double n) {
-    if (__builtin_fabs(n) < 4503599627370496.0) {  // |n| < 2^52: exact in int64
-        return static_cast<int>(static_cast<long long>(n) & 3LL);
-    }
-    int q = static_cast<int>(fmod(n, 4.0));
-    return q < 0 ? q + 4 : q;
+    const double f = floor(n * 0.25);
+    return static_cast<int>(n - 4.0 * f);
 }
+
+// Residual polynomials for results rounded to f32, on |r| <= pi/4:
+// sin r ~ r + r^3 (s0 + s1 r^2 + s2 r^4), cos r ~ 1 - r^2/2 + r^4 (c0 + c1 r^2
+// + c2 r^4). Fitted by iteratively reweighted least squares on 2e5 points
+// (converging to the minimax): relative error 3.9e-9 (sine) and 1.2e-10
+// (cosine) before the coefficients' rounding to f32.
+constexpr float kSinF32[3] = {-0x1.555546p-3f, 0x1.11073cp-7f, -0x1.994446p-13f};
+constexpr float kCosF32[3] = {0x1.55554ap-5f, -0x1.6c0c34p-10f, 0x1.99ebf6p-16f};
 
 }  // namespace mlk
 
@@ -58,32 +68,76 @@ __device__ __forceinline__ double mlk_p7_sin(double x) {
     return (q & 2) ? -v : v;
 }
 
+#ifndef MLK_HOST_SHIM
+/// The hardware f32 exp2 (v_exp_f32, 1 ULP on the finite range).
+__device__ __forceinline__ float mlk_hw_exp2f(float x) { return __builtin_amdgcn_exp2f(x); }
+/// Bitwise select: bits of a where m is set, of b elsewhere (v_bitop3_b32,
+/// truth table 0xCA).
+__device__ __forceinline__ unsigned mlk_bitsel(unsigned m, unsigned a, unsigned b) {
+    return __builtin_amdgcn_bitop3_b32(m, a, b, 0xCA);
+}
+/// The wave's lanes where a >= b or either is NaN (one compare into a
+/// scalar lane mask; LLVM's FCMP_UGE).
+__device__ __forceinline__ unsigned long long mlk_lanes_uge(double a, double b) {
+    return __builtin_amdgcn_fcmp(a, b, 11);
+}
+#endif
+
 /// poly7 sin for a value rounded to f32 right after (the planner uses it
-/// only when sin is the chain's last op and the output is f32). The
-/// reduction r = (x - n*hi) - n*lo stays in f64; the residual polynomials run
-/// in f32 on r rounded to f32 (|r| <= pi/4: ~1 f32 ULP, plus r's own 0.5 ULP
-/// relative rounding). n = floor(x*2/pi + 0.5) can differ from the
-/// reference's floor(x/(pi/2) + 0.5) only within an ULP of an odd multiple of
-/// pi/4, where both reductions are valid and agree to polynomial accuracy.
-__device__ __forceinline__ double mlk_p7_sin_f32out(double x) {
+/// only when sin is the chain's last op, the output is f32 and stores are
+/// plain).
+///
+/// The reduction is the reference's r = (x - n*hi) - n*lo in f64, with n =
+/// floor(y), y = x*(2/pi) + 0.5 in one fused operation where the reference
+/// divides by pi/2. For |y| < 2^20 that y is within 5 ULP (< 2^-30) of the
+/// reference's, so the two n differ only where x is that close to an odd
+/// multiple of pi/4; there both reductions are valid (|r| ~ pi/4, each
+/// exact to 2^-32) and give the same value to 1e-9 relative. Elsewhere n,
+/// r and the quadrant are the reference's bits, so r near a zero of the sine
+/// is the reference's r. For |y| >= 2^20, NaN and infinities the function
+/// adds the lane to the wave mask `slow` and the caller recomputes the
+/// element with mlk_p7_sin. The degree-7 sine and degree-8 cosine residual
+/// polynomials (kSinF32, kCosF32) run in f32 on r rounded to f32: within 2
+/// f32 ULP of the f64 form rounded to f32 (CPU sweeps of 3.2e7 arguments,
+/// and of 3e6 within 4 ULP of multiples of pi/4, find no larger). The exact
+/// form is not inlined here, so the caller's unrolled hot loop carries no
+/// f64 division or full polynomial.
+__device__ __forceinline__ float mlk_p7_sin_f32out(double x, unsigned long long& slow) {
     using namespace mlk;
-    const double n = floor(x * kTwoOverPi + 0.5);
+    const double y = __builtin_fma(x, kTwoOverPi, 0.5);
+    const double n = floor(y);
     const double r = (x - n * kPio2Hi) - n * kPio2Lo;
-    const int q = quadrantOf(n);
+    slow |= mlk_lanes_uge(__builtin_fabs(y), 0x1p20);
+    const int q = static_cast<int>(n);  // |n| <= 2^20 wherever the result is used
     const float rf = static_cast<float>(r);
     const float r2 = rf * rf;
-    float ps = static_cast<float>(kS[0]);
-    float pc = static_cast<float>(kC[0]);
-#pragma unroll
-    for (int i = 1; i < 6; ++i) {
-        ps = __builtin_fmaf(ps, r2, static_cast<float>(kS[i]));
-        pc = __builtin_fmaf(pc, r2, static_cast<float>(kC[i]));
-    }
+    const float ps = __builtin_fmaf(__builtin_fmaf(kSinF32[2], r2, kSinF32[1]), r2, kSinF32[0]);
+    const float pc = __builtin_fmaf(__builtin_fmaf(kCosF32[2], r2, kCosF32[1]), r2, kCosF32[0]);
     const float s = __builtin_fmaf(rf * r2, ps, rf);
-    const float c = __builtin_fmaf(r2 * r2, pc, __builtin_fmaf(-0.5f, r2, 1.0f));
-    float v = (q & 1) ? c : s;
-    v = (q & 2) ? -v : v;
-    return r == r ? static_cast<double>(v) : r;  // NaN/inf arguments give NaN
+    const float c = __builtin_fmaf(r2, __builtin_fmaf(r2, pc, -0.5f), 1.0f);  // 1 - r2/2 + r2^2 pc
+    // Odd quadrants take the cosine (an all-ones mask from bit 0 selects it
+    // bitwise), quadrants 2 and 3 flip the sign (bit 1 moved to bit 31).
+    const unsigned odd = static_cast<unsigned>(static_cast<int>(static_cast<unsigned>(q) << 31) >> 31);
+    const unsigned v = mlk_bitsel(odd, __float_as_uint(c), __float_as_uint(s));
+    return __uint_as_float(v ^ ((static_cast<unsigned>(q) << 30) & 0x80000000u));
+}
+
+
+/// exp for a chain whose result reaches an f32 output only through products
+/// and quotients (which carry a relative error through unchanged):
+/// exp(u) = 2^k * 2^f with t = u*log2(e) in f64, k = rint(t), f = t - k
+/// (exact, |f| <= 1/2) and 2^f from the hardware's f32 exp2 on f rounded to
+/// f32 (1 f32 ULP, plus 2e-8 from the rounding of f): about 1.4e-7 relative,
+/// so the f32 result is within 2 ULP of the reference's f64 exp rounded to
+/// f32. |t| >= 1000 (near overflow and underflow), NaN and infinities add
+/// the lane to the wave mask `slow`: the caller recomputes that element with
+/// the f64 exp.
+__device__ __forceinline__ double mlk_exp_f32acc(double u, unsigned long long& slow) {
+    const double t = u * 1.4426950408889634074;
+    slow |= mlk_lanes_uge(__builtin_fabs(t), 1000.0);
+    const double k = __builtin_rint(t);
+    const float e = mlk_hw_exp2f(static_cast<float>(t - k));
+    return __builtin_ldexp(static_cast<double>(e), static_cast<int>(k));
 }
 
 struct mlk_scalars {

@@ -43,6 +43,7 @@ std::string elementwiseSource(const KernelModule& km, const Step& st, std::strin
     std::string p;
     p += "#define MLK_GENERATED 1\n";
     p += "#define MLK_NIN " + std::to_string(nin) + "\n";
+    p += "constexpr long long kHostSegment = " + std::to_string(kElementwiseSegment) + ";\n";
     p += "constexpr int kRank = " + std::to_string(st.rank) + ";\n";
     p += "constexpr bool kDynamicExtent = " + std::string(st.dynamicExtent ? "true" : "false") + ";\n";
     int64_t ext[4] = {st.extent[0], st.extent[1], st.extent[2], st.extent[3]};
@@ -71,18 +72,20 @@ std::string elementwiseSource(const KernelModule& km, const Step& st, std::strin
     p += "constexpr long long kOutC[4] = " + list(oc, 4) + ";\n";
     p += "constexpr int kAccum = " +
          std::to_string(st.accum == AccumMode::Add ? 1 : (st.accum == AccumMode::Max ? 2 : 0)) + ";\n";
-    p += "#define MLK_CHAIN_BODY \\\n";
-    // One statement per line of the body, joined with line continuations.
-    std::string body = st.chainBody;
-    std::string joined;
-    size_t start = 0;
-    while (start < body.size()) {
-        size_t nl = body.find('\n', start);
-        if (nl == std::string::npos) nl = body.size();
-        joined += body.substr(start, nl - start) + " \\\n";
-        start = nl + 1;
-    }
-    p += joined + "\n";
+    // One statement per line of a body, joined with line continuations.
+    auto macro = [](const std::string& name, const std::string& body) {
+        std::string joined = "#define " + name + " \\\n";
+        size_t start = 0;
+        while (start < body.size()) {
+            size_t nl = body.find('\n', start);
+            if (nl == std::string::npos) nl = body.size();
+            joined += body.substr(start, nl - start) + " \\\n";
+            start = nl + 1;
+        }
+        return joined + "\n";
+    };
+    p += macro("MLK_CHAIN_BODY", st.chainBody);
+    if (!st.chainExact.empty()) p += macro("MLK_CHAIN_EXACT", st.chainExact);
     const std::string text = p + kDeviceMathHeader + kElementwiseTemplate;
     const std::string name = elementwiseKernelName(text);
     if (kernelName != nullptr) *kernelName = name;

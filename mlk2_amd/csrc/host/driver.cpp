@@ -325,8 +325,9 @@ int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* 
                 int64_t rows = 1;
                 for (int d = 0; d < st.rank - 1; ++d) rows *= st.extent[d];
                 const int64_t w = st.rank == 1 ? ext0 : st.extent[st.rank - 1];
-                // One wave per 1024-element row segment (the template's kSeg).
-                const int64_t threads = rows * ((w + 1023) / 1024) * 64;
+                // One wave per row segment (the template's kSeg).
+                const int64_t threads =
+                    rows * ((w + kElementwiseSegment - 1) / kElementwiseSegment) * 64;
                 rc = mlkd_jit_launch_elementwise(st.fn, gridFor(threads), in, out, &sc, ext0, stream);
                 break;
             }

@@ -79,6 +79,14 @@ bool sameMap(const StreamRef& a, const StreamRef& b, int rank) {
     return true;
 }
 
+/// Significant bits of a stream's values: 24 (f32), 11 (f16), 99 for f64
+/// and unbound ids (no exact-product claim).
+int streamBits(const KernelModule& km, int64_t bid) {
+    if (bid < 0 || static_cast<size_t>(bid) >= km.buffers.size()) return 99;
+    const Dtype d = km.buffers[static_cast<size_t>(bid)].dtype;
+    return d == Dtype::F32 ? 24 : (d == Dtype::F16 ? 11 : 99);
+}
+
 /// Adapts a stream-index lookup to chainCode's operand callback.
 template <class StreamOf>
 std::function<std::string(const KernelOperand&)> streamCode(StreamOf& streamOf) {
@@ -98,15 +106,91 @@ std::string literal(double v) {
     return std::string("(") + buf + ")";
 }
 
+namespace {
+
+/// Significant bits of an f64 constant whose products with f32/f16 values
+/// stay normal and finite (|v| in [2^-200, 2^200], or zero); 99 otherwise.
+int constBits(double v) {
+    if (v == 0.0) return 0;
+    if (!std::isfinite(v) || std::fabs(v) > 0x1p200 || std::fabs(v) < 0x1p-200) return 99;
+    int e = 0;
+    const double m = std::frexp(std::fabs(v), &e);
+    uint64_t i = static_cast<uint64_t>(std::ldexp(m, 53));
+    int bits = 53;
+    while ((i & 1u) == 0) {
+        i >>= 1;
+        --bits;
+    }
+    return bits;
+}
+
+}  // namespace
+
 /// Builds the f64 chain body; elemCode(o) returns the device expression of an
 /// element operand (empty when it cannot be realized). The reference
 /// evaluation (kernel_buffers.cpp:106-178): unary ops ignore b, Temp reads
 /// earlier results, ScalarParam past the table reads 0.0.
+///
+/// A product used only by one sum, whose operands' significant bits
+/// (elemBits: 24 for f32 streams, 11 for f16) add up to 53 or fewer, is exact
+/// in f64; the sum is then written as one fused multiply-add, which rounds
+/// once exactly as the reference's separate product and sum do.
 Result<std::string> chainCode(const std::vector<KernelExpr>& exprs, bool poly7, bool f32Out,
                               const std::function<std::string(const KernelOperand&)>& elemCode,
-                              const std::string& sink) {
+                              const std::string& sink,
+                              const std::function<int(const KernelOperand&)>& elemBits) {
     if (exprs.empty() || exprs.size() > 64) {
         return err(ErrorCode::UnsupportedCapability, "chain length outside 1..64");
+    }
+    // exp with f32 accuracy (mlk_exp_f32acc) where the result is rounded to
+    // f32 and the exp's value reaches it only as a factor: every use of it,
+    // and of each temp on the way, is an operand of Mul, Div or Neg, which
+    // carry a relative error through unchanged. One such exp per chain, used
+    // once, keeps the f32 result within 3 ULP of the reference's.
+    const size_t last = exprs.size() - 1;
+    std::vector<int> uses(exprs.size(), 0);
+    std::vector<std::vector<size_t>> users(exprs.size());
+    for (size_t j = 0; j < exprs.size(); ++j) {
+        const KernelExpr& e = exprs[j];
+        for (const KernelOperand* o : {&e.a, &e.b}) {
+            if (o == &e.b && isUnaryMath(e.op)) continue;
+            if (o->kind == K::Temp && o->index >= 0 && static_cast<size_t>(o->index) < j) {
+                ++uses[static_cast<size_t>(o->index)];
+                users[static_cast<size_t>(o->index)].push_back(j);
+            }
+        }
+    }
+    std::vector<char> factorPath(exprs.size(), 0);
+    factorPath[last] = 1;
+    for (size_t k = last; k-- > 0;) {
+        bool ok = !users[k].empty();
+        for (size_t j : users[k]) {
+            const MathOp op = exprs[j].op;
+            ok = ok && factorPath[j] && (op == MathOp::Mul || op == MathOp::Div || op == MathOp::Neg);
+        }
+        factorPath[k] = ok ? 1 : 0;
+    }
+    auto operandBits = [&](const KernelOperand& o) -> int {
+        if (o.kind == K::Const) return constBits(o.constValue);
+        if ((o.kind == K::ElemA || o.kind == K::ElemB || o.kind == K::ElemIdx) && elemBits) return elemBits(o);
+        return 99;
+    };
+    std::vector<char> exactMul(exprs.size(), 0);
+    for (size_t k = 0; k < exprs.size(); ++k) {
+        const KernelExpr& e = exprs[k];
+        exactMul[k] = e.op == MathOp::Mul && uses[k] == 1 && operandBits(e.a) + operandBits(e.b) <= 53;
+    }
+    auto exactTemp = [&](const KernelOperand& o, size_t self) {
+        return o.kind == K::Temp && o.index >= 0 && static_cast<size_t>(o.index) < self &&
+               exactMul[static_cast<size_t>(o.index)];
+    };
+    int fastExp = -1;
+    if (f32Out) {
+        for (size_t k = 0; k < exprs.size() && fastExp < 0; ++k) {
+            if (exprs[k].op == MathOp::Exp && factorPath[k] && (k == last || uses[k] == 1)) {
+                fastExp = static_cast<int>(k);
+            }
+        }
     }
     std::string body;
     auto operand = [&](const KernelOperand& o, size_t self, std::string& out) -> bool {
@@ -145,20 +229,36 @@ Result<std::string> chainCode(const std::vector<KernelExpr>& exprs, bool poly7, 
         body += "    (void)b" + id + ";\n";
         const std::string A = "a" + id, B = "b" + id;
         std::string v;
-        const bool last = k + 1 == exprs.size();
+        const bool isLast = k == last;
+        // Fused forms of a sum with an exact product t = p*q (its line stays
+        // and is dropped as dead code): t + X, X + t, t - X, X - t.
+        const bool fuseA = (e.op == MathOp::Add || e.op == MathOp::Sub) && exactTemp(e.a, k);
+        const bool fuseB = !fuseA && (e.op == MathOp::Add || e.op == MathOp::Sub) && exactTemp(e.b, k);
+        const std::string P = fuseA ? "a" + std::to_string(e.a.index) : "a" + std::to_string(e.b.index);
+        const std::string Q = fuseA ? "b" + std::to_string(e.a.index) : "b" + std::to_string(e.b.index);
         switch (e.op) {
-            case MathOp::Add: v = A + " + " + B; break;
-            case MathOp::Sub: v = A + " - " + B; break;
+            case MathOp::Add:
+                if (fuseA) v = "__builtin_fma(" + P + ", " + Q + ", " + B + ")";
+                else if (fuseB) v = "__builtin_fma(" + P + ", " + Q + ", " + A + ")";
+                else v = A + " + " + B;
+                break;
+            case MathOp::Sub:
+                if (fuseA) v = "__builtin_fma(" + P + ", " + Q + ", -" + B + ")";
+                else if (fuseB) v = "__builtin_fma(-" + P + ", " + Q + ", " + A + ")";
+                else v = A + " - " + B;
+                break;
             case MathOp::Mul: v = A + " * " + B; break;
             case MathOp::Div: v = "(" + B + " != 0.0) ? " + A + " / " + B + " : 0.0"; break;
             case MathOp::Neg: v = "-" + A; break;
             case MathOp::Pow:
                 v = "(" + A + " == 2.0 && " + B + " == 2.0) ? " + A + " * " + A + " : pow(" + A + ", " + B + ")";
                 break;
-            case MathOp::Exp: v = "exp(" + A + ")"; break;
+            case MathOp::Exp:
+                v = static_cast<int>(k) == fastExp ? "mlk_exp_f32acc(" + A + ", slow)" : "exp(" + A + ")";
+                break;
             case MathOp::Log: v = "(" + A + " > 0.0) ? log(" + A + ") : 0.0"; break;
             case MathOp::Sin:
-                v = poly7 ? ((last && f32Out) ? "mlk_p7_sin_f32out(" + A + ")" : "mlk_p7_sin(" + A + ")")
+                v = poly7 ? ((isLast && f32Out) ? "mlk_p7_sin_f32out(" + A + ", slow)" : "mlk_p7_sin(" + A + ")")
                           : "sin(" + A + ")";
                 break;
             case MathOp::Cos: v = "cos(" + A + ")"; break;
@@ -325,8 +425,14 @@ Result<Step> elementwiseNest(const KernelModule& km, const NestInfo& ni) {
     // reference's f16 value bit for bit, where a few f32 ULP of error would
     // move about one value in a thousand to the neighbouring f16.
     const bool f32Out = od == Dtype::F32 && so.accum == AccumMode::None;
-    auto body = chainCode(cp.exprs, cp.family == "poly7", f32Out, streamCode(streamOf), "return ");
+    auto bits = [&km](const KernelOperand& o) {
+        return o.kind == K::ElemIdx ? streamBits(km, o.index) : 99;
+    };
+    auto body = chainCode(cp.exprs, cp.family == "poly7", f32Out, streamCode(streamOf), "return ", bits);
     if (!body.has_value()) return err(body.error().code, body.error().message);
+    auto exact = chainCode(cp.exprs, cp.family == "poly7", false, streamCode(streamOf), "return ", bits);
+    if (!exact.has_value()) return err(exact.error().code, exact.error().message);
+    if (*exact != *body) st.chainExact = *exact;
     if (bad) return err(ErrorCode::UnsupportedCapability, "more than 4 distinct element streams");
     for (const StreamRef& s : ins) {
         MLK_TRYV(checkInBounds(km, s, st.rank, st.extent, "operand"));
@@ -415,9 +521,16 @@ Result<std::vector<Step>> tier1Loop(const KernelModule& km, const KernelNode& lo
         };
         const Dtype od = km.buffers[so.bufferOut].dtype;
         // Split-precision sin for f32 outputs only, as in the n-D path.
-        auto body = chainCode(exprs, c.family == "poly7", od == Dtype::F32, streamCode(streamOf), "return ");
+        auto bits = [&](const KernelOperand& o) {
+            return o.kind == K::ElemA ? streamBits(km, c.bufferA == kInvalidId ? -1 : static_cast<int64_t>(c.bufferA))
+                                      : (o.kind == K::ElemB ? streamBits(km, c.bufferB == kInvalidId ? -1 : static_cast<int64_t>(c.bufferB)) : 99);
+        };
+        auto body = chainCode(exprs, c.family == "poly7", od == Dtype::F32, streamCode(streamOf), "return ", bits);
         if (!body.has_value()) return err(body.error().code, body.error().message);
+        auto exact = chainCode(exprs, c.family == "poly7", false, streamCode(streamOf), "return ", bits);
+        if (!exact.has_value()) return err(exact.error().code, exact.error().message);
         st.chainBody = *body;
+        if (*exact != *body) st.chainExact = *exact;
         st.out = ref(so.bufferOut);
         if (!st.dynamicExtent) {
             if (st.extent[0] == 0) continue;
@@ -868,6 +981,7 @@ std::string policyFor(const KernelModule& km, const std::vector<Step>& steps) {
                 break;
             case StepKind::Elementwise:
                 if (st.chainBody.find("mlk_p7_sin_f32out") != std::string::npos) p7out = true;
+                if (st.chainBody.find("mlk_exp_f32acc") != std::string::npos) transcend = true;
                 for (const char* f : {"exp(", "log(", "sin(", "cos(", "tan(", "tanh(", "erf(", "pow("}) {
                     if (st.chainBody.find(std::string(" ") + f) != std::string::npos ||
                         st.chainBody.find(std::string("(") + f) != std::string::npos) {

@@ -22,6 +22,10 @@ struct StreamRef {
     int64_t coeff[4]{0, 0, 0, 0};
 };
 
+/// Elements of one row segment of the elementwise template (one wave: 64
+/// lanes x 8 elements); the grid has one wave per segment.
+constexpr int64_t kElementwiseSegment = 512;
+
 struct Step {
     StepKind kind{StepKind::Fail};
     std::string what;                 // class name for reports
@@ -35,6 +39,10 @@ struct Step {
     StreamRef out;
     AccumMode accum{AccumMode::None};
     std::string chainBody;
+    /// The chain in the reference's f64 forms when chainBody uses a form that
+    /// can decline an element (split-precision sin, f32-accurate exp); empty
+    /// otherwise.
+    std::string chainExact;
     std::string source;
     std::string kernelName;           // hipRTC symbol (elementwise and nest steps)
     void* fn{nullptr};
@@ -132,7 +140,8 @@ std::string literal(double v);
 /// the result is written as `<sink>tN;`.
 Result<std::string> chainCode(const std::vector<KernelExpr>& exprs, bool poly7, bool f32Out,
                               const std::function<std::string(const KernelOperand&)>& elemCode,
-                              const std::string& sink);
+                              const std::string& sink,
+                              const std::function<int(const KernelOperand&)>& elemBits = {});
 
 /// Buffer element count as the executors size it (dims product, else
 /// `elements`; dynamic buffers take the run's element count).

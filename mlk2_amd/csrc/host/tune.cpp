@@ -310,10 +310,11 @@ std::string launchCoverage(const KernelModule& km, const Step& st, int64_t eleme
             int64_t rows = 1;
             for (int d = 0; d + 1 < st.rank; ++d) rows *= st.extent[d];
             instances = rows * std::max<int64_t>(w, 0);
-            const int64_t segs = rows * ((std::max<int64_t>(w, 0) + 1023) / 1024);
+            const int64_t segs =
+                rows * ((std::max<int64_t>(w, 0) + kElementwiseSegment - 1) / kElementwiseSegment);
             workgroups = std::min<int64_t>(std::max<int64_t>((segs * 64 + 255) / 256, 1), 16384);
-            perGroup = 4 * 1024;
-            form = "grid-stride 1024-element segments, one per wave";
+            perGroup = 4 * kElementwiseSegment;
+            form = "grid-stride 512-element segments, one per wave";
             break;
         }
         case StepKind::Nest:

@@ -24,6 +24,13 @@ struct mlk_dim3 {
 };
 extern mlk_dim3 blockIdx, threadIdx, gridDim, blockDim;
 
+/// The hardware f32 exp2 (v_exp_f32, 1 ULP) stands as libm's exp2f.
+#define MLK_HOST_SHIM 1
+inline float mlk_hw_exp2f(float x) { return exp2f(x); }
+inline unsigned mlk_bitsel(unsigned m, unsigned a, unsigned b) { return (a & m) | (b & ~m); }
+/// One thread at a time: lane masks of a wave of one.
+inline unsigned long long mlk_lanes_uge(double a, double b) { return !(a < b) ? 1ull : 0ull; }
+
 inline float __uint_as_float(unsigned u) {
     float f;
     memcpy(&f, &u, sizeof(f));

@@ -1,0 +1,141 @@
+"""Chain forms whose operations differ from the reference's list but whose
+results do not, run on the device against the oracle.
+
+* A sum of an exact product (two f32 or f16 values, or one and a short
+  constant) is one fused multiply-add: bit-exact with the walker's separate
+  product and sum (kernel_buffers.cpp:130-160 evaluates each in f64).
+* exp as a factor of an f32 result takes the f32-accurate form: within 1e-6
+  relative. Arguments outside its range (|u*log2(e)| >= 1000, NaN, +-inf) make
+  their wave redo its segment with the f64 exp; the inputs put such arguments
+  in some waves and not in others.
+* The split-precision poly7 sine (math_families.h:81-90) with arguments whose
+  reduction it declines (|x*2/pi| >= 2^20, NaN, inf) beside ones it takes:
+  within 4 f32 ULP, the declined ones from the exact f64 form.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from mlk2_amd import fixtures as fx
+from mlk2_amd import inputs
+from mlk2_amd.parity import max_rel, ulp_distance_f32
+from test_host import EXP_CASES, FUSE_CASES
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(f"[fast-forms] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def finite_max_rel(got, ref):
+    """Max relative error of an f32 output over the finite references, after
+    checking that NaNs and infinities sit where the reference's do. The
+    walker holds f64 values; the reference's f32 buffer holds them rounded,
+    so a value past the f32 range is inf there too."""
+    got = np.asarray(got, dtype=np.float64)
+    with np.errstate(over="ignore"):
+        ref = np.asarray(ref, dtype=np.float64).astype(np.float32).astype(np.float64)
+    assert np.array_equal(np.isnan(got), np.isnan(ref)), "NaN positions differ"
+    inf = np.isinf(ref)
+    assert np.array_equal(got[inf], ref[inf]), "infinities differ"
+    fin = np.isfinite(ref)
+    return max_rel(got[fin], ref[fin])
+
+
+@pytest.mark.parametrize("name,chain,fused", FUSE_CASES, ids=[c[0] for c in FUSE_CASES])
+@pytest.mark.parametrize("dt_in", ["f32", "f16"])
+@pytest.mark.parametrize("lift", [False, True])
+def test_exact_product_sums_bit_exact(hip, name, chain, fused, dt_in, lift):
+    n = 70001                                    # ragged: a partial last segment
+    rng = np.random.default_rng(11)
+    np_dt = np.float32 if dt_in == "f32" else np.float16
+    a = rng.uniform(-3, 3, n).astype(np_dt).astype(np.float64)
+    b = rng.uniform(-3, 3, n).astype(np_dt).astype(np.float64)
+    a[:4] = [0.0, -0.0, np.inf, np.nan]
+    b[:4] = [-0.0, 0.0, 1.0, 2.0]
+    km = fx.lower_elementwise([("a", [n], dt_in), ("b", [n], dt_in)], chain, [n], out_dtype="f64")
+    if lift:
+        km = fx.lift_1d(km)
+    art = hip.build(km)
+    assert art.policy == "bitexact-rne-gfx950-v1"
+    got = art.run({0: a, 1: b})[2]
+    ref = oracle.run(km, {0: a, 1: b})[2]
+    # Bit-exact means equal bits except NaN payloads and signs (IEEE leaves
+    # those to the implementation; the reference's writer emits NaN as null).
+    same = (got.view(np.int64) == ref.view(np.int64)) | (np.isnan(got) & np.isnan(ref))
+    say(f"{name} {dt_in} lift={lift}: fused={fused}, {int((~same).sum())} bit differences")
+    assert same.all()
+
+
+def exp_arguments(n, rng):
+    """Mostly ordinary arguments; a few waves' worth around overflow,
+    underflow and the non-finite values."""
+    a = rng.uniform(-10, 10, n)
+    a[20000:20400] = rng.uniform(700, 720, 400)      # exp overflows past 709.78
+    a[30000:30400] = rng.uniform(-760, -690, 400)    # subnormal and zero results
+    a[40000:40010] = [np.nan, np.inf, -np.inf, 709.78, -708.4, -745.2, 0.0, -0.0, 693.0, -693.0]
+    return a.astype(np.float32).astype(np.float64)
+
+
+@pytest.mark.parametrize("name,chain,out_dt,fast_exp", [c for c in EXP_CASES if c[2] == "f32"],
+                         ids=[c[0] for c in EXP_CASES if c[2] == "f32"])
+@pytest.mark.parametrize("lift", [False, True])
+def test_f32_accurate_exp_against_the_walker(hip, name, chain, out_dt, fast_exp, lift):
+    n = 50000
+    rng = np.random.default_rng(12)
+    a = exp_arguments(n, rng)
+    b = rng.uniform(0.5, 2, n).astype(np.float32).astype(np.float64)
+    km = fx.lower_elementwise([("a", [n], "f32"), ("b", [n], "f32")], chain, [n], out_dtype="f32")
+    if lift:
+        km = fx.lift_1d(km)
+    art = hip.build(km)
+    got = art.run({0: a, 1: b})[2]
+    ref = oracle.run(km, {0: a, 1: b})[2]
+    err = finite_max_rel(got, ref)
+    say(f"{name} lift={lift}: f32-accurate exp={fast_exp}, max rel {err:.3g}")
+    assert err <= 1e-6
+
+
+def test_c3_chain_with_exact_pass_rows(hip):
+    rows, cols = 256, 1024
+    km = fx.config3_module(rows, cols, 2)
+    d = inputs.config_inputs("c3", {"rows": rows, "cols": cols})
+    x = d["x"].astype(np.float64)
+    x[5, :] = 1500.0                                  # exp(750 + b): overflow, the exact pass
+    x[9, 100:200] = -1600.0                           # exp(-800 + b): zero
+    x[77, 3] = np.nan
+    got = hip.build(km).run({0: x, 1: d["b"]})[2]
+    ref = oracle.run(km, {0: x, 1: d["b"]})[2]
+    err = finite_max_rel(got, ref)
+    say(f"c3 with exact-pass rows: max rel {err:.3g}")
+    assert err <= 1e-6
+
+
+@pytest.mark.parametrize("lift", [False, True])
+def test_c1_sine_with_declined_reductions(hip, lift):
+    n = 1 << 20
+    rng = np.random.default_rng(13)
+    x = rng.uniform(-4, 4, n)
+    x[100000:101000] = rng.uniform(-3000, 3000, 1000)    # |t| up to 9e6: y beyond 2^20
+    x[300000:300064] = rng.uniform(-1e4, 1e4, 64)
+    x[500000:500005] = [np.nan, np.inf, -np.inf, 1e19, -1e19]
+    x = x.astype(np.float32).astype(np.float64)
+    km = fx.config1_module(n=n)
+    if lift:
+        km = fx.lift_1d(km)
+    art = hip.build(km)
+    assert art.policy == "tol-4ulp-f32-gfx950-v1"
+    got = art.run({0: x})[1].astype(np.float32)
+    ref = oracle.run(km, {0: x}, hw_threads=4)[1]
+    d = ulp_distance_f32(got, ref)
+    with np.errstate(invalid="ignore", over="ignore"):
+        t = x * x + 3.0 * x
+        big = ~(np.abs(t * (2 / np.pi) + 0.5) < 2.0 ** 20)  # declined: |y| >= 2^20, NaN, inf
+    say(f"c1 lift={lift}: max ULP {d.max()}, over the declined arguments {d[big].max()}")
+    assert d.max() <= 4.0
+    # The declined arguments come from the exact f64 form.
+    assert d[big].max() == 0

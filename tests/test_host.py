@@ -16,7 +16,7 @@ import test_nest as tn
 import numpy as np
 
 from mlk2_amd.kernel_ir import (INVALID_ID, KernelBuffer, KernelExpr, KernelModule, KernelNode, const,
-                                elem_a, temp)
+                                elem_a, elem_b, temp)
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
@@ -220,6 +220,89 @@ def test_declared_variant_space(km, space):
 def test_variant_space_step_out_of_range():
     with pytest.raises(be.MlkHipError):
         be.plan_variants(fx.config2_module(64, 128, 2), 3)
+
+
+def chain_bodies(km):
+    """(fast body, exact body or "") of the instance's chain prelude."""
+    _, src = be.compile_check(km)
+    prelude = src.split("// Fused elementwise kernel template")[0]
+
+    def body(name):
+        if f"#define {name} " not in prelude:
+            return ""
+        return prelude.split(f"#define {name} ")[1].split("\n\n")[0]
+    return body("MLK_CHAIN_BODY"), body("MLK_CHAIN_EXACT")
+
+
+# Chains over two streams a, b: (name, chain, fused?) -- a sum of an exact
+# product becomes one fused multiply-add (the product of two f32 or f16
+# values, or of one and a short constant, is exact in f64).
+FUSE_CASES = [
+    ("t+X", [KernelExpr("mul", elem_a(), elem_b()), KernelExpr("add", temp(0), elem_b())], True),
+    ("X+t", [KernelExpr("mul", elem_a(), elem_b()), KernelExpr("add", elem_a(), temp(0))], True),
+    ("t-X", [KernelExpr("mul", elem_a(), elem_b()), KernelExpr("sub", temp(0), elem_a())], True),
+    ("X-t", [KernelExpr("mul", elem_a(), elem_b()), KernelExpr("sub", elem_b(), temp(0))], True),
+    ("c1-form", [KernelExpr("mul", elem_a(), elem_a()), KernelExpr("mul", const(3.0), elem_a()),
+                 KernelExpr("add", temp(0), temp(1))], True),
+    ("long-const", [KernelExpr("mul", const(0.1), elem_a()), KernelExpr("add", temp(0), elem_b())], False),
+    ("product-read-twice", [KernelExpr("mul", elem_a(), elem_b()), KernelExpr("add", temp(0), elem_a()),
+                            KernelExpr("mul", temp(1), temp(0))], False),
+]
+
+
+@pytest.mark.parametrize("name,chain,fused", FUSE_CASES, ids=[c[0] for c in FUSE_CASES])
+@pytest.mark.parametrize("dt_in", ["f32", "f16", "f64"])
+@pytest.mark.parametrize("lift", [False, True])
+def test_exact_product_sums_fuse(name, chain, fused, dt_in, lift):
+    n = 4096
+    km = fx.lower_elementwise([("a", [n], dt_in), ("b", [n], dt_in)], chain, [n], out_dtype="f64")
+    if lift:
+        km = fx.lift_1d(km)
+    fast, exact = chain_bodies(km)
+    want = fused and dt_in != "f64"
+    assert ("__builtin_fma(" in fast) == want, (name, dt_in, fast)
+    assert exact == ""          # no form here declines an element
+    assert be.plan(km)[1] == "bitexact-rne-gfx950-v1"
+
+
+# (name, chain, output dtype, whether the exp takes the f32-accurate form)
+EXP_CASES = [
+    ("exp*b", [KernelExpr("exp", elem_a()), KernelExpr("mul", temp(0), elem_b())], "f32", True),
+    ("b/exp", [KernelExpr("exp", elem_a()), KernelExpr("div", elem_b(), temp(0))], "f32", True),
+    ("-exp/b", [KernelExpr("exp", elem_a()), KernelExpr("neg", temp(0)), KernelExpr("div", temp(1), elem_b())],
+     "f32", True),
+    ("exp", [KernelExpr("exp", elem_a())], "f32", True),
+    ("exp+b", [KernelExpr("exp", elem_a()), KernelExpr("add", temp(0), elem_b())], "f32", False),
+    ("exp*exp-same", [KernelExpr("exp", elem_a()), KernelExpr("mul", temp(0), temp(0))], "f32", False),
+    # The outer exp is the result itself; the inner one feeds its argument
+    # (absolute error there becomes relative error of the result) and stays f64.
+    ("exp(exp)", [KernelExpr("exp", elem_a()), KernelExpr("exp", temp(0))], "f32", True),
+    ("exp*b-f64", [KernelExpr("exp", elem_a()), KernelExpr("mul", temp(0), elem_b())], "f64", False),
+    ("exp*b-f16", [KernelExpr("exp", elem_a()), KernelExpr("mul", temp(0), elem_b())], "f16", False),
+]
+
+
+@pytest.mark.parametrize("name,chain,out_dt,fast_exp", EXP_CASES, ids=[c[0] for c in EXP_CASES])
+def test_f32_accurate_exp_only_as_a_factor_of_an_f32_result(name, chain, out_dt, fast_exp):
+    n = 4096
+    km = fx.lower_elementwise([("a", [n], "f32"), ("b", [n], "f32")], chain, [n], out_dtype=out_dt)
+    fast, exact = chain_bodies(km)
+    assert fast.count("mlk_exp_f32acc(") == (1 if fast_exp else 0), (name, fast)
+    if name == "exp(exp)":
+        assert "t0 = exp(a0)" in fast and "t1 = mlk_exp_f32acc(a1, slow)" in fast
+    # A declining form always comes with the exact chain for its elements.
+    assert (exact != "") == fast_exp
+    assert "mlk_exp_f32acc(" not in exact and "slow" not in exact
+    if fast_exp:
+        assert be.plan(km)[1] == "tol-rel1e-6-gfx950-v1"
+
+
+def test_f32_accurate_exp_once_per_chain():
+    n = 4096
+    chain = [KernelExpr("exp", elem_a()), KernelExpr("exp", elem_b()), KernelExpr("mul", temp(0), temp(1))]
+    km = fx.lower_elementwise([("a", [n], "f32"), ("b", [n], "f32")], chain, [n])
+    fast, _ = chain_bodies(km)
+    assert fast.count("mlk_exp_f32acc(") == 1 and fast.count(" exp(") == 1
 
 
 @pytest.mark.parametrize("lift", [False, True])
