@@ -20,6 +20,9 @@ Bars, per op:
   tanh/erf/pow; their bits are pinned by no reference fixture): f64 buffers
   within 4 f64 ULP, f32 buffers within 1 f32 ULP (the two f64 values round to
   the same or an adjacent f32). Non-finite results must match in class.
+  exp into an f32 buffer through the template takes the f32-accurate form
+  (hardware exp2 on the reduced fraction, about 1.4e-7 relative): within 2
+  f32 ULP.
 * Gelu: 0.5 a (1 + tanh(u)) cancels for a below about -3, where an f64 ULP of
   tanh is many ULP of the result, so it is held to the reference's relative
   measure |got - ref| / max(|ref|, 1) <= 1e-14 on f64 buffers and 1e-7 on f32.
@@ -109,7 +112,7 @@ def generic(km):
     return g
 
 
-def check(op, dtype, family, got, ref):
+def check(op, dtype, family, got, ref, f32_ulps=1.0):
     """Asserts the per-op bar; returns the measure for the log line."""
     finite_ref = np.isfinite(ref)
     # Non-finite results match in class (NaN with NaN, inf with the same inf).
@@ -139,8 +142,8 @@ def check(op, dtype, family, got, ref):
         return f"{worst:g} f64 ULP (bound 4)"
     d = ulp_distance_f32(got.astype(np.float32), ref)
     worst = float(d.max())
-    assert worst <= 1.0, (op, dtype, worst, int(d.argmax()))
-    return f"{worst:g} f32 ULP (bound 1)"
+    assert worst <= f32_ulps, (op, dtype, worst, int(d.argmax()))
+    return f"{worst:g} f32 ULP (bound {f32_ulps:g})"
 
 
 CASES = [(op, None) for op in ["add", "sub", "mul", "div", "neg", "pow", "exp", "log", "sin", "cos",
@@ -162,7 +165,8 @@ def test_op_parity_gpu(hip, op, family, dtype):
         # Exact ops on f32 buffers: the f64 result rounded once to f32.
         with np.errstate(over="ignore"):
             cmp_ref = ref.astype(np.float32).astype(np.float64) if (dtype == "f32" and op in EXACT) else ref
-        note = check(op, dtype, family, got, cmp_ref)
+        fast_exp = op == "exp" and dtype == "f32" and path == "template"
+        note = check(op, dtype, family, got, cmp_ref, 2.0 if fast_exp else 1.0)
         say(f"{op}{'/' + family if family else ''} {dtype} {path} ({art.class_name}): {note}")
 
 
