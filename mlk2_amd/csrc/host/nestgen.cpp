@@ -483,6 +483,26 @@ struct Emitter {
     std::vector<Reg> regs;            // register-held buffers in scope
     std::vector<Slab> slabs;          // LDS-staged inputs
     std::vector<int> memReads, memStores, memAdds;
+    // Register sites per buffer: opens emitted, closes emitted, and whether
+    // an open can run more than once for one element (an enclosing loop
+    // with a zero coefficient in the address, more than one iteration, and
+    // no deeper loop bound on the path that it moves).
+    std::vector<int> regOpens, regCloses;
+    std::vector<char> regRepeats;
+    // Each open site's in-thread element hull, with the address's
+    // coefficients on the collapsed (thread) loops: other threads own other
+    // elements, so two sites meet only with equal thread coefficients and
+    // meeting hulls.
+    struct RegSpan {
+        std::vector<int64_t> threadCoeffs;
+        int64_t lo, hi;
+    };
+    std::vector<std::vector<RegSpan>> regSpans;
+    size_t chainLen{0};
+    std::vector<int> steerCount;      // loop position -> deeper path loops whose bounds use it
+    // Element hulls of the kernel's memory reads and writes, per buffer
+    // (lo > hi: none), over every thread's iterations.
+    std::vector<std::pair<int64_t, int64_t>> readHull, writeHull;
     std::string code;
     int nextReg{0};
     bool checked{false};
@@ -490,7 +510,34 @@ struct Emitter {
 
     Emitter(Ctx& c)
         : cx(c), km(c.km), slotOf(c.km.buffers.size(), -1), memReads(c.km.buffers.size(), 0),
-          memStores(c.km.buffers.size(), 0), memAdds(c.km.buffers.size(), 0) {}
+          memStores(c.km.buffers.size(), 0), memAdds(c.km.buffers.size(), 0), regOpens(c.km.buffers.size(), 0),
+          regCloses(c.km.buffers.size(), 0), regRepeats(c.km.buffers.size(), 0), regSpans(c.km.buffers.size()),
+          steerCount(kMaxDepth + 1, 0), readHull(c.km.buffers.size(), {INT64_MAX, INT64_MIN}),
+          writeHull(c.km.buffers.size(), {INT64_MAX, INT64_MIN}) {}
+
+    void widenHull(std::vector<std::pair<int64_t, int64_t>>& h, uint32_t b, const Affine& at,
+                   const std::vector<Range>& r) {
+        int64_t lo = 0, hi = 0;
+        bool u = false;
+        if (!bound(at, r, r.size(), lo, hi, u) || u) {
+            lo = INT64_MIN;
+            hi = INT64_MAX;
+        }
+        h[b].first = std::min(h[b].first, lo);
+        h[b].second = std::max(h[b].second, hi);
+    }
+
+    /// Two register sites of buffer b can reach one element.
+    bool regSitesOverlap(uint32_t b) const {
+        const auto& v = regSpans[b];
+        for (size_t i = 0; i < v.size(); ++i) {
+            for (size_t j = i + 1; j < v.size(); ++j) {
+                if (v[i].threadCoeffs != v[j].threadCoeffs) return true;
+                if (v[i].lo <= v[j].hi && v[j].lo <= v[i].hi) return true;
+            }
+        }
+        return false;
+    }
 
     int slot(uint32_t b) {
         if (slotOf[b] >= 0) return slotOf[b];
@@ -566,6 +613,7 @@ struct Emitter {
         const std::string dt = std::to_string(dtypeCode(km.buffers[b].dtype));
         const std::string f = affineCode(at, r.size());
         ++memReads[b];
+        widenHull(readHull, b, at, r);
         for (size_t k = 0; k < slabs.size(); ++k) {
             // The slab's hull covers every read of the buffer in the root.
             if (slabs[k].buf == b) {
@@ -648,6 +696,8 @@ struct Emitter {
                 line(ind + 1, "if (f >= a.n[" + std::to_string(s) + "]) { *a.status = 6; return; }");
             }
             ++memStores[w];
+            widenHull(writeHull, w, at, r);
+            if (so.accum != AccumMode::None) widenHull(readHull, w, at, r);
             if (so.accum == AccumMode::Add) {
                 ++memAdds[w];
                 ++memReads[w];
@@ -671,6 +721,28 @@ struct Emitter {
             line(ind, "const long long " + name + "f = " + affineCode(c.second, outer.size()) + ";");
             line(ind, "double " + name + " = mlk::loadOne<" + dt + ">(mb" + std::to_string(s) + ", " + name + "f);");
             regs.push_back(Reg{c.first, name});
+            ++regOpens[c.first];
+            widenHull(readHull, c.first, c.second, outer);
+            widenHull(writeHull, c.first, c.second, outer);
+            {
+                RegSpan sp;
+                Affine local = c.second;
+                for (size_t p = 0; p < chainLen && p < local.c.size(); ++p) {
+                    sp.threadCoeffs.push_back(local.c[p]);
+                    local.c[p] = 0;
+                }
+                bool u = false;
+                if (!bound(local, outer, outer.size(), sp.lo, sp.hi, u) || u) {
+                    sp.lo = INT64_MIN;
+                    sp.hi = INT64_MAX;
+                }
+                regSpans[c.first].push_back(std::move(sp));
+            }
+            for (size_t p = 0; p < outer.size(); ++p) {
+                if (coeffAt(c.second, p) == 0 && steerCount[p] == 0 && !outer[p].unbounded && outer[p].hi > outer[p].lo) {
+                    regRepeats[c.first] = 1;
+                }
+            }
         }
         return cands.size();
     }
@@ -682,6 +754,7 @@ struct Emitter {
             const std::string dt = std::to_string(dtypeCode(km.buffers[rg.buf].dtype));
             line(ind, "mlk::storeOne<" + dt + ">(mb" + std::to_string(s) + ", " + rg.name + "f, " + rg.name + ");");
             ++memStores[rg.buf];
+            ++regCloses[rg.buf];
         }
     }
 
@@ -739,6 +812,13 @@ struct Emitter {
         r.pop_back();
         if (cx.failed) return;
         const auto cands = regCandidates(acc, d, r);
+        std::vector<size_t> steered;
+        for (size_t p = 0; p < d; ++p) {
+            if (coeffAt(lb.begin, p) != 0 || coeffAt(lb.endInc, p) != 0) {
+                ++steerCount[p];
+                steered.push_back(p);
+            }
+        }
         int bodyInd = ind + 1;
         if (!cands.empty()) {
             line(ind + 1, "if (" + v + "b <= " + v + "e) {");
@@ -761,6 +841,7 @@ struct Emitter {
         closeRegs(opened, bodyInd);
         if (!cands.empty()) line(ind + 1, "}");
         line(ind, "}");
+        for (const size_t p : steered) --steerCount[p];
     }
 
     void guard(const KernelNode& n, std::vector<Range>& r, int ind, int level) {
@@ -876,6 +957,14 @@ Result<Step> planNestWith(const KernelModule& km, uint32_t root, bool allowSlabs
                 chainCodeText += "        if (" + v + " > " + affineCode(chainB[l].endInc, l) + ") continue;\n";
             }
         }
+        em.chainLen = chainLen;
+        // Chain loops whose bounds use an outer chain variable (a tile index
+        // moving its point loop's window) steer it for the whole body.
+        for (size_t l = 0; l < chainB.size(); ++l) {
+            for (size_t p = 0; p < l; ++p) {
+                if (coeffAt(chainB[l].begin, p) != 0 || coeffAt(chainB[l].endInc, p) != 0) ++em.steerCount[p];
+            }
+        }
         // Registers over the whole thread body.
         std::vector<Access> acc;
         collect(cx, body->children, r, true, acc, 1);
@@ -952,6 +1041,8 @@ extern "C" __global__ __launch_bounds__(256) void mlk_nest(const mlk_nest_args a
     src += "    }\n}\n";
 
     st.source = std::move(src);
+    st.readHull = em.readHull;
+    st.writeHull = em.writeHull;
     st.slabs = static_cast<int>(em.slabs.size());
     st.nestBufs = em.slots;
     st.threads = static_cast<int64_t>(total);
@@ -961,8 +1052,17 @@ extern "C" __global__ __launch_bounds__(256) void mlk_nest(const mlk_nest_args a
     for (const uint32_t b : em.slots) {
         const Dtype d = km.buffers[b].dtype;
         if (em.memStores[b] > 0) st.nestWrites.push_back(b);
+        if (em.memReads[b] > 0 || em.regOpens[b] > 0) st.nestReads.push_back(b);
         if (d == Dtype::F16) st.touchesF16 = true;
-        if (d != Dtype::F64 && ((em.memReads[b] > em.memAdds[b] && em.memStores[b] > 0) || em.memAdds[b] > 0)) {
+        // A narrow buffer's value is rounded on every store; reading one back
+        // (a memory read or += of a stored buffer, a register reopened on
+        // one element by a repeating loop or by two sites whose element
+        // hulls meet, or a register beside direct accesses) departs from the
+        // walker, which holds f64 throughout.
+        const bool regTrip = em.regSitesOverlap(b) || em.regRepeats[b] != 0 ||
+                             (em.regOpens[b] > 0 && (em.memStores[b] > em.regCloses[b] || em.memReads[b] > 0));
+        if (d != Dtype::F64 && ((em.memReads[b] > em.memAdds[b] && em.memStores[b] > 0) || em.memAdds[b] > 0 ||
+                                regTrip)) {
             st.narrowRoundTrip = true;
         }
     }

@@ -79,6 +79,10 @@ struct Step {
     std::string sourceNoSlabs;
     std::vector<uint32_t> nestBufs;
     std::vector<uint32_t> nestWrites;
+    std::vector<uint32_t> nestReads;  // buffers the kernel reads from memory (registers' loads included)
+    // Element hulls of the step's reads and writes per buffer id (lo > hi:
+    // none); empty vectors mean whole buffers.
+    std::vector<std::pair<int64_t, int64_t>> readHull, writeHull;
     int64_t threads{0};
     int collapsed{0};
     bool checked{false};

@@ -582,3 +582,38 @@ def tiled_gemm_module(m: int, k: int, n: int, dtype_in: str = "f32", tile: int =
 
     _emit_tiled_levels(km, [("i", 0, m - 1, True, False), ("j", 0, n - 1, True, True)], k_band, tile)
     return km
+
+
+def split_gemm_module(m: int, k: int, n: int, dtype_in: str = "f32", out_dtype: str = "f32") -> KernelModule:
+    """The untiled scheduled GEMM in the piecewise-split form the reference's
+    spec writes out (docs/polyhedral_spec.md:252-267):
+    `for i { for k in [0,1) { for j { init; acc } } for k in [1,K) { for j
+    { acc } } }`. The k segments are sibling subtrees under i, so j appears
+    once per segment (tests/unit/unit_poly.cpp:4279-4286). i and the j loops
+    carry the parallel mark; the j loops carry the vector hint."""
+    km = KernelModule()
+    a = km.add_buffer(KernelBuffer("A", dtype_in, True, False, False, m * k, [m, k]))
+    b = km.add_buffer(KernelBuffer("B", dtype_in, True, False, False, k * n, [k, n]))
+    c = km.add_buffer(KernelBuffer("C", out_dtype, False, True, False, m * n, [m, n]))
+    pos = {"i": 0, "k": 1, "j": 2}
+
+    def init():
+        cp = KernelNode(op="compute", exprs=[KernelExpr("add", const(0.0), const(0.0))])
+        st = KernelNode(op="store", out=c, out_index_coeffs=_stack_coeffs(3, pos, {"i": n, "j": 1}))
+        return [km.add_node(cp), km.add_node(st)]
+
+    def acc():
+        cp = KernelNode(op="compute", exprs=[
+            KernelExpr("add", elem_idx(a, _stack_coeffs(3, pos, {"i": k, "k": 1})), const(0.0)),
+            KernelExpr("add", elem_idx(b, _stack_coeffs(3, pos, {"k": n, "j": 1})), const(0.0)),
+            KernelExpr("mul", temp(0), temp(1))])
+        st = KernelNode(op="store", out=c, accum="add", out_index_coeffs=_stack_coeffs(3, pos, {"i": n, "j": 1}))
+        return [km.add_node(cp), km.add_node(st)]
+
+    segs = []
+    for lo, hi, body in ((0, 1, init() + acc()), (1, k, acc())):
+        j = km.add_node(KernelNode(op="loop", var="j", begin=0, end=n, parallel=True, vector_hint=True,
+                                   children=body))
+        segs.append(km.add_node(KernelNode(op="loop", var="k", begin=lo, end=hi, children=[j])))
+    km.add_node(KernelNode(op="loop", var="i", begin=0, end=m, parallel=True, children=segs))
+    return km

@@ -258,6 +258,133 @@ def test_tiled_gemm_collapses_all_parallel_levels():
     assert "double r0 = " in src  # C[i,j] held in an f64 register over the k band
 
 
+# ------------------------------------------- anchors in the reference ----
+def _loop(km, nid):
+    n = km.nodes[nid]
+    assert n.op == "loop", n.op
+    return n
+
+
+def test_split_gemm_fixture_is_the_spec_form():
+    # docs/polyhedral_spec.md:252-267 writes the piecewise-split GEMM out as
+    # for i { for k in [0,1) { for j { init; acc } } for k in [1,K) { for j
+    # { acc } } }: the split k segments are sibling subtrees under i, the
+    # init (a plain store of 0) runs only in the singleton segment, before
+    # the accumulation in the same j body.
+    m, k, n = 5, 7, 3
+    km = fx.split_gemm_module(m, k, n)
+    (root,) = km.roots()
+    i = _loop(km, root)
+    assert (i.var, i.begin, i.end, i.parallel) == ("i", 0, m, True)
+    assert len(i.children) == 2
+    segs = [_loop(km, c) for c in i.children]
+    assert [(s_.var, s_.begin, s_.end) for s_ in segs] == [("k", 0, 1), ("k", 1, k)]
+    bodies = []
+    for seg in segs:
+        (jid,) = seg.children
+        j = _loop(km, jid)
+        assert (j.var, j.begin, j.end, j.parallel) == ("j", 0, n, True)
+        bodies.append([km.nodes[c] for c in j.children])
+    assert [b.op for b in bodies[0]] == ["compute", "store", "compute", "store"]
+    assert [b.op for b in bodies[1]] == ["compute", "store"]
+    assert bodies[0][1].accum in (None, "none") and bodies[0][3].accum == "add" and bodies[1][1].accum == "add"
+
+
+def test_split_gemm_collapse_chain_is_one_level():
+    # tests/unit/unit_poly.cpp:4279-4286: the untiled scheduled GEMM's
+    # collapse chain is ONE level [i], because the split k segments are
+    # sibling subtrees (j duplicated per segment) and the interior
+    # single-loop-child rule stops the collapse at i. The generic kernel
+    # applies the same rule.
+    km = fx.split_gemm_module(70, 45, 37)
+    assert collapsed(generic(km, canonical=False)) == 1
+    assert collapsed(generic(km, canonical=True)) == 1
+
+
+@pytest.mark.parametrize("dtype", ["f64", "f32"])
+def test_split_gemm_spec_form_host(dtype):
+    # In this form C[i,j] is reloaded for every k (the k segments enclose the
+    # j loops): an f32 C is rounded at each k step where the walker keeps
+    # f64, so the plan claims bit-exactness for f64 buffers only.
+    m, k, n = 70, 45, 37
+    km = generic(fx.split_gemm_module(m, k, n, dtype, dtype), canonical=False)
+    assert backend.plan(km)[1] == ("bitexact-rne-gfx950-v1" if dtype == "f64" else "tol-rel1e-6-gfx950-v1")
+    a, b = gemm_inputs(m, k, n)
+    st, cur, ref = host_vs_oracle(km, {0: a, 1: b, 2: np.full(m * n, 7.0)})
+    assert st == 0
+    if dtype == "f64":
+        assert nf.same_bits(cur[2], ref[2])
+    else:
+        assert not nf.same_bits(cur[2], expected(ref[2], dtype))  # the per-step rounding shows
+        assert max_rel(cur[2], ref[2]) <= 1e-6
+    # The init overwrote the 7.0 everywhere: C = A B exactly as the walker sums it.
+    assert np.array_equal(ref[2], oracle.run(fx.matmul_call_module(m, k, n, "f64", "f64"),
+                                             {0: a, 1: b}, init={2: np.zeros(m * n)})[2])
+
+
+def _chained_roots_module(dtype, overlap=True):
+    """Root 1: y[i] = 0.1 x[i]; root 2: z[i] = 3 y[i + s] (s = 0, or past
+    root 1's writes when overlap is False)."""
+    n = 64
+    km = KernelModule()
+    x = km.add_buffer(KernelBuffer("x", dtype, True, False, False, 2 * n, [2 * n]))
+    y = km.add_buffer(KernelBuffer("y", dtype, False, True, False, 2 * n, [2 * n]))
+    z = km.add_buffer(KernelBuffer("z", dtype, False, True, False, n, [n]))
+    for src, dst, c, off in ((x, y, 0.1, 0), (y, z, 3.0, 0 if overlap else n)):
+        ex = KernelExpr("mul", elem_idx(src, [1], off), const(c))
+        cp = km.add_node(KernelNode(op="compute", exprs=[ex]))
+        st = km.add_node(KernelNode(op="store", out=dst, out_index_coeffs=[1]))
+        km.add_node(KernelNode(op="loop", var="i", begin=0, end=n, children=[cp, st]))
+    return km
+
+
+@pytest.mark.parametrize("dtype", ["f64", "f32", "f16"])
+def test_later_root_reading_a_narrow_output_is_not_bit_exact(dtype):
+    # The walker keeps y in f64 between the roots; the device stores it in
+    # y's dtype, so root 2 reads the rounded value. The plan says so.
+    km = _chained_roots_module(dtype)
+    want = {"f64": "bitexact-rne-gfx950-v1", "f32": "tol-rel1e-6-gfx950-v1", "f16": "tol-rel1e-2-gfx950-v1"}
+    assert backend.plan(km)[1] == want[dtype]
+    xs = np.random.default_rng(1).uniform(-1, 1, 128)
+    ref = oracle.run(km, {0: xs})
+    if dtype == "f32":
+        xs32 = xs.astype(np.float32).astype(np.float64)
+        ref = oracle.run(km, {0: xs32})
+        y_dev = (ref[1][:64]).astype(np.float32).astype(np.float64)
+        assert not np.array_equal((3.0 * y_dev).astype(np.float32), ref[2].astype(np.float32))
+    # Reads of elements no earlier root wrote keep the claim.
+    assert backend.plan(_chained_roots_module(dtype, overlap=False))[1] == "bitexact-rne-gfx950-v1"
+
+
+@pytest.mark.parametrize("lo,hi,t", [(0, 44, 16), (0, 63, 16), (0, 15, 16), (0, 9, 16), (3, 40, 8)])
+def test_tiled_level_parts_follow_the_spec(lo, hi, t):
+    # docs/polyhedral_spec.md:275-282: a tiled band level is a TILE loop with
+    # constant bounds floor(lo/t) .. floor(hi/t) and a POINT loop with affine
+    # bounds t*ti .. t*ti + t - 1; a trailing partial tile, present exactly
+    # when (hi + 1) % t != 0, is a sibling part whose point loop carries the
+    # constant clipped end hi. Each point loop's begin is the tile
+    # coefficient at the tile index's stack slot.
+    km = fx.KernelModule()
+    parts = fx._emit_tiled_levels(km, [("x", lo, hi, True, False)], lambda p, d: [], t)
+    tiles = [_loop(km, pid) for pid in parts]
+    covered = []
+    for tl in tiles:
+        assert tl.var == "x_t" and not tl.begin_coeffs and not tl.end_coeffs
+        covered += list(range(tl.begin, tl.end))
+        (pid,) = tl.children
+        pt = _loop(km, pid)
+        assert pt.var == "x" and pt.begin_coeffs == [t] and pt.begin_offset == 0
+    assert covered == list(range(lo // t, hi // t + 1))
+    partial = (hi + 1) % t != 0
+    assert len(tiles) == (1 if not partial or (hi + 1) // t - 1 < lo // t else 2) or (partial and len(tiles) == 2)
+    last_point = _loop(km, tiles[-1].children[0])
+    if partial:
+        assert tiles[-1].begin == hi // t and tiles[-1].end == hi // t + 1
+        assert not last_point.end_coeffs and last_point.end == hi + 1
+    else:
+        assert last_point.end_coeffs == [t] and last_point.end_offset == t - 1
+
+
 @pytest.mark.parametrize("canonical", [False, True])
 def test_tiled_elementwise_generic_host(canonical):
     km = generic(fx.tiled_elementwise_module(fx.config3_module(37, 100, tier=2), tile=32), canonical)
@@ -369,6 +496,22 @@ def test_tiled_gemm_gpu(hip, init, shape):
         r = max_rel(got, ref)
         say(f"  {dtype} gemm-nest max_rel={r:.3e}")
         assert r <= 1e-5 * np.sqrt(k)
+
+
+@pytest.mark.gpu
+def test_split_gemm_spec_form_gpu(hip):
+    # The spec's piecewise-split GEMM on the generic kernel (chain [i] only):
+    # the walker's f64 sums, bit-exact (f32: rounded once).
+    m, k, n = 70, 45, 37
+    a, b = gemm_inputs(m, k, n)
+    c0 = np.full(m * n, 7.0)
+    for dtype in ("f64", "f32"):
+        km = fx.split_gemm_module(m, k, n, dtype, dtype)
+        ref = oracle.run(km, {0: a, 1: b}, init={2: c0})[2]
+        for canonical in (False, True):
+            got = hip.build(generic(km, canonical)).run({0: a, 1: b, 2: c0})[2]
+            assert nf.same_bits(got, expected(ref, dtype)), (dtype, canonical)
+        say(f"split gemm (spec form) {dtype}: bit-exact")
 
 
 @pytest.mark.gpu
