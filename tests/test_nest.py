@@ -501,7 +501,8 @@ def test_tiled_gemm_gpu(hip, init, shape):
 @pytest.mark.gpu
 def test_split_gemm_spec_form_gpu(hip):
     # The spec's piecewise-split GEMM on the generic kernel (chain [i] only):
-    # the walker's f64 sums, bit-exact (f32: rounded once).
+    # the walker's f64 sums, bit-exact on f64 buffers; an f32 C is reloaded
+    # per k step, so it is held to its plan's 1e-6.
     m, k, n = 70, 45, 37
     a, b = gemm_inputs(m, k, n)
     c0 = np.full(m * n, 7.0)
@@ -509,9 +510,15 @@ def test_split_gemm_spec_form_gpu(hip):
         km = fx.split_gemm_module(m, k, n, dtype, dtype)
         ref = oracle.run(km, {0: a, 1: b}, init={2: c0})[2]
         for canonical in (False, True):
-            got = hip.build(generic(km, canonical)).run({0: a, 1: b, 2: c0})[2]
-            assert nf.same_bits(got, expected(ref, dtype)), (dtype, canonical)
-        say(f"split gemm (spec form) {dtype}: bit-exact")
+            art = hip.build(generic(km, canonical))
+            got = art.run({0: a, 1: b, 2: c0})[2]
+            if dtype == "f64":
+                assert art.policy == "bitexact-rne-gfx950-v1"
+                assert nf.same_bits(got, ref), canonical
+            else:
+                assert art.policy == "tol-rel1e-6-gfx950-v1"
+                assert max_rel(got, ref) <= 1e-6, canonical
+        say(f"split gemm (spec form) {dtype}: within its policy")
 
 
 @pytest.mark.gpu
