@@ -139,3 +139,65 @@ def test_c1_sine_with_declined_reductions(hip, lift):
     assert d.max() <= 4.0
     # The declined arguments come from the exact f64 form.
     assert d[big].max() == 0
+
+
+def mixed_streams_module(rows, cols):
+    """out[i, j] = exp(0.5 * x[i, j] + s[i]) * t[j, i]: a unit-stride stream,
+    a broadcast stream (coefficient 0 on the innermost loop) and a gather
+    (coefficient `rows`), so the exact pass re-reads all three kinds."""
+    from mlk2_amd.kernel_ir import (KernelBuffer, KernelExpr, KernelModule, KernelNode, const, elem_idx,
+                                    temp)
+    km = KernelModule()
+    x = km.add_buffer(KernelBuffer("x", "f32", True, False, False, rows * cols, [rows, cols]))
+    s = km.add_buffer(KernelBuffer("s", "f32", True, False, False, rows, [rows]))
+    t = km.add_buffer(KernelBuffer("t", "f32", True, False, False, cols * rows, [cols, rows]))
+    y = km.add_buffer(KernelBuffer("y", "f32", False, True, False, rows * cols, [rows, cols]))
+    cp = km.add_node(KernelNode(op="compute", exprs=[
+        KernelExpr("mul", elem_idx(x, [cols, 1]), const(0.5)),
+        KernelExpr("add", temp(0), elem_idx(s, [1, 0])),
+        KernelExpr("exp", temp(1)),
+        KernelExpr("mul", temp(2), elem_idx(t, [1, rows]))]))
+    st = km.add_node(KernelNode(op="store", out=y, out_index_coeffs=[cols, 1]))
+    j = km.add_node(KernelNode(op="loop", var="j", begin=0, end=cols, children=[cp, st]))
+    km.add_node(KernelNode(op="loop", var="i", begin=0, end=rows, children=[j]))
+    return km
+
+
+def test_exact_pass_rereads_broadcast_and_gather_streams(hip):
+    rows, cols = 67, 1100                       # ragged: partial last segments
+    km = mixed_streams_module(rows, cols)
+    art = hip.build(km)
+    assert art.class_name == "elementwise-nd"
+    rng = np.random.default_rng(14)
+    x = rng.uniform(-4, 4, (rows, cols)).astype(np.float32).astype(np.float64)
+    s = rng.uniform(-1, 1, rows).astype(np.float32).astype(np.float64)
+    t = rng.uniform(0.5, 2, (cols, rows)).astype(np.float32).astype(np.float64)
+    x[3, 700] = 1500.0                          # exp overflows: that wave's exact pass
+    x[10, :] = -1600.0                          # a row of zeros
+    x[20, 5] = np.nan
+    s[33] = 800.0                               # a broadcast value that declines a whole row
+    got = art.run({0: x, 1: s, 2: t})[3]
+    ref = oracle.run(km, {0: x, 1: s, 2: t})[3]
+    err = finite_max_rel(got, ref)
+    say(f"mixed streams {rows}x{cols}: max rel {err:.3g}")
+    assert err <= 1e-6
+
+
+def test_exact_pass_with_a_dynamic_bound(hip):
+    # The 1-D dynamic form (loop end = the run's element count) through the
+    # legacy ABI, with declined sine arguments in a partial last segment.
+    km = fx.config1_module(n=1)
+    km.nodes[2].end = -1
+    for b in km.buffers:
+        b.elements = -1
+        b.dims = []
+    n = 5000
+    rng = np.random.default_rng(15)
+    x = rng.uniform(-4, 4, n)
+    x[4990:4996] = [3000.0, -2500.0, np.nan, np.inf, 1e7, -1e7]
+    x = x.astype(np.float32).astype(np.float64)
+    got = hip.build(km).run({0: x}, elements=n, legacy=True)[1].astype(np.float32)
+    ref = oracle.run(km, {0: x}, elements=n)[1]
+    d = ulp_distance_f32(got, ref)
+    say(f"dynamic bound with declined arguments: max ULP {d.max()}, tail {d[4990:4996].tolist()}")
+    assert d.max() <= 4.0 and d[4990:4996].max() == 0
