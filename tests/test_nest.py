@@ -499,6 +499,26 @@ def test_tiled_gemm_gpu(hip, init, shape):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("dtype", ["f64", "f32", "f16"])
+def test_later_root_reading_a_narrow_output_gpu(hip, dtype):
+    # Root 2 reads root 1's output: bit-exact on f64 buffers, and within the
+    # plan's tolerance where the device rounds the intermediate buffer.
+    km = _chained_roots_module(dtype)
+    xs = np.random.default_rng(2).uniform(-1, 1, 128)
+    np_dt = {"f64": np.float64, "f32": np.float32, "f16": np.float16}[dtype]
+    xs = xs.astype(np_dt).astype(np.float64)
+    art = hip.build(km)
+    got = art.run({0: xs})
+    ref = oracle.run(km, {0: xs})
+    tol = {"bitexact-rne-gfx950-v1": 0.0, "tol-rel1e-6-gfx950-v1": 1e-6, "tol-rel1e-2-gfx950-v1": 1e-2}[art.policy]
+    for bid in km.output_ids():
+        want = ref[bid].astype(np_dt).astype(np.float64)
+        err = max_rel(got[bid][:64], want[:64])
+        say(f"chained roots {dtype} buffer {bid}: {art.policy}, max rel {err:.2e}")
+        assert err <= tol if tol else nf.same_bits(got[bid][:64], want[:64])
+
+
+@pytest.mark.gpu
 def test_split_gemm_spec_form_gpu(hip):
     # The spec's piecewise-split GEMM on the generic kernel (chain [i] only):
     # the walker's f64 sums, bit-exact on f64 buffers; an f32 C is reloaded
