@@ -27,6 +27,10 @@ PEAK_HBM_GBS = 8000.0          # MI355X HBM3E, AMD datasheet
 PEAK_F16_TFLOPS = 2500.0       # dense FP16 MFMA
 PEAK_F32_TFLOPS = 157.3        # FP32 matrix
 PROFILE_PMC = os.path.join(ROOT, "profiles", "softmax_c2_8192x4096_pmc.txt")
+# Back-to-back launches of a config before it is timed. Under sustained load
+# the chip's clock settles within about 30 ms; a few launches alone time the
+# ramp instead (4096^3 f16 GEMM: 130-150 us cold, 119 us settled).
+SETTLE_MS = 100.0
 
 
 def _cpu_model() -> str:
@@ -121,7 +125,11 @@ def bench_config(be, name: str, steps: int, warmup: int) -> dict:
     else:
         raise KeyError(name)
     art = be.build(km)
-    span_ms = art.time_device_span(bufs, reps=steps, warmup=warmup)
+    # Settle: at least SETTLE_MS of back-to-back launches, then the timed span.
+    est = art.time_device_span(bufs, reps=3, warmup=1)
+    settle_reps = max(warmup, int(SETTLE_MS / max(est, 1e-3)) + 1)
+    settled_ms = art.time_device_span(bufs, reps=settle_reps, warmup=0) * settle_reps
+    span_ms = art.time_device_span(bufs, reps=steps, warmup=0)
     st = _stats(art.time_device(bufs, reps=steps, warmup=1))
     scale = 1e9 if unit == "GB/s" else 1e12
     achieved = work / (span_ms * 1e-3) / scale
@@ -129,7 +137,8 @@ def bench_config(be, name: str, steps: int, warmup: int) -> dict:
     return {"workload": wl, "class": art.class_name, "policy": art.policy, "kernels": kernels, "unit": unit,
             "bound": bound, "algorithmic_work": work, "achieved": round(achieved, 2),
             "peak": peak, "frac": round(achieved / peak, 4), "kernel_ms": round(span_ms, 5),
-            "per_launch_event": {k: round(v, 5) for k, v in st.items()}}
+            "per_launch_event": {k: round(v, 5) for k, v in st.items()},
+            "settle": {"launches": settle_reps, "ms": round(settled_ms, 1)}}
 
 
 def cpu_baseline_softmax() -> dict:
@@ -321,6 +330,9 @@ def main() -> int:
                                        "WRITE_SIZE runs of this workload, copy-calibrated); not measured "
                                        "in this run"},
         "cpu_baseline": None if args.no_cpu else cpu_baseline_softmax(),
+        # Each config is timed after >= SETTLE_MS of back-to-back launches
+        # (its "settle" field); the headline's steps follow --warmup steps.
+        "config_settle_ms": SETTLE_MS,
         "configs": configs,
     }
     print(json.dumps(line), flush=True)
