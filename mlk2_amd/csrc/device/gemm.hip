@@ -3,8 +3,12 @@
 // and the poly.synth init+accumulate nest (compiler/src/passes/poly/
 // poly.synth.cpp:58-147, C = 0 then +=).
 //
-// f16 x f16 -> f32 (tensor_f16_gpu): v_mfma_f32_32x32x16_f16. Workgroup tile
-// 256x256, K step 64, 512 threads = 8 waves as 2 (M) x 4 (N); each wave owns
+// f16 x f16 -> f32 (tensor_f16_gpu), 256x256 workgroup tiles, launch forms 0-8.
+// The default, form 8 (gemmF16Dma8), moves both operands global -> LDS by
+// the direct path into a 4-deep ring of K steps and runs 8 waves of
+// v_mfma_f32_16x16x32_f16 tiles; form 7 (gemmF16Dma) is the same data path
+// with 4 waves of 32x32x16 tiles. Form 0, the first: v_mfma_f32_32x32x16_f16,
+// K step 64, 512 threads = 8 waves as 2 (M) x 4 (N); each wave owns
 // 128x64 = 4x2 MFMA tiles (128 accumulator VGPRs). A and B tiles are double
 // buffered in LDS (2 x 72 KiB): the next K step's global loads are issued
 // before the current step's MFMAs and written to the other buffer after
@@ -917,6 +921,170 @@ __global__ __launch_bounds__(256, 1) void gemmF16Dma(const _Float16* __restrict_
     }
 }
 
+/// Variant 8: variant 7's data movement (the same 4-deep direct-to-LDS ring
+/// of K steps of 32, the same swizzles and transposed B reads) with 8 waves
+/// (2 per SIMD, 2 (M) x 4 (N)), each owning 128 x 64, and
+/// v_mfma_f32_16x16x32_f16 with the operands swapped: each 16 x 16 tile is
+/// D = B^T A^T, so a lane holds 4 consecutive columns of one row of C and
+/// stores them with one 16-byte write. The 32 tiles of a wave (8 x 4) keep
+/// their 128 accumulators in ordinary registers. Under this chip's power
+/// limit the smaller MFMA sustains more work per joule (a register-only loop
+/// runs 12% faster with it than with 32x32x16). Each K step is two groups of
+/// 16 MFMAs (m-tiles 0-3, then 4-7): the first group's MFMAs overlap the
+/// reads of the second group's A fragments; the barrier that certifies the
+/// next stage sits between the groups, and the second group overlaps the
+/// reads of the next step's first group (B fragments double buffered).
+/// Every output element takes its products in the same k order as variant
+/// 7, and the results match it bit for bit. Needs K a multiple of 64.
+template <bool ACC>
+__global__ __launch_bounds__(512, 1) void gemmF16Dma8(const _Float16* __restrict__ A,
+                                                      const _Float16* __restrict__ B,
+                                                      float* __restrict__ C, int M, int N, int K,
+                                                      int64_t lda, int64_t ldb, int64_t ldc) {
+    extern __shared__ __align__(16) _Float16 lds[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 2, wn = wave & 3;
+    int tm, tn;
+    xcdTile(M / kBM, N / kBN, tm, tn);
+    const int64_t row0 = static_cast<int64_t>(tm) * kBM;
+    const int64_t col0 = static_cast<int64_t>(tn) * kBN;
+    const int steps = K / kDmaBK;
+
+    // Stage `slot` receives K step min(slot, steps - 1) in ring slot
+    // slot % kDmaStages. Wave w issues A instructions 2w, 2w + 1 (16 rows
+    // each) and B instructions 2w, 2w + 1 (2 k-rows each).
+    auto issue = [&](int slot) {
+        const int k0 = min(slot, steps - 1) * kDmaBK;
+        const _Float16* st = lds + (slot % kDmaStages) * kDmaStage;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int ins = wave * 2 + j;
+            const int q = ins * 64 + lane;
+            const int row = q >> 2;
+            const int c = (q & 3) ^ ((row >> 2) & 3);
+            dmaLoad16(A + (row0 + row) * lda + k0 + c * 8, st + ins * 512);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int ins = wave * 2 + j;
+            const int q = ins * 64 + lane;
+            const int krow = q >> 5;
+            const int c = (q & 31) ^ ((krow & 3) * 4);
+            dmaLoad16(B + static_cast<int64_t>(k0 + krow) * ldb + col0 + c * 8, st + kDmaA + ins * 512);
+        }
+    };
+
+    f32x4 acc[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.0f;
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < kDmaStages - 1; ++s) issue(s);
+
+    const int l16 = lane & 15, g = lane >> 4;
+    // The MFMA's B operand (A^T): row wm * 128 + 16 mt + l16 of A, chunk g
+    // (k 8g .. 8g + 7) at its swizzled slot; tile mt adds 1024 bytes.
+    uint32_t offA;
+    {
+        const int row = wm * 128 + l16;
+        offA = 2u * (row * kDmaBK + ((g ^ ((row >> 2) & 3)) * 8));
+    }
+    // The MFMA's A operand (B^T): column wn * 64 + 16 nt + l16 of B, k 8g ..
+    // 8g + 7 by two transposed reads (h = 0, 1); lane (g, l16) points at
+    // k-row 8g + 4h + l16 / 4, columns 4 (l16 % 4) .. + 3 of the tile.
+    uint32_t offB[4][2];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int krow = 8 * g + 4 * h + (l16 >> 2);
+            const int col = wn * 64 + nt * 16 + 4 * (l16 & 3);
+            offB[nt][h] = 2u * (kDmaA + krow * 256 + (((col >> 3) ^ ((krow & 3) * 4)) * 8) + (col & 7));
+        }
+    }
+    const uint32_t ldsBase = ldsOffset(lds);
+    auto readA = [&](f16x8& f, uint32_t base, int mt) {
+        f = *reinterpret_cast<const __attribute__((address_space(3))) f16x8*>(base + offA + 1024u * mt);
+    };
+    auto readB = [&](f16x8& f, uint32_t base, int nt) {
+        const fp16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+            reinterpret_cast<__attribute__((address_space(3))) fp16x4*>(base + offB[nt][0]));
+        const fp16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+            reinterpret_cast<__attribute__((address_space(3))) fp16x4*>(base + offB[nt][1]));
+        f = __builtin_shufflevector(__builtin_bit_cast(f16x4, v0), __builtin_bit_cast(f16x4, v1), 0, 1, 2, 3, 4, 5,
+                                    6, 7);
+    };
+    f16x8 aLo[4], aHi[4], bX[4], bY[4];
+    // 16 MFMAs: m-tiles mt0 .. mt0 + 3 against the 4 n-tiles.
+    auto group = [&](const f16x8 (&a)[4], const f16x8 (&b)[4], int mt0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                acc[mt0 + i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b[j], a[i], acc[mt0 + i][j], 0, 0, 0);
+            }
+        }
+    };
+    // Stage 0 landed (stages 1 and 2, 4 direct loads each per wave, may be
+    // in flight).
+    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    asm volatile("s_barrier" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < 4; ++i) readA(aLo[i], ldsBase, i);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) readB(bX[j], ldsBase, j);
+    auto step = [&](int s, f16x8 (&bCur)[4], f16x8 (&bNxt)[4]) {
+        const uint32_t cb = ldsBase + 2u * static_cast<uint32_t>((s % kDmaStages) * kDmaStage);
+        group(aLo, bCur, 0);                          // m-tiles 0-3 of step s; reads m-tiles 4-7
+#pragma unroll
+        for (int i = 0; i < 4; ++i) readA(aHi[i], cb, 4 + i);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+            if (i < 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        // Stage s + 1 landed (one later stage may be in flight); after the
+        // barrier every wave is past step s - 1, so its slot can be refilled.
+        asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+        asm volatile("s_barrier" ::: "memory");
+        issue(s + kDmaStages - 1);
+        const uint32_t nb = ldsBase + 2u * static_cast<uint32_t>(((s + 1) % kDmaStages) * kDmaStage);
+        group(aHi, bCur, 4);                          // m-tiles 4-7 of step s; reads step s + 1's first group
+#pragma unroll
+        for (int i = 0; i < 4; ++i) readA(aLo[i], nb, i);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) readB(bNxt[j], nb, j);
+#pragma unroll
+        for (int i = 0; i < 12; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    };
+    for (int s = 0; s < steps; s += 2) {              // steps is even (K % 64 == 0)
+        step(s, bX, bY);
+        step(s + 1, bY, bX);
+    }
+    // No direct load may still be writing LDS when the workgroup ends.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int64_t row = row0 + wm * 128 + i * 16 + l16;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            f32x4* dst = reinterpret_cast<f32x4*>(C + row * ldc + col0 + wn * 64 + j * 16 + 4 * g);
+            f32x4 v = acc[i][j];
+            if (ACC) v += *dst;
+            *dst = v;
+        }
+    }
+}
+
 // ---------------------------------------------------------------- f32 ----
 constexpr int kFM = 64, kFN = 64, kFK = 32;
 constexpr int kFDepth = 2;   // K steps of global loads in flight ahead of the MFMAs
@@ -1100,9 +1268,10 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 // field overrides it): 0: 8 waves of 128x64; 1: 4 waves of 128x128; 2: 4
 // waves with A direct to LDS; 3: 4 waves, explicitly pipelined; 5/6:
 // 128x256 tiles, two workgroups per CU, loads two / one step ahead;
-// 7: 4 waves, both operands direct to a 4-deep LDS ring, B read transposed
-// (measured fastest on gfx950).
-int gGemmF16Variant = 7;
+// 7: 4 waves, both operands direct to a 4-deep LDS ring, B read transposed;
+// 8: variant 7's data path with 8 waves of 16x16x32 MFMA tiles (measured
+// fastest on gfx950).
+int gGemmF16Variant = 8;
 
 }  // namespace
 
@@ -1138,7 +1307,26 @@ extern "C" int mlkd_launch_gemm(const mlkd_gemm* p, void* stream) {
             }
             ldsRaised = true;
         }
-        if (variant == 7) {
+        if (variant == 8 && (p->ldc % 4) == 0 && aligned16(p->c)) {
+            static bool raised8 = false;
+            if (!raised8) {
+                if (hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF16Dma8<true>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        static_cast<int>(kLdsDma)) != hipSuccess ||
+                    hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF16Dma8<false>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        static_cast<int>(kLdsDma)) != hipSuccess) {
+                    return MLKD_RT_LAUNCH;
+                }
+                raised8 = true;
+            }
+            hipLaunchKernelGGL((p->accumulate ? gemmF16Dma8<true> : gemmF16Dma8<false>), dim3(tiles), dim3(512),
+                               kLdsDma, st, static_cast<const _Float16*>(p->a), static_cast<const _Float16*>(p->b),
+                               static_cast<float*>(p->c), static_cast<int>(p->m), static_cast<int>(p->n),
+                               static_cast<int>(p->k), p->lda, p->ldb, p->ldc);
+            return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
+        }
+        if (variant == 7 || variant == 8) {
             static bool raised7 = false;
             if (!raised7) {
                 if (hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF16Dma<true>),

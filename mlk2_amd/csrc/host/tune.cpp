@@ -370,7 +370,7 @@ std::vector<int> variantSpace(const KernelModule& km, const Step& st) {
         case StepKind::Gemm:
             if (dt(st.a) == Dtype::F16 && dt(st.b) == Dtype::F16 && dt(st.c) == Dtype::F32 && st.m % 256 == 0 &&
                 st.n % 256 == 0 && st.k % 64 == 0 && st.k > 0) {
-                return {7, 0, 1, 2, 3, 5, 6};
+                return {8, 7, 0, 1, 2, 3, 5, 6};
             }
             return {};
         case StepKind::ScoreSoftmax:

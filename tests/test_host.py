@@ -202,7 +202,7 @@ def test_chain_codegen_exact_constants():
 
 @pytest.mark.parametrize("km,space", [
     (fx.config2_module(8192, 4096, 2), [5, 0, 2, 3, 4, 1]),
-    (fx.config4_module(4096, 4096, 4096, "f16", 2), [7, 0, 1, 2, 3, 5, 6]),
+    (fx.config4_module(4096, 4096, 4096, "f16", 2), [8, 7, 0, 1, 2, 3, 5, 6]),
     (fx.score_softmax_module(16, 2048, 128), [0, 1]),
     (fx.score_softmax_module(2, 4096, 128), [0, 1]),
     (fx.score_softmax_module(2, 256, 128), [0, 1]),
