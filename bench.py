@@ -31,6 +31,16 @@ PROFILE_PMC = os.path.join(ROOT, "profiles", "softmax_c2_8192x4096_pmc.txt")
 # the chip's clock settles within about 30 ms; a few launches alone time the
 # ramp instead (4096^3 f16 GEMM: 130-150 us cold, 119 us settled).
 SETTLE_MS = 100.0
+# Each config's duration is the median of SPANS event-timed spans of back-to-
+# back launches, each at least SPAN_MS long: the runtime now and then leaves a
+# gap of tens of microseconds between two launches, which a single short
+# span of a 20 us kernel would spread over its average.
+SPANS, SPAN_MS = 5, 2.0
+
+
+def median_span(art, bufs, reps: int) -> float:
+    """Median over SPANS spans of `reps` back-to-back launches (ms per launch)."""
+    return float(np.median([art.time_device_span(bufs, reps=reps, warmup=0) for _ in range(SPANS)]))
 
 
 def _cpu_model() -> str:
@@ -129,7 +139,8 @@ def bench_config(be, name: str, steps: int, warmup: int) -> dict:
     est = art.time_device_span(bufs, reps=3, warmup=1)
     settle_reps = max(warmup, int(SETTLE_MS / max(est, 1e-3)) + 1)
     settled_ms = art.time_device_span(bufs, reps=settle_reps, warmup=0) * settle_reps
-    span_ms = art.time_device_span(bufs, reps=steps, warmup=0)
+    span_reps = max(steps, int(SPAN_MS / max(est, 1e-3)) + 1)
+    span_ms = median_span(art, bufs, span_reps)
     st = _stats(art.time_device(bufs, reps=steps, warmup=1))
     scale = 1e9 if unit == "GB/s" else 1e12
     achieved = work / (span_ms * 1e-3) / scale
@@ -138,7 +149,8 @@ def bench_config(be, name: str, steps: int, warmup: int) -> dict:
             "bound": bound, "algorithmic_work": work, "achieved": round(achieved, 2),
             "peak": peak, "frac": round(achieved / peak, 4), "kernel_ms": round(span_ms, 5),
             "per_launch_event": {k: round(v, 5) for k, v in st.items()},
-            "settle": {"launches": settle_reps, "ms": round(settled_ms, 1)}}
+            "settle": {"launches": settle_reps, "ms": round(settled_ms, 1)},
+            "spans": {"count": SPANS, "launches_each": span_reps}}
 
 
 def cpu_baseline_softmax() -> dict:
@@ -291,9 +303,10 @@ def main() -> int:
     ms_per_step = wall * 1e3 / args.steps
     bytes_alg = 2 * 4 * m * k
     value = bytes_alg / (ms_per_step * 1e-3) / 1e9
-    # Kernel duration: one HIP event pair on the launch stream around K
-    # back-to-back launches (the same span the wall clock covers above).
-    kernel_ms = art.time_device_span(bufs, reps=args.steps, warmup=2)
+    # Kernel duration: HIP event pairs on the launch stream around K
+    # back-to-back launches (the span the wall clock covers above), the
+    # median of SPANS such spans.
+    kernel_ms = median_span(art, bufs, args.steps)
     achieved = bytes_alg / (kernel_ms * 1e-3) / 1e9
 
     configs = {}
