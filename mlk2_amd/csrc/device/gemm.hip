@@ -20,8 +20,11 @@
 // runs form a 4x8 block that shares A and B panels in that XCD's L2.
 //
 // f32 x f32 -> f32: v_mfma_f32_32x32x2_f32, 64x64 tiles (256 tiles at 1024^2
-// fill the 256 CUs), K step 32, A transposed into LDS ([k][m]) and B stored as
-// loaded ([k][n]) so each MFMA operand is one conflict-free 4-byte read.
+// fill the 256 CUs). Form 0 (K a multiple of 64, the default) moves both
+// tiles by the direct path into a 4-deep LDS ring; form 1 (K a multiple of
+// 32) stages them through registers, A transposed into LDS ([k][m]) and B
+// stored as loaded ([k][n]) so each MFMA operand is one conflict-free 4-byte
+// read.
 //
 // Any other shape or dtype mix runs the general tiled kernel (f32 or f64
 // accumulation, bounds-checked).
@@ -1089,8 +1092,9 @@ __global__ __launch_bounds__(512, 1) void gemmF16Dma8(const _Float16* __restrict
 constexpr int kFM = 64, kFN = 64, kFK = 32;
 constexpr int kFDepth = 2;   // K steps of global loads in flight ahead of the MFMAs
 
-/// 64x64 output tile per workgroup of 4 waves (2 x 2 of 32x32), K steps of
-/// 32 through double-buffered LDS, v_mfma_f32_32x32x2f32 with k ascending.
+/// f32 form 1: 64x64 output tile per workgroup of 4 waves (2 x 2 of 32x32),
+/// K steps of 32 through double-buffered LDS, v_mfma_f32_32x32x2f32 with k
+/// ascending.
 /// Global loads run kFDepth steps ahead in registers (slot t % kFDepth holds
 /// step t); A is stored transposed ([k][m]) for the MFMA's A operand, and its
 /// load mapping gives each wave 16 rows x 4 k-chunks, so every transposed LDS
@@ -1180,6 +1184,109 @@ __global__ __launch_bounds__(256) void gemmF32Mfma(const float* __restrict__ A,
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         const int64_t row = row0 + wm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        float* dst = C + row * ldc + cBase;
+        *dst = ACC ? *dst + acc[r] : acc[r];
+    }
+}
+
+/// f32 form 0: both 64x64 tiles move global -> LDS by the direct path
+/// (global_load_lds_dwordx4, no register staging and no LDS writes) into a
+/// 4-deep ring of K steps of 64 (32 KiB per stage). 4 waves (2 x 2) each own
+/// a 32x32 tile on v_mfma_f32_32x32x2_f32, with the k order permuted within
+/// a step: MFMA t takes k = t from lanes 0-31 and k = 32 + t from lanes
+/// 32-63, so the A operand of 4 consecutive MFMAs is one 16-byte read of a
+/// row of A (16-byte chunk c of row m sits at c ^ (m & 15): the 16 rows a
+/// quarter-wave reads hit 16 distinct slots), and the B operand is a 4-byte
+/// read of 32 consecutive columns. One barrier per K step; every step issues
+/// exactly one stage (past the end a harmless reload into a slot nothing
+/// reads), so the wait before the barrier is a constant vmcnt. Needs K a
+/// multiple of 64. Each output's sum runs over k in a different order from
+/// form 1's k ascending, within the f32 tolerance.
+constexpr int kQK = 64, kQStages = 4;
+constexpr int kQA = kFM * kQK;                        // floats per A stage (64 rows x 64 k)
+constexpr int kQStage = 2 * kQA;                      // A, then B (64 k x 64 n)
+constexpr size_t kLdsF32Dma = static_cast<size_t>(kQStages) * kQStage * sizeof(float);   // 128 KiB
+
+template <bool ACC>
+__global__ __launch_bounds__(256, 1) void gemmF32Dma(const float* __restrict__ A, const float* __restrict__ B,
+                                                     float* __restrict__ C, int N, int K, int64_t lda,
+                                                     int64_t ldb, int64_t ldc) {
+    extern __shared__ __align__(16) float ldsF[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int tilesN = N / kFN;
+    const int64_t row0 = static_cast<int64_t>(blockIdx.x / tilesN) * kFM;
+    const int64_t col0 = static_cast<int64_t>(blockIdx.x % tilesN) * kFN;
+    const int steps = K / kQK;
+    // Stage `slot` receives K step min(slot, steps - 1) in ring slot
+    // slot % kQStages. A is 64 rows of 256 bytes and B 64 k-rows of 256
+    // bytes, 16 direct loads of 4 rows each: wave w issues instructions
+    // 4w .. 4w + 3 of each.
+    auto issue = [&](int slot) {
+        const int k0 = min(slot, steps - 1) * kQK;
+        const float* st = ldsF + (slot % kQStages) * kQStage;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int ins = wave * 4 + j;
+            const int row = ins * 4 + (lane >> 4);
+            const int c = (lane & 15) ^ (row & 15);
+            dmaLoad16(reinterpret_cast<const _Float16*>(A + (row0 + row) * lda + k0 + c * 4),
+                      reinterpret_cast<const _Float16*>(st + ins * 256));
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int ins = wave * 4 + j;
+            const int krow = ins * 4 + (lane >> 4);
+            dmaLoad16(reinterpret_cast<const _Float16*>(B + static_cast<int64_t>(k0 + krow) * ldb + col0 +
+                                                        (lane & 15) * 4),
+                      reinterpret_cast<const _Float16*>(st + kQA + ins * 256));
+        }
+    };
+    f32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < kQStages - 1; ++s) issue(s);
+    const int l32 = lane & 31, hl = lane >> 5;
+    const int m = wm * 32 + l32;
+    // A: row m, chunks 8 hl .. 8 hl + 7 (k 32 hl .. + 31) at their slots.
+    uint32_t offA[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) offA[q] = 4u * static_cast<uint32_t>(m * kQK + (((8 * hl + q) ^ (m & 15)) * 4));
+    // B: k-row 32 hl + t, column wn * 32 + l32.
+    const uint32_t offB = 4u * static_cast<uint32_t>(kQA + 32 * hl * kFN + wn * 32 + l32);
+    const uint32_t ldsBase = ldsOffset(ldsF);
+    // Stage 0 landed (stages 1 and 2, 8 direct loads each per wave, may be
+    // in flight).
+    asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    asm volatile("s_barrier" ::: "memory");
+    for (int s = 0; s < steps; ++s) {
+        const uint32_t cb = ldsBase + 4u * static_cast<uint32_t>((s % kQStages) * kQStage);
+        f32x4 a[8];
+        float b[32];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            a[q] = *reinterpret_cast<const __attribute__((address_space(3))) f32x4*>(cb + offA[q]);
+        }
+#pragma unroll
+        for (int t = 0; t < 32; ++t) {
+            b[t] = *reinterpret_cast<const __attribute__((address_space(3))) float*>(cb + offB + 4u * kFN * t);
+        }
+#pragma unroll
+        for (int t = 0; t < 32; ++t) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t >> 2][t & 3], b[t], acc, 0, 0, 0);
+        // Stage s + 1 landed (one later stage may be in flight); after the
+        // barrier every wave is past step s, so slot (s + 3) % 4, which held
+        // step s - 1, can be refilled.
+        asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        asm volatile("s_barrier" ::: "memory");
+        issue(s + kQStages - 1);
+    }
+    // No direct load may still be writing LDS when the workgroup ends.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    const int64_t cBase = col0 + wn * 32 + l32;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int64_t row = row0 + wm * 32 + 8 * (r >> 2) + 4 * hl + (r & 3);
         float* dst = C + row * ldc + cBase;
         *dst = ACC ? *dst + acc[r] : acc[r];
     }
@@ -1414,6 +1521,27 @@ extern "C" int mlkd_launch_gemm(const mlkd_gemm* p, void* stream) {
         p->c_dtype == MLKD_F32 && p->m % kFM == 0 && p->n % kFN == 0 && p->k % kFK == 0 &&
         p->lda % 4 == 0 && p->ldb % 4 == 0 && aligned16(p->a) && aligned16(p->b)) {
         const int tiles = static_cast<int>((p->m / kFM) * (p->n / kFN));
+        // f32 forms: 0 (the default) direct to the LDS ring, 1 register-staged.
+        const int fv = p->variant >= 0 ? p->variant : 0;
+        if (fv != 1 && p->k % kQK == 0) {
+            static bool raisedF = false;
+            if (!raisedF) {
+                if (hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF32Dma<true>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        static_cast<int>(kLdsF32Dma)) != hipSuccess ||
+                    hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF32Dma<false>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        static_cast<int>(kLdsF32Dma)) != hipSuccess) {
+                    return MLKD_RT_LAUNCH;
+                }
+                raisedF = true;
+            }
+            hipLaunchKernelGGL((p->accumulate ? gemmF32Dma<true> : gemmF32Dma<false>), dim3(tiles), dim3(256),
+                               kLdsF32Dma, st, static_cast<const float*>(p->a), static_cast<const float*>(p->b),
+                               static_cast<float*>(p->c), static_cast<int>(p->n), static_cast<int>(p->k), p->lda,
+                               p->ldb, p->ldc);
+            return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
+        }
         hipLaunchKernelGGL((p->accumulate ? gemmF32Mfma<true> : gemmF32Mfma<false>), dim3(tiles), dim3(256), 0, st,
                            static_cast<const float*>(p->a), static_cast<const float*>(p->b),
                            static_cast<float*>(p->c), static_cast<int>(p->m), static_cast<int>(p->n),

@@ -372,6 +372,12 @@ std::vector<int> variantSpace(const KernelModule& km, const Step& st) {
                 st.n % 256 == 0 && st.k % 64 == 0 && st.k > 0) {
                 return {8, 7, 0, 1, 2, 3, 5, 6};
             }
+            // f32: 0, both tiles direct to a 4-deep LDS ring (K % 64); 1,
+            // register-staged with A transposed.
+            if (dt(st.a) == Dtype::F32 && dt(st.b) == Dtype::F32 && dt(st.c) == Dtype::F32 && st.m % 64 == 0 &&
+                st.n % 64 == 0 && st.k % 64 == 0 && st.k > 0) {
+                return {0, 1};
+            }
             return {};
         case StepKind::ScoreSoftmax:
             // 0: two-pass query-stationary (the default); 1: scores, then the

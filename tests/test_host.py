@@ -207,7 +207,8 @@ def test_chain_codegen_exact_constants():
     (fx.score_softmax_module(2, 4096, 128), [0, 1]),
     (fx.score_softmax_module(2, 256, 128), [0, 1]),
     (fx.score_softmax_module(2, 384, 128), []),
-    (fx.config4_module(1024, 1024, 1024, "f32", 2), []),
+    (fx.config4_module(1024, 1024, 1024, "f32", 2), [0, 1]),
+    (fx.config4_module(64, 32, 64, "f32", 2), []),      # K below the 64-deep ring steps
     (fx.config1_module(1 << 12), []),
     (fx.config4_module(64, 64, 64, "f16", 1), []),     # below the 256-multiple tiles
     (tn.generic(tn.weighted_rows_module()), [0, 1]),  # loop nest with LDS slabs, and without

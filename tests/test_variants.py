@@ -62,6 +62,17 @@ def _gemm_case(m=512, k=1024, n=512):
     return km, bufs, 2, ref, 1e-2
 
 
+def _gemm_f32_case(m=256, k=1024, n=512):
+    # f32 forms 0 (direct to the LDS ring, k permuted within a step) and 1
+    # (register-staged, k ascending): within 1e-5 sqrt(k) of the f64 product.
+    d = inputs.config_inputs("c4a", {"m": m, "k": k, "n": n})
+    km = fx.config4_module(m, k, n, "f32", 2)
+    ref = _gemm_ref(d["A"].astype(np.float64), d["B"].astype(np.float64)).reshape(-1)
+    bufs = {0: DeviceBuffer.from_array(d["A"], "f32"), 1: DeviceBuffer.from_array(d["B"], "f32"),
+            2: DeviceBuffer(m * n, "f32")}
+    return km, bufs, 2, ref, 1e-5 * math.sqrt(k)
+
+
 def _score_case(b=2, s=512, dm=128):
     d = inputs.config_inputs("c5", {"batch": b, "seq": s, "dim": dm})
     km = fx.score_softmax_module(b, s, dm)
@@ -109,6 +120,7 @@ CASES = {
     "softmax-333x1000": lambda: _softmax_case(333, 1000),
     "softmax-70001x8": lambda: _softmax_case(70001, 8),
     "gemm-f16-512x1024x512": _gemm_case,
+    "gemm-f32-256x1024x512": _gemm_f32_case,
     "score-2x512x128": _score_case,
     "score-1x2048x128": lambda: _score_case(1, 2048, 128),
     "nest-slabs-64x256x41": _nest_case,
@@ -224,13 +236,13 @@ def test_autotune_certifies_restores_and_caches(hip, name, tmp_path):
 
 
 def test_autotune_without_variants_is_a_no_op(hip):
-    # An f32 GEMM has one form: the search times nothing and keeps defaults.
-    m = k = n = 256
-    d = inputs.config_inputs("c4a", {"m": m, "k": k, "n": n})
-    km = fx.config4_module(m, k, n, "f32", 2)
+    # A 1-D elementwise chain has one form: the search times nothing and
+    # keeps defaults.
+    n = 1 << 16
+    d = inputs.config_inputs("c1", {"n": n})
+    km = fx.config1_module(n=n)
     art = hip.build(km)
-    bufs = {0: DeviceBuffer.from_array(d["A"], "f32"), 1: DeviceBuffer.from_array(d["B"], "f32"),
-            2: DeviceBuffer(m * n, "f32")}
+    bufs = {0: DeviceBuffer.from_array(d["x"], "f32"), 1: DeviceBuffer(n, "f32")}
     rep = art.autotune(bufs, reps=3)
     assert rep["steps"] == [] and rep["variants"] == [-1]
     assert rep["cache"]["file"] == ""
