@@ -275,6 +275,9 @@ def _gemm_ref(A, B):
 
 
 @pytest.mark.parametrize("m,k,n,tier", [(1024, 1024, 1024, 2), (1024, 1024, 1024, 1),
+                                        (64, 64, 64, 2),      # f32 form 0: one K step
+                                        (192, 128, 320, 2),   # form 0: two steps, 3 x 5 tiles
+                                        (128, 96, 64, 2),     # K % 64 != 0: form 1
                                         (64, 32, 64, 2), (100, 70, 33, 2)])
 def test_c4a_gemm_f32(hip, m, k, n, tier):
     say(f"c4a gemm f32 {m}x{k}x{n} tier{tier}")
