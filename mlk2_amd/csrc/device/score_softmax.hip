@@ -83,8 +83,9 @@ typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 //   exp(v - max) / sum for the panel at once: each 32-lane half-wave stores
 //   one 128-byte line, while the other workgroup on the CU computes.
 // Both passes work in base 2 with log2(e) folded into 1/div and the bias, so
-// a score costs one fused multiply-add and one v_exp_f32: the passes are
-// bound by VALU work (67M exponentials each), not by the MFMAs.
+// a score costs one fused multiply-add and one v_exp_f32. Pass 2 is bound by
+// its stores (256 MiB in the MFMA output layout); pass 1 by its MFMAs and
+// the VALU work per score together.
 constexpr int kPanelQ = 128;                   // keys per streamed panel
 constexpr float kLog2e = 1.44269504088896340736f;
 constexpr int kRowQ = kD2 + 8;                 // halves per LDS panel row
