@@ -174,8 +174,8 @@ def test_set_variant_outside_space_refused(hip):
     assert art.step_variant(7) == -2
 
 
-@pytest.mark.parametrize("name", ["softmax-512x4096", "gemm-f16-512x1024x512", "score-2x512x128",
-                                  "nest-slabs-64x256x41"])
+@pytest.mark.parametrize("name", ["softmax-512x4096", "gemm-f16-512x1024x512", "gemm-f32-256x1024x512",
+                                  "score-2x512x128", "nest-slabs-64x256x41"])
 def test_autotune_certifies_restores_and_caches(hip, name, tmp_path):
     km, bufs, out, ref, tol = CASES[name]()
     # A sentinel in the output: the search must hand the buffer back as it was.
