@@ -300,7 +300,6 @@ std::string launchCoverage(const KernelModule& km, const Step& st, int64_t eleme
     // exactly once. Grid-stride forms cover any instance count; tiled forms
     // cover when the tile divides the extent (the launcher checks the same
     // divisibility and falls back to the bounds-checked general kernel).
-    (void)km;
     int64_t instances = 0, workgroups = 0, perGroup = 0;
     bool covered = true;
     const char* form = "";
@@ -331,12 +330,23 @@ std::string launchCoverage(const KernelModule& km, const Step& st, int64_t eleme
             form = "rows over waves, grid-stride";
             break;
         case StepKind::Gemm: {
+            // f16 x f16 -> f32 with M, N % 256 and K % 64 runs the MFMA forms
+            // on 256 x 256 tiles (forms 5 and 6: 128 x 256); f32 with M, N % 64
+            // and K % 32 the 64 x 64 MFMA tiles; anything else the
+            // bounds-checked 64 x 64 general kernel.
             instances = st.m * st.n;
-            const bool tiled = st.m % 256 == 0 && st.n % 256 == 0;
-            workgroups = tiled ? (st.m / 256) * (st.n / 256) : ((st.m + 63) / 64) * ((st.n + 63) / 64);
-            perGroup = tiled ? 256 * 256 : 64 * 64;
+            auto dt = [&](uint32_t b) { return km.buffers[b].dtype; };
+            const bool f16 = dt(st.a) == Dtype::F16 && dt(st.b) == Dtype::F16 && dt(st.c) == Dtype::F32 &&
+                             st.m % 256 == 0 && st.n % 256 == 0 && st.k % 64 == 0 && st.k > 0;
+            const bool f32 = dt(st.a) == Dtype::F32 && dt(st.b) == Dtype::F32 && dt(st.c) == Dtype::F32 &&
+                             st.m % 64 == 0 && st.n % 64 == 0 && st.k % 32 == 0 && st.k > 0;
+            const bool half = f16 && (st.variant == 5 || st.variant == 6);
+            const int64_t tm = f16 ? (half ? 128 : 256) : 64, tn = f16 ? 256 : 64;
+            workgroups = ((st.m + tm - 1) / tm) * ((st.n + tn - 1) / tn);
+            perGroup = tm * tn;
             covered = workgroups * perGroup >= instances;
-            form = tiled ? "256 x 256 output tiles" : "64 x 64 output tiles, bounds-checked";
+            form = f16 ? (half ? "128 x 256 output tiles, two workgroups per CU" : "256 x 256 output tiles")
+                       : f32 ? "64 x 64 output tiles" : "64 x 64 output tiles, bounds-checked";
             break;
         }
         case StepKind::ScoreSoftmax: {
