@@ -19,7 +19,9 @@ import numpy as np
 from .kernel_ir import KernelModule
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "lib", "libmlk_hip.so")
+# MLK_HIP_LIB names another build of the same library (the host-sanitized
+# one that tests/test_host_sanitizers.py links); by default the in-tree one.
+LIB_PATH = os.environ.get("MLK_HIP_LIB") or os.path.join(HERE, "lib", "libmlk_hip.so")
 
 OK, NEG_STORE, RUNTIME, LAUNCH, NO_DEVICE, BAD_BINDING, REFUSED = 0, 1, 2, 3, 4, 6, 7
 F32, F16, F64 = 0, 1, 2

@@ -81,6 +81,13 @@ def run(src: str, dtypes: Dict[int, str], arrays: Dict[int, np.ndarray], scalars
             f.write(bytes(blob))
         env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=0:exitcode=23",
                    UBSAN_OPTIONS="print_stacktrace=1:halt_on_error=1:exitcode=24")
+        # Inside the host-sanitizer run the parent preloads clang's ASan
+        # runtime; this harness links gcc's, and two runtimes refuse to mix.
+        pre = [e for e in env.get("LD_PRELOAD", "").split(":") if e and "libclang_rt.asan" not in e]
+        if pre:
+            env["LD_PRELOAD"] = ":".join(pre)
+        else:
+            env.pop("LD_PRELOAD", None)
         r = subprocess.run([exe, fin, fout] + (["r"] if reverse else []), stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
                            text=True, env=env, timeout=300)
         if r.returncode != 0:
