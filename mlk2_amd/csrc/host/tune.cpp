@@ -322,12 +322,39 @@ std::string launchCoverage(const KernelModule& km, const Step& st, int64_t eleme
             perGroup = 256;
             form = "grid-stride over the collapsed parallel loops";
             break;
-        case StepKind::Softmax:
+        case StepKind::Softmax: {
+            // f32 rows of at most 8192 (cols % 4 == 0) run the wave path:
+            // form 5 (the default) two rows per wave, form 1 a fixed grid of
+            // 2048 waves, the other forms a row per wave, at most 8192
+            // workgroups; anything else a workgroup per row.
+            instances = st.rows;
+            auto dt = [&](uint32_t b) { return km.buffers[b].dtype; };
+            const bool wave = dt(st.x) == Dtype::F32 && dt(st.y) == Dtype::F32 && st.cols % 4 == 0 && st.cols <= 8192;
+            const int v = st.variant >= 0 ? st.variant : 5;
+            if (!wave) {
+                workgroups = std::min<int64_t>(std::max<int64_t>(st.rows, 1), 65536);
+                perGroup = 1;
+                form = "a workgroup per row, grid-stride";
+            } else if (v == 5) {
+                workgroups = std::min<int64_t>(std::max<int64_t>(((st.rows + 1) / 2 + 3) / 4, 1), 8192);
+                perGroup = 8;
+                form = "two adjacent rows per wave, grid-stride";
+            } else if (v == 1) {
+                workgroups = (std::min<int64_t>(std::max<int64_t>(st.rows, 1), 2048) + 3) / 4;
+                perGroup = 4;
+                form = "rows pipelined over a fixed grid of waves";
+            } else {
+                workgroups = std::min<int64_t>(std::max<int64_t>((st.rows + 3) / 4, 1), 8192);
+                perGroup = 4;
+                form = "a row per wave, grid-stride";
+            }
+            break;
+        }
         case StepKind::RowSum:
             instances = st.rows;
-            workgroups = std::min<int64_t>(std::max<int64_t>((st.rows + 3) / 4, 1), 65536);
+            workgroups = std::min<int64_t>(std::max<int64_t>((st.rows + 3) / 4, 1), 16384);
             perGroup = 4;
-            form = "rows over waves, grid-stride";
+            form = "a row per wave, grid-stride";
             break;
         case StepKind::Gemm: {
             // f16 x f16 -> f32 with M, N % 256 and K % 64 runs the MFMA forms
@@ -665,11 +692,14 @@ int HipLoadedKernel::autotune(const DeviceBinding* binds, int n, const double* s
                      ",\"reps\":" + std::to_string(admissible ? reps : 0) + ",\"warmup\":" +
                      std::to_string(admissible ? kWarmup : 0) + "}}}";
         }
+        // The launch certificate is that of the chosen form.
+        plan_.steps[si].variant = chosen[si];
+        const std::string launch = launchCoverage(km_, plan_.steps[si], elements);
         plan_.steps[si].variant = -1;
         if (!steps.empty()) steps += ",";
         steps += "{\"step\":" + std::to_string(si) + ",\"class\":\"" + plan_.steps[si].what + "\",\"kernel\":\"" +
                  kindName(plan_.steps[si].kind) + "\",\"chosen\":" + std::to_string(chosen[si]) +
-                 ",\"launch\":" + launchCoverage(km_, plan_.steps[si], elements) + ",\"candidates\":[" + cands + "]}";
+                 ",\"launch\":" + launch + ",\"candidates\":[" + cands + "]}";
     }
     for (size_t i = 0; i < plan_.steps.size(); ++i) plan_.steps[i].variant = chosen[i];
     bool combined = true;

@@ -24,6 +24,24 @@ from mlk2_amd.parity import max_rel
 pytestmark = pytest.mark.gpu
 
 
+def launched_workgroups(name, v):
+    """Workgroups the launcher of form `v` starts for the autotune cases, from
+    the launchers: softmax form 5 two rows per wave (4 waves a workgroup),
+    form 1 a grid of min(rows, 2048) waves, the others a row per wave; f16
+    GEMM forms 5 and 6 on 128 x 256 tiles, the others 256 x 256; f32 GEMM
+    64 x 64; score-softmax form 0 128 rows x 2 key halves per pass, form 1
+    64 x 128 score tiles. The launch certificate must name the chosen form's
+    geometry."""
+    if name == "softmax-512x4096":
+        return {5: (256 + 3) // 4, 1: (512 + 3) // 4}.get(v, (512 + 3) // 4)
+    if name == "gemm-f16-512x1024x512":
+        return (512 // 128) * (512 // 256) if v in (5, 6) else (512 // 256) ** 2
+    if name == "gemm-f32-256x1024x512":
+        return (256 // 64) * (512 // 64)
+    if name == "score-2x512x128":
+        return 2 * (512 // 128) * 2 if v != 1 else 2 * (512 // 64) * (512 // 128)
+    return None
+
 def say(msg):
     print(f"[gpu] {msg}", flush=True)
     sys.stdout.flush()
@@ -213,6 +231,9 @@ def test_autotune_certifies_restores_and_caches(hip, name, tmp_path):
     assert rep["roofline_lower_sec"] > 0 and rep["winner_sec"] > rep["roofline_lower_sec"]
     assert abs(rep["winner_gap_over_lower"] - (rep["winner_sec"] / rep["roofline_lower_sec"] - 1)) < 1e-3
     assert step["launch"]["covered"] and step["launch"]["workgroups"] > 0
+    expect = launched_workgroups(name, step["chosen"])
+    if expect is not None:
+        assert step["launch"]["workgroups"] == expect, (name, step["chosen"], step["launch"])
     env = rep["environment"]
     assert 1e12 < env["measured_bytes_per_sec"] < 1e13 and 1e14 < env["measured_f16_flops_per_sec"] < 3e15
     assert rep["roofline_lower_sec_measured"] >= rep["roofline_lower_sec"]
