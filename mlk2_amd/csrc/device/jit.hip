@@ -236,14 +236,16 @@ int mlkd_jit_launch_elementwise(void* fn, unsigned grid, const void* const* in, 
     return e == hipSuccess ? 0 : MLKD_RT_LAUNCH;
 }
 
-/// Launches a generic loop-nest instance, 256 threads per workgroup.
-int mlkd_jit_launch_nest(void* fn, unsigned grid, const mlkd_nest_args* args,
+/// Launches a generic loop-nest instance, `block` threads per workgroup (the
+/// instance's MLK_NEST_WG).
+int mlkd_jit_launch_nest(void* fn, unsigned grid, unsigned block, const mlkd_nest_args* args,
                          const mlkd_scalars* scalars, long long total, void* stream) {
+    if (block == 0 || block > 1024) return MLKD_RT_LAUNCH;
     mlkd_nest_args a = *args;
     mlkd_scalars sc = *scalars;
     long long t = total;
     void* kargs[] = {&a, &sc, &t};
-    const hipError_t e = hipModuleLaunchKernel(static_cast<hipFunction_t>(fn), grid, 1, 1, 256, 1, 1, 0,
+    const hipError_t e = hipModuleLaunchKernel(static_cast<hipFunction_t>(fn), grid, 1, 1, block, 1, 1, 0,
                                                static_cast<hipStream_t>(stream), kargs, nullptr);
     return e == hipSuccess ? 0 : MLKD_RT_LAUNCH;
 }

@@ -71,8 +71,9 @@ typedef struct {
     long long elements;
 } mlkd_nest_args;
 
-/// Launches a loop-nest instance: (mlkd_nest_args, scalars, long long total).
-int mlkd_jit_launch_nest(void* fn, unsigned grid, const mlkd_nest_args* args,
+/// Launches a loop-nest instance: (mlkd_nest_args, scalars, long long total),
+/// `block` threads per workgroup.
+int mlkd_jit_launch_nest(void* fn, unsigned grid, unsigned block, const mlkd_nest_args* args,
                          const mlkd_scalars* scalars, long long total, void* stream);
 int mlkd_launch_rowsum(const mlkd_softmax* p, void* stream);
 

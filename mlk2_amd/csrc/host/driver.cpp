@@ -15,8 +15,8 @@ namespace {
 
 int dtypeCode(Dtype d) { return d == Dtype::F32 ? MLKD_F32 : (d == Dtype::F16 ? MLKD_F16 : MLKD_F64); }
 
-unsigned gridFor(int64_t threads) {
-    int64_t blocks = (threads + 255) / 256;
+unsigned gridFor(int64_t threads, int64_t perGroup = 256) {
+    int64_t blocks = (threads + perGroup - 1) / perGroup;
     // Grid-stride beyond 64 workgroups of 4 waves per CU on 256 CUs.
     if (blocks > 16384) blocks = 16384;
     if (blocks < 1) blocks = 1;
@@ -118,7 +118,7 @@ Result<std::unique_ptr<HipLoadedKernel>> buildHipKernelArtifact(const KernelModu
     }
     k->fingerprint_ = artifactFingerprint(k->km_, k->plan_, config.arch);
     k->fromCache_ = applyCachedVariants(config.cacheDir, k->fingerprint_, k->km_, k->plan_);
-    k->noSlabFn_.assign(k->plan_.steps.size(), nullptr);
+    k->nestFormFn_.assign(k->plan_.steps.size(), std::array<void*, 4>{nullptr, nullptr, nullptr, nullptr});
     return k;
 }
 
@@ -191,8 +191,9 @@ int HipLoadedKernel::arenaLayout(const DeviceBinding* binds, int64_t elements, c
                   "read-back, which the allocation-free entry does not do";
             return MLKHIP_REFUSED;
         }
-        if (st.kind == StepKind::Nest && st.variant == 1 && !st.sourceNoSlabs.empty() && noSlabFn_[si] == nullptr) {
-            why = "step " + std::to_string(si) + " pins the loop nest's no-slab form, which is not loaded yet";
+        if (st.kind == StepKind::Nest && st.variant >= 1 && st.variant <= 3 && nestFormFn_[si][st.variant] == nullptr) {
+            why = "step " + std::to_string(si) + " pins loop-nest launch form " + std::to_string(st.variant) +
+                  ", which is not loaded yet";
             return MLKHIP_REFUSED;
         }
         if (st.kind == StepKind::ScoreSoftmax) {
@@ -414,21 +415,28 @@ int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* 
                     na.status = static_cast<int*>(status);
                 }
                 void* fn = st.fn;
-                if (st.variant == 1 && !st.sourceNoSlabs.empty()) {
+                const int form = st.variant >= 1 && st.variant <= 3 ? st.variant : 0;
+                const unsigned wg = nestFormThreads(form);
+                if (form != 0) {
                     std::lock_guard<std::mutex> g(scratchLock_);
-                    if (noSlabFn_[si] == nullptr) {
+                    if (nestFormFn_[si][form] == nullptr) {
+                        const std::string src = nestFormSource(st, form);
+                        if (src.empty()) {
+                            why = "loop-nest launch form " + std::to_string(form) + " is not declared for this step";
+                            return MLKHIP_REFUSED;
+                        }
                         char log[4096] = {0};
                         uint64_t fp = 0;
-                        if (mlkd_jit_build(st.sourceNoSlabs.data(), st.sourceNoSlabs.size(), "mlk_nest", arch_.c_str(),
-                                           cacheDir_.c_str(), &noSlabFn_[si], &fp, log, sizeof(log)) != 0) {
-                            noSlabFn_[si] = nullptr;
-                            why = std::string("loop-nest instance without slabs: ") + log;
+                        if (mlkd_jit_build(src.data(), src.size(), "mlk_nest", arch_.c_str(), cacheDir_.c_str(),
+                                           &nestFormFn_[si][form], &fp, log, sizeof(log)) != 0) {
+                            nestFormFn_[si][form] = nullptr;
+                            why = "loop-nest launch form " + std::to_string(form) + ": " + log;
                             return MLKHIP_RUNTIME;
                         }
                     }
-                    fn = noSlabFn_[si];
+                    fn = nestFormFn_[si][form];
                 }
-                rc = mlkd_jit_launch_nest(fn, gridFor(st.threads), &na, &sc, st.threads, stream);
+                rc = mlkd_jit_launch_nest(fn, gridFor(st.threads, wg), wg, &na, &sc, st.threads, stream);
                 if (rc == 0 && st.checked) {
                     int code = 0;
                     if (mlkd_rt_d2h(&code, status, sizeof(code), stream) != 0 || mlkd_rt_sync(stream) != 0) {

@@ -999,11 +999,16 @@ struct mlk_nest_args {
     long long elements;
 };
 
+// Threads per workgroup: 256 unless the launch form defines another.
+#ifndef MLK_NEST_WG
+#define MLK_NEST_WG 256
+#endif
+
 // The workgroup's threads share each slab's copy; a host harness that runs
 // one thread at a time defines these to copy the whole slab per thread.
 #ifndef MLK_SLAB_FIRST
 #define MLK_SLAB_FIRST static_cast<long long>(threadIdx.x)
-#define MLK_SLAB_STEP 256
+#define MLK_SLAB_STEP MLK_NEST_WG
 #endif
 
 template <int DT>
@@ -1016,7 +1021,7 @@ __device__ __forceinline__ double mlk_ld_chk(const void* p, long long f, long lo
     return mlk::loadOne<DT>(p, f);
 }
 
-extern "C" __global__ __launch_bounds__(256) void mlk_nest(const mlk_nest_args a, const mlk_scalars sc,
+extern "C" __global__ __launch_bounds__(MLK_NEST_WG) void mlk_nest(const mlk_nest_args a, const mlk_scalars sc,
                                                            long long total) {
     (void)sc;
 )";
@@ -1034,8 +1039,9 @@ extern "C" __global__ __launch_bounds__(256) void mlk_nest(const mlk_nest_args a
                "[i] = static_cast<const " + ty + "*>(" + mb + ")[" + intLit(sl.lo) + " + i];\n";
     }
     if (!em.slabs.empty()) src += "    __syncthreads();\n";
-    src += "    const long long stride = static_cast<long long>(gridDim.x) * 256;\n";
-    src += "    for (long long g = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; g < total; g += stride) {\n";
+    src += "    const long long stride = static_cast<long long>(gridDim.x) * MLK_NEST_WG;\n";
+    src += "    for (long long g = static_cast<long long>(blockIdx.x) * MLK_NEST_WG + threadIdx.x; g < total; "
+           "g += stride) {\n";
     src += chainLen > 0 ? chainCodeText : "        (void)g;\n";
     src += em.code;
     src += "    }\n}\n";
@@ -1079,6 +1085,23 @@ Result<Step> planNest(const KernelModule& km, uint32_t root) {
     if (!plain.has_value() || plain->nestBufs != st->nestBufs) return st;   // same slots: one binding serves both
     st->sourceNoSlabs = std::move(plain->source);
     return st;
+}
+
+std::vector<int> nestForms(const Step& st) {
+    if (!st.sourceNoSlabs.empty()) return {0, 1, 2, 3};
+    return {0, 2, 3};
+}
+
+unsigned nestFormThreads(int form) { return form == 2 ? 512u : (form == 3 ? 64u : 256u); }
+
+std::string nestFormSource(const Step& st, int form) {
+    switch (form) {
+        case 0: return st.source;
+        case 1: return st.sourceNoSlabs;
+        case 2:
+        case 3: return "#define MLK_NEST_WG " + std::to_string(nestFormThreads(form)) + "\n" + st.source;
+        default: return std::string();
+    }
 }
 
 }  // namespace mlk::hip

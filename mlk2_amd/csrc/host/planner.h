@@ -136,6 +136,17 @@ KernelModule canonicalModule(const KernelModule& km, int* rewrites);
 /// collapsed onto threads. The step's `source` holds the hipRTC text.
 Result<Step> planNest(const KernelModule& km, uint32_t root);
 
+/// Launch forms of a loop-nest step (nestgen.cpp): 0 the step's own kernel
+/// (its LDS slabs, 256 threads per workgroup); 1 the same kernel without
+/// slabs (declared only where the step has slabs); 2 and 3 form 0 with 512
+/// and 64 threads per workgroup. Every form runs each instance's code
+/// unchanged, so all give the same bits.
+std::vector<int> nestForms(const Step& st);
+/// Threads per workgroup of loop-nest form `form`.
+unsigned nestFormThreads(int form);
+/// hipRTC source of loop-nest form `form` of `st` (empty if not declared).
+std::string nestFormSource(const Step& st, int form);
+
 /// Hex-float literal of an f64 constant (exact), or the non-finite builtins.
 std::string literal(double v);
 

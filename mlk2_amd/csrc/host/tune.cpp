@@ -316,12 +316,14 @@ std::string launchCoverage(const KernelModule& km, const Step& st, int64_t eleme
             form = "grid-stride 512-element segments, one per wave";
             break;
         }
-        case StepKind::Nest:
+        case StepKind::Nest: {
+            const int64_t wg = nestFormThreads(st.variant >= 0 ? st.variant : 0);
             instances = st.threads;
-            workgroups = std::min<int64_t>(std::max<int64_t>((st.threads + 255) / 256, 1), 16384);
-            perGroup = 256;
+            workgroups = std::min<int64_t>(std::max<int64_t>((st.threads + wg - 1) / wg, 1), 16384);
+            perGroup = wg;
             form = "grid-stride over the collapsed parallel loops";
             break;
+        }
         case StepKind::Softmax: {
             // f32 rows of at most 8192 (cols % 4 == 0) run the wave path:
             // form 5 (the default) two rows per wave, form 1 a fixed grid of
@@ -425,9 +427,10 @@ std::vector<int> variantSpace(const KernelModule& km, const Step& st) {
             }
             return {};
         case StepKind::Nest:
-            // 0: with the step's LDS slabs; 1: the same kernel without them.
-            if (!st.sourceNoSlabs.empty()) return {0, 1};
-            return {};
+            // 0: with the step's LDS slabs; 1: the same kernel without them
+            // (where it has slabs); 2, 3: form 0 at 512 and 64 threads per
+            // workgroup.
+            return nestForms(st);
         default: return {};
     }
 }

@@ -52,11 +52,12 @@ int main(int argc, char** argv) {
     a.status = &status;
     a.elements = elements;
     gridDim.x = static_cast<unsigned>(grid);
-    blockDim.x = 256;
-    for (int64_t i = 0; i < grid * 256; ++i) {
-        const int64_t g = reverse ? grid * 256 - 1 - i : i;
-        blockIdx.x = static_cast<unsigned>(g / 256);
-        threadIdx.x = static_cast<unsigned>(g % 256);
+    const int64_t wg = MLK_NEST_WG;   // the instance's workgroup size (256 unless its launch form sets another)
+    blockDim.x = static_cast<unsigned>(wg);
+    for (int64_t i = 0; i < grid * wg; ++i) {
+        const int64_t g = reverse ? grid * wg - 1 - i : i;
+        blockIdx.x = static_cast<unsigned>(g / wg);
+        threadIdx.x = static_cast<unsigned>(g % wg);
         mlk_nest(a, sc, total);
     }
     FILE* o = fopen(argv[2], "wb");

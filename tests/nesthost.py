@@ -34,9 +34,16 @@ def parse_header(src: str) -> Tuple[List[int], int]:
     return slots, total
 
 
-def grid_for(threads: int) -> int:
+def workgroup_size(src: str) -> int:
+    """Threads per workgroup of an instance: 256, or what its launch form's
+    leading `#define MLK_NEST_WG` sets."""
+    m = re.match(r"#define MLK_NEST_WG (\d+)\n", src)
+    return int(m.group(1)) if m else 256
+
+
+def grid_for(threads: int, wg: int = 256) -> int:
     """The driver's launch grid for `threads` instances (gridFor)."""
-    return max(1, min((threads + 255) // 256, 16384))
+    return max(1, min((threads + wg - 1) // wg, 16384))
 
 
 def build(src: str) -> str:
@@ -74,7 +81,7 @@ def run(src: str, dtypes: Dict[int, str], arrays: Dict[int, np.ndarray], scalars
         blob += struct.pack("<iq", code, a.size) + a.tobytes()
     sc = list(scalars)[:8] + [0.0] * (8 - min(8, len(scalars)))
     blob += struct.pack("<8d", *sc)
-    blob += struct.pack("<qqq", elements, total, grid_for(total))
+    blob += struct.pack("<qqq", elements, total, grid_for(total, workgroup_size(src)))
     with tempfile.TemporaryDirectory() as td:
         fin, fout = os.path.join(td, "in.bin"), os.path.join(td, "out.bin")
         with open(fin, "wb") as f:
@@ -105,12 +112,14 @@ def run(src: str, dtypes: Dict[int, str], arrays: Dict[int, np.ndarray], scalars
 
 
 def run_module(km, arrays: Dict[int, np.ndarray], scalars: Sequence[float] = (), elements: int = 0,
-               reverse: bool = False, skip_other: bool = False) -> Tuple[int, Dict[int, np.ndarray]]:
+               reverse: bool = False, skip_other: bool = False, wg: int = 0) -> Tuple[int, Dict[int, np.ndarray]]:
     """Runs every step of a module whose plan is all loop-nest steps, in order,
     the way the artifact does (temps zeroed first, held in f64). Returns the
     first nonzero status (or 0) and every buffer as f64. ``skip_other`` skips
     steps of other classes instead of refusing (an address check of the
-    loop-nest kernels only: the values are then not the module's)."""
+    loop-nest kernels only: the values are then not the module's). ``wg``
+    runs launch forms 2 and 3 (512 or 64 threads per workgroup): the form-0
+    source behind a leading `#define MLK_NEST_WG`, as the driver builds it."""
     from mlk2_amd import backend
     cls, _, nsteps = backend.plan(km)
     kinds = cls.split("+")
@@ -130,6 +139,8 @@ def run_module(km, arrays: Dict[int, np.ndarray], scalars: Sequence[float] = (),
         if kinds[s] != "loop-nest":
             raise ValueError(f"step {s} is a {kinds[s]} step, not a loop-nest step")
         _, src = backend.compile_check(km, s)
+        if wg:
+            src = f"#define MLK_NEST_WG {wg}\n" + src
         st, out = run(src, dtypes, cur, scalars, elements, reverse)
         for b, v in out.items():
             cur[b] = v.astype(np.float64)

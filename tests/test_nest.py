@@ -250,6 +250,32 @@ def test_slabs_host(dtype, stored_w):
     assert nf.same_bits(cur[2], want)
 
 
+@pytest.mark.parametrize("wg", [64, 512])
+@pytest.mark.parametrize("case", ["slabs-f64", "slabs-f16", "fuzz-3", "fuzz-11"])
+def test_workgroup_forms_host(case, wg):
+    # Launch forms 2 and 3 (512 and 64 threads per workgroup): the slab copy
+    # loop strides by the workgroup size and the grid-stride loop by the
+    # grid's thread count; under AddressSanitizer every access stays in
+    # bounds, and the bits are form 0's and the walker's.
+    if case.startswith("slabs"):
+        km = generic(weighted_rows_module(dtype=case.split("-")[1]))
+        arrays, scalars = weighted_rows_inputs(km), ()
+    else:
+        seed = int(case.split("-")[1])
+        km = generic(nf.random_module(seed))
+        arrays, scalars = nf.random_inputs(km, seed)
+    assert backend.plan_variants(km, 0)[-2:] == [2, 3]
+    st0, cur0 = nesthost.run_module(km, arrays, scalars)
+    st, cur = nesthost.run_module(km, arrays, scalars, reverse=True, wg=wg)
+    assert st == st0 == 0
+    ref = oracle.run(km, {i: arrays[i] for i in km.input_ids()}, scalars,
+                     init={i: arrays[i] for i in km.output_ids() if i in arrays})
+    for i in km.output_ids():
+        assert nf.same_bits(cur[i], cur0[i]), (case, wg, i)
+        if km.buffers[i].dtype == "f64":
+            assert nf.same_bits(cur[i], ref[i]), (case, wg, i)
+
+
 def test_tiled_gemm_collapses_all_parallel_levels():
     # Divisible sizes: one full tile part per level, i_t/i/j_t/j collapse.
     km = generic(fx.tiled_gemm_module(64, 32, 64, "f32", tile=16, init="split"), canonical=False)
