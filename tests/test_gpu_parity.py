@@ -15,6 +15,7 @@ import numpy as np
 import pytest
 
 import oracle
+from mlk2_amd import backend as be
 from mlk2_amd import fixtures as fx
 from mlk2_amd import inputs
 from mlk2_amd.backend import DeviceBuffer, MlkHipError
@@ -462,6 +463,34 @@ def test_c5_full_size_sampled_rows(hip):
         assert e <= 1e-2
     sums = got.reshape(b * s, s)[::97].astype(np.float64).sum(axis=1)
     assert np.abs(sums - 1.0).max() < 1e-3
+
+
+@pytest.mark.parametrize("s,two_pass", [(4096, True), (8192, True), (8448, False)])
+def test_c5_long_rows_sampled(hip, s, two_pass):
+    # The two-pass form up to its largest row (seq <= 8192: pass 1 keeps a
+    # key half's bias in LDS), and one row length past it, which takes the
+    # scores-then-softmax form with the workgroup-per-row softmax (rows
+    # longer than the wave path's 8192).
+    b, dm = 1, 128
+    say(f"c5 long rows b={b} s={s}, sampled rows")
+    d = inputs.config_inputs("c5", {"batch": b, "seq": s, "dim": dm})
+    km = fx.score_softmax_module(b, s, dm)
+    assert be.plan_variants(km, 0) == ([0, 1] if two_pass else [])
+    art = hip.build(km)
+    bufs = {0: DeviceBuffer.from_array(d["Q"], "f16"), 1: DeviceBuffer.from_array(d["K"], "f16"),
+            2: DeviceBuffer.from_array(d["bias"], "f32"), 3: DeviceBuffer(b * s * s, "f32")}
+    art.run_device(bufs)
+    got = bufs[3].to_numpy().reshape(s, s)
+    rows = np.random.default_rng(6).choice(s, 12, replace=False)
+    rows[0], rows[1] = 0, s - 1
+    ref = _score_ref(d["Q"], d["K"], d["bias"], rows=rows)
+    e = max_rel(got[rows], ref)
+    say(f"c5 long rows s={s} max_rel={e:.3e}")
+    assert e <= 1e-2
+    sums = got[::131].astype(np.float64).sum(axis=1)
+    assert np.abs(sums - 1.0).max() < 1e-3
+    for bb in bufs.values():
+        bb.free()
 
 
 # ------------------------------------------------------------- entries ----
