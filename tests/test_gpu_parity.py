@@ -138,7 +138,9 @@ def test_scalar_param_and_two_inputs_1d(hip):
                                         # more rows than the capped grid has waves (each
                                         # wave walks several pairs); a row length that is
                                         # not a multiple of 4 (block-per-row kernel)
-                                        ((70001, 8), 1), ((33, 101), 2)])
+                                        ((70001, 8), 1), ((33, 101), 2),
+                                        # the wave path's longest rows (32 float4 a lane)
+                                        ((5, 8192), 1), ((2, 8192), 2)])
 def test_c2_softmax(hip, shape, tier):
     m, k = shape
     say(f"c2 softmax {m}x{k} tier{tier}")
