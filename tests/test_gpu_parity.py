@@ -294,7 +294,9 @@ def test_c4a_gemm_f32(hip, m, k, n, tier):
     assert e <= 1e-5 * math.sqrt(k)
 
 
-@pytest.mark.parametrize("m,k,n", [(512, 4096, 512), (256, 64, 256), (300, 50, 70)])
+@pytest.mark.parametrize("m,k,n", [(512, 4096, 512), (256, 64, 256), (300, 50, 70),
+                                   (768, 128, 1280),   # 3 x 5 tiles: the row-major tile map
+                                   (256, 4160, 512)])  # 130 K steps of 32
 def test_c4b_gemm_f16(hip, m, k, n):
     say(f"c4b gemm f16 {m}x{k}x{n}")
     d = inputs.config_inputs("c4b", {"m": m, "k": k, "n": n})
@@ -340,6 +342,28 @@ def test_c4b_full_size_sampled_rows(hip):
     e = max_rel(got[rows], ref)
     say(f"c4b full max_rel(sampled)={e:.3e}")
     assert e <= 1e-2
+
+
+def test_c4b_blocked_tile_map_non_square(hip):
+    # 8 x 32 tiles of 256 x 256: a multiple of 256 tiles, so each XCD takes
+    # 4 x 8 blocks of tiles, here over a grid four blocks wide; sampled rows
+    # from every block row against the oracle's GEMM.
+    m, k, n = 2048, 256, 8192
+    say(f"c4b gemm f16 {m}x{k}x{n}, blocked tile map, sampled rows")
+    d = inputs.config_inputs("c4b", {"m": m, "k": k, "n": n})
+    km = fx.config4_module(m, k, n, "f16", 2)
+    art = hip.build(km)
+    bufs = {0: DeviceBuffer.from_array(d["A"], "f16"), 1: DeviceBuffer.from_array(d["B"], "f16"),
+            2: DeviceBuffer(m * n, "f32")}
+    art.run_device(bufs)
+    got = bufs[2].to_numpy().reshape(m, n)
+    rows = np.concatenate([np.arange(b * 1024, b * 1024 + 1024, 97) for b in range(2)])
+    ref = _gemm_ref(d["A"][rows].astype(np.float64), d["B"].astype(np.float64))
+    e = max_rel(got[rows], ref)
+    say(f"c4b blocked map max_rel(sampled)={e:.3e}")
+    assert e <= 1e-2
+    for bb in bufs.values():
+        bb.free()
 
 
 def test_matmul_call_accumulates_into_c(hip):
