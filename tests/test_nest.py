@@ -627,6 +627,33 @@ def test_fuzz_gpu(hip, seed):
             assert nf.same_bits(got[i], ref[i]), (seed, i)
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", [0, 2, 5, 11])
+def test_fuzz_every_nest_form_gpu(hip, seed):
+    # Every loop-nest launch form (slabs, no slabs, 512 and 64 threads per
+    # workgroup) pinned on every loop-nest step that declares it: the bits
+    # are the walker's for each.
+    km = generic(nf.random_module(seed), canonical=False)
+    arrays, scalars = nf.random_inputs(km, seed)
+    ref = oracle.run(km, {i: arrays[i] for i in km.input_ids()}, scalars,
+                     init={i: arrays[i] for i in km.output_ids()})
+    art = hip.build(km)
+    steps = art.num_steps()
+    for form in (0, 1, 2, 3):
+        pinned = 0
+        for s in range(steps):
+            space = art.step_variants(s)
+            if space:
+                art.set_step_variant(s, form if form in space else 0)
+                pinned += form in space
+        if form != 0 and pinned == 0:
+            continue
+        say(f"fuzz seed {seed}: nest form {form} on {pinned} step(s)")
+        got = art.run(arrays, scalars)
+        for i in km.output_ids():
+            assert nf.same_bits(got[i], ref[i]), (seed, form, i)
+
+
 def close_to_walker(got, ref, tol):
     """NaN where the walker has NaN, the same infinities, and
     |got - ref| / max(|ref|, 1) <= tol elsewhere."""
