@@ -189,9 +189,10 @@ int mlkhip_time_device_span(const mlkhip_artifact* a, const mlkhip_binding* bind
 /* The reference's fastkernel search (fastkernel/include/mlk/fastkernel/
  * fast_kernel.h:165-355, src/fast_kernel.cpp:797-887) certifies tile and
  * exec-path variants of a kernel and keeps the fastest. Here the declared
- * space is the launch forms of each step's hand-written kernel: softmax
- * rows (exp form, store cache policy, pipelining), f16 GEMM tiles and
- * schedules, score-softmax pass structure. */
+ * space is the launch forms of each step's kernel: softmax rows (exp form,
+ * store cache policy, pipelining), f16 GEMM tiles and schedules, the f32
+ * GEMM's operand staging, score-softmax pass structure, and the generic
+ * loop-nest kernel's LDS slabs and workgroup size (256, 512, 64). */
 
 /* Number of steps (kernel launches) of the artifact's plan. */
 int mlkhip_num_steps(const mlkhip_artifact* a);
