@@ -192,7 +192,8 @@ int mlkhip_time_device_span(const mlkhip_artifact* a, const mlkhip_binding* bind
  * space is the launch forms of each step's kernel: softmax rows (exp form,
  * store cache policy, pipelining), f16 GEMM tiles and schedules, the f32
  * GEMM's operand staging, score-softmax pass structure, and the generic
- * loop-nest kernel's LDS slabs and workgroup size (256, 512, 64). */
+ * loop-nest kernel's LDS slabs, workgroup size (256, 512, 64) and collapse
+ * depth. */
 
 /* Number of steps (kernel launches) of the artifact's plan. */
 int mlkhip_num_steps(const mlkhip_artifact* a);

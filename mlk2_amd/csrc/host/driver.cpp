@@ -118,7 +118,7 @@ Result<std::unique_ptr<HipLoadedKernel>> buildHipKernelArtifact(const KernelModu
     }
     k->fingerprint_ = artifactFingerprint(k->km_, k->plan_, config.arch);
     k->fromCache_ = applyCachedVariants(config.cacheDir, k->fingerprint_, k->km_, k->plan_);
-    k->nestFormFn_.assign(k->plan_.steps.size(), std::array<void*, 4>{nullptr, nullptr, nullptr, nullptr});
+    k->nestFormFn_.assign(k->plan_.steps.size(), std::array<void*, 5>{});
     return k;
 }
 
@@ -186,12 +186,13 @@ int HipLoadedKernel::arenaLayout(const DeviceBinding* binds, int64_t elements, c
     for (size_t i = 0; i < bindables_.size(); ++i) ptr[bindables_[i]] = binds[i].ptr;
     for (size_t si = 0; si < plan_.steps.size(); ++si) {
         const Step& st = plan_.steps[si];
-        if (st.kind == StepKind::Nest && st.checked) {
+        if (st.kind == StepKind::Nest &&
+            nestFormChecked(st, st.variant >= 1 && st.variant <= 4 ? st.variant : 0)) {
             why = "step " + std::to_string(si) + " (loop nest) reports run-time bounds checks through a host "
                   "read-back, which the allocation-free entry does not do";
             return MLKHIP_REFUSED;
         }
-        if (st.kind == StepKind::Nest && st.variant >= 1 && st.variant <= 3 && nestFormFn_[si][st.variant] == nullptr) {
+        if (st.kind == StepKind::Nest && st.variant >= 1 && st.variant <= 4 && nestFormFn_[si][st.variant] == nullptr) {
             why = "step " + std::to_string(si) + " pins loop-nest launch form " + std::to_string(st.variant) +
                   ", which is not loaded yet";
             return MLKHIP_REFUSED;
@@ -401,8 +402,11 @@ int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* 
                                    : binds[bi].elements;
                 }
                 na.elements = elements;
+                const int form = st.variant >= 1 && st.variant <= 4 ? st.variant : 0;
+                const bool checked = nestFormChecked(st, form);
+                const int64_t instances = nestFormInstances(st, form);
                 void* status = nullptr;
-                if (st.checked) {
+                if (checked) {
                     status = statusWord();
                     if (status == nullptr) {
                         why = "status word allocation failed";
@@ -415,7 +419,6 @@ int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* 
                     na.status = static_cast<int*>(status);
                 }
                 void* fn = st.fn;
-                const int form = st.variant >= 1 && st.variant <= 3 ? st.variant : 0;
                 const unsigned wg = nestFormThreads(form);
                 if (form != 0) {
                     std::lock_guard<std::mutex> g(scratchLock_);
@@ -436,8 +439,8 @@ int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* 
                     }
                     fn = nestFormFn_[si][form];
                 }
-                rc = mlkd_jit_launch_nest(fn, gridFor(st.threads, wg), wg, &na, &sc, st.threads, stream);
-                if (rc == 0 && st.checked) {
+                rc = mlkd_jit_launch_nest(fn, gridFor(instances, wg), wg, &na, &sc, instances, stream);
+                if (rc == 0 && checked) {
                     int code = 0;
                     if (mlkd_rt_d2h(&code, status, sizeof(code), stream) != 0 || mlkd_rt_sync(stream) != 0) {
                         why = "status word read-back failed";

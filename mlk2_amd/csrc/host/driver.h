@@ -114,9 +114,10 @@ private:
     void fillScoreParams(const Step& st, const std::vector<void*>& ptr, mlkd_score_softmax& p) const;
     mutable std::mutex scratchLock_;
     mutable std::vector<std::pair<void*, std::unique_ptr<RunScratch>>> scratchByStream_;
-    // Loop-nest launch forms 1-3 (no LDS slabs; 512 and 64 threads per
-    // workgroup), each compiled on first use; form 0 is the step's own.
-    mutable std::vector<std::array<void*, 4>> nestFormFn_;
+    // Loop-nest launch forms 1-4 (no LDS slabs; 512 and 64 threads per
+    // workgroup; one fewer collapsed loop), each compiled on first use; form
+    // 0 is the step's own.
+    mutable std::vector<std::array<void*, 5>> nestFormFn_;
 };
 
 /// Essential work of a module (the reference's EssentialWork,

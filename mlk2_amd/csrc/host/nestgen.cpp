@@ -858,7 +858,7 @@ struct Emitter {
 
 }  // namespace
 
-Result<Step> planNestWith(const KernelModule& km, uint32_t root, bool allowSlabs) {
+Result<Step> planNestWith(const KernelModule& km, uint32_t root, bool allowSlabs, int maxChain) {
     Ctx cx{km, false, ErrorCode::UnsupportedCapability, std::string(), 0};
     Step st;
     st.kind = StepKind::Nest;
@@ -875,7 +875,7 @@ Result<Step> planNestWith(const KernelModule& km, uint32_t root, bool allowSlabs
     const KernelNode* body = nullptr;   // the last chain loop
     uint32_t cur = root;
     bool deadRoot = false;
-    while (km.nodes[cur].op == KernelOp::Loop && chainB.size() < static_cast<size_t>(kMaxChain)) {
+    while (km.nodes[cur].op == KernelOp::Loop && chainB.size() < static_cast<size_t>(maxChain)) {
         const KernelNode& n = km.nodes[cur];
         if (n.step != 1) break;
         const LoopBounds lb = loopBounds(km, n);
@@ -1078,18 +1078,38 @@ extern "C" __global__ __launch_bounds__(MLK_NEST_WG) void mlk_nest(const mlk_nes
 Result<Step> planNest(const KernelModule& km, uint32_t root) {
     // Schedule parameter "hip_slabs" = 0 keeps every buffer in global memory
     // (the reference's slabs are likewise an emitter option,
-    // slab_plan.h:51-62).
-    auto st = planNestWith(km, root, km.param("hip_slabs", 1) != 0);
-    if (!st.has_value() || st->slabs == 0) return st;
-    auto plain = planNestWith(km, root, false);
-    if (!plain.has_value() || plain->nestBufs != st->nestBufs) return st;   // same slots: one binding serves both
-    st->sourceNoSlabs = std::move(plain->source);
+    // slab_plan.h:51-62); "hip_collapse_max" caps the collapsed loops.
+    const bool slabsOn = km.param("hip_slabs", 1) != 0;
+    const int maxChain = static_cast<int>(std::clamp<int64_t>(km.param("hip_collapse_max", kMaxChain), 0, kMaxChain));
+    auto st = planNestWith(km, root, slabsOn, maxChain);
+    if (!st.has_value() || st->kind != StepKind::Nest) return st;
+    if (st->slabs > 0) {
+        auto plain = planNestWith(km, root, false, maxChain);
+        // Same slots: one binding serves both.
+        if (plain.has_value() && plain->nestBufs == st->nestBufs) st->sourceNoSlabs = std::move(plain->source);
+    }
+    // Form 4: the innermost collapsed loop runs inside each thread. Declared
+    // only where it and form 0 both hold the walker's values exactly (no
+    // narrow round trip), so the two give the same bits.
+    if (st->collapsed >= 2 && !st->narrowRoundTrip) {
+        auto less = planNestWith(km, root, slabsOn, st->collapsed - 1);
+        if (less.has_value() && less->kind == StepKind::Nest && less->nestBufs == st->nestBufs &&
+            !less->narrowRoundTrip && less->collapsed == st->collapsed - 1) {
+            st->sourceLessCollapse = std::move(less->source);
+            st->threadsLessCollapse = less->threads;
+            st->checkedLessCollapse = less->checked;
+        }
+    }
     return st;
 }
 
 std::vector<int> nestForms(const Step& st) {
-    if (!st.sourceNoSlabs.empty()) return {0, 1, 2, 3};
-    return {0, 2, 3};
+    std::vector<int> v{0};
+    if (!st.sourceNoSlabs.empty()) v.push_back(1);
+    v.push_back(2);
+    v.push_back(3);
+    if (!st.sourceLessCollapse.empty()) v.push_back(4);
+    return v;
 }
 
 unsigned nestFormThreads(int form) { return form == 2 ? 512u : (form == 3 ? 64u : 256u); }
@@ -1100,8 +1120,13 @@ std::string nestFormSource(const Step& st, int form) {
         case 1: return st.sourceNoSlabs;
         case 2:
         case 3: return "#define MLK_NEST_WG " + std::to_string(nestFormThreads(form)) + "\n" + st.source;
+        case 4: return st.sourceLessCollapse;
         default: return std::string();
     }
 }
+
+int64_t nestFormInstances(const Step& st, int form) { return form == 4 ? st.threadsLessCollapse : st.threads; }
+
+bool nestFormChecked(const Step& st, int form) { return form == 4 ? st.checkedLessCollapse : st.checked; }
 
 }  // namespace mlk::hip

@@ -77,6 +77,11 @@ struct Step {
     // when it has none): launch form 1 of the step, compiled on first use.
     int slabs{0};
     std::string sourceNoSlabs;
+    // Launch form 4: the innermost collapsed loop run inside each thread
+    // (empty when not declared), its instance count and bounds-check flag.
+    std::string sourceLessCollapse;
+    int64_t threadsLessCollapse{0};
+    bool checkedLessCollapse{false};
     std::vector<uint32_t> nestBufs;
     std::vector<uint32_t> nestWrites;
     std::vector<uint32_t> nestReads;  // buffers the kernel reads from memory (registers' loads included)
@@ -139,9 +144,14 @@ Result<Step> planNest(const KernelModule& km, uint32_t root);
 /// Launch forms of a loop-nest step (nestgen.cpp): 0 the step's own kernel
 /// (its LDS slabs, 256 threads per workgroup); 1 the same kernel without
 /// slabs (declared only where the step has slabs); 2 and 3 form 0 with 512
-/// and 64 threads per workgroup. Every form runs each instance's code
-/// unchanged, so all give the same bits.
+/// and 64 threads per workgroup; 4 the kernel with its innermost collapsed
+/// loop run inside each thread (declared where two or more loops collapse
+/// and both forms keep the walker's values). Every form computes each
+/// instance with the same operations, so all give the same bits.
 std::vector<int> nestForms(const Step& st);
+/// Instances (threads' work items) and the bounds-check flag of form `form`.
+int64_t nestFormInstances(const Step& st, int form);
+bool nestFormChecked(const Step& st, int form);
 /// Threads per workgroup of loop-nest form `form`.
 unsigned nestFormThreads(int form);
 /// hipRTC source of loop-nest form `form` of `st` (empty if not declared).

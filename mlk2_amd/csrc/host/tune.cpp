@@ -317,8 +317,9 @@ std::string launchCoverage(const KernelModule& km, const Step& st, int64_t eleme
             break;
         }
         case StepKind::Nest: {
-            const int64_t wg = nestFormThreads(st.variant >= 0 ? st.variant : 0);
-            instances = st.threads;
+            const int nf = st.variant >= 0 ? st.variant : 0;
+            const int64_t wg = nestFormThreads(nf);
+            instances = nestFormInstances(st, nf);
             workgroups = std::min<int64_t>(std::max<int64_t>((st.threads + wg - 1) / wg, 1), 16384);
             perGroup = wg;
             form = "grid-stride over the collapsed parallel loops";
@@ -429,7 +430,7 @@ std::vector<int> variantSpace(const KernelModule& km, const Step& st) {
         case StepKind::Nest:
             // 0: with the step's LDS slabs; 1: the same kernel without them
             // (where it has slabs); 2, 3: form 0 at 512 and 64 threads per
-            // workgroup.
+            // workgroup; 4: one fewer collapsed loop.
             return nestForms(st);
         default: return {};
     }

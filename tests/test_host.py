@@ -211,7 +211,9 @@ def test_chain_codegen_exact_constants():
     (fx.config4_module(64, 32, 64, "f32", 2), []),      # K below the 64-deep ring steps
     (fx.config1_module(1 << 12), []),
     (fx.config4_module(64, 64, 64, "f16", 1), []),     # below the 256-multiple tiles
-    (tn.generic(tn.weighted_rows_module()), [0, 1, 2, 3]),  # slabs, none, 512 and 64 threads per workgroup
+    (tn.generic(tn.weighted_rows_module()), [0, 1, 2, 3, 4]),  # slabs, none, 512/64 threads, one fewer collapse
+    (tn.generic(fx.tiled_gemm_module(70, 45, 37, "f32", tile=16, init="split", out_dtype="f32"), False),
+     [0, 1, 2, 3]),   # f32 sums stored between k bands: no form 4
     (tn.generic(fx.lift_1d(fx.config1_module(n=1 << 12)), False), [0, 2, 3]),   # loop nest without slabs
 ])
 def test_declared_variant_space(km, space):

@@ -17,6 +17,7 @@ walker's f64 value rounded once (round to nearest even), so they are
 bit-exact against the oracle's result rounded to f32. Chains with exp use
 the elementwise tolerance of 1e-6 relative.
 """
+import copy
 import sys
 
 import numpy as np
@@ -264,7 +265,7 @@ def test_workgroup_forms_host(case, wg):
         seed = int(case.split("-")[1])
         km = generic(nf.random_module(seed))
         arrays, scalars = nf.random_inputs(km, seed)
-    assert backend.plan_variants(km, 0)[-2:] == [2, 3]
+    assert {2, 3} <= set(backend.plan_variants(km, 0))
     st0, cur0 = nesthost.run_module(km, arrays, scalars)
     st, cur = nesthost.run_module(km, arrays, scalars, reverse=True, wg=wg)
     assert st == st0 == 0
@@ -274,6 +275,36 @@ def test_workgroup_forms_host(case, wg):
         assert nf.same_bits(cur[i], cur0[i]), (case, wg, i)
         if km.buffers[i].dtype == "f64":
             assert nf.same_bits(cur[i], ref[i]), (case, wg, i)
+
+
+@pytest.mark.parametrize("case", ["slabs-f64", "slabs-f16", "tiled-hoist", "tiled-split"])
+def test_less_collapse_form_host(case):
+    # Launch form 4 runs the innermost collapsed loop inside each thread: the
+    # module planned with hip_collapse_max = (collapsed loops - 1) gives its
+    # source. Under AddressSanitizer every access stays in bounds, and the
+    # bits are form 0's and the walker's.
+    if case.startswith("slabs"):
+        km = generic(weighted_rows_module(dtype=case.split("-")[1]))
+        arrays, scalars = weighted_rows_inputs(km), ()
+    else:
+        km = generic(fx.tiled_gemm_module(70, 45, 37, "f64", tile=16, init=case.split("-")[1], out_dtype="f64"),
+                     canonical=False)
+        rng = np.random.default_rng(3)
+        arrays, scalars = {b: rng.integers(-32, 32, km.buffers[b].elements).astype(np.float64) / 8.0
+                           for b in (0, 1)}, ()
+    assert 4 in backend.plan_variants(km, 0)
+    less = copy.deepcopy(km)
+    less.schedule["hip_collapse_max"] = collapsed(km) - 1
+    assert collapsed(less) == collapsed(km) - 1
+    st0, cur0 = nesthost.run_module(km, arrays, scalars)
+    st, cur = nesthost.run_module(less, arrays, scalars, reverse=True)
+    assert st == st0 == 0
+    ref = oracle.run(km, {i: arrays[i] for i in km.input_ids()}, scalars,
+                     init={i: arrays[i] for i in km.output_ids() if i in arrays})
+    for i in km.output_ids():
+        assert nf.same_bits(cur[i], cur0[i]), (case, i)
+        if km.buffers[i].dtype == "f64":
+            assert nf.same_bits(cur[i], ref[i]), (case, i)
 
 
 def test_tiled_gemm_collapses_all_parallel_levels():
@@ -628,18 +659,28 @@ def test_fuzz_gpu(hip, seed):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("seed", [0, 2, 5, 11])
-def test_fuzz_every_nest_form_gpu(hip, seed):
+@pytest.mark.parametrize("case", ["fuzz-0", "fuzz-2", "fuzz-5", "fuzz-11", "tiled-split", "tiled-guard"])
+def test_fuzz_every_nest_form_gpu(hip, case):
     # Every loop-nest launch form (slabs, no slabs, 512 and 64 threads per
-    # workgroup) pinned on every loop-nest step that declares it: the bits
-    # are the walker's for each.
-    km = generic(nf.random_module(seed), canonical=False)
-    arrays, scalars = nf.random_inputs(km, seed)
+    # workgroup, one fewer collapsed loop) pinned on every loop-nest step that
+    # declares it: the bits are the walker's for each.
+    if case.startswith("fuzz"):
+        seed = int(case.split("-")[1])
+        km = generic(nf.random_module(seed), canonical=False)
+        arrays, scalars = nf.random_inputs(km, seed)
+    else:
+        seed = case
+        km = generic(fx.tiled_gemm_module(70, 45, 37, "f64", tile=16, init=case.split("-")[1], out_dtype="f64"),
+                     canonical=False)
+        rng = np.random.default_rng(3)
+        arrays = {b: rng.integers(-32, 32, km.buffers[b].elements).astype(np.float64) / 8.0 for b in (0, 1)}
+        arrays[2] = np.zeros(km.buffers[2].elements)
+        scalars = ()
     ref = oracle.run(km, {i: arrays[i] for i in km.input_ids()}, scalars,
                      init={i: arrays[i] for i in km.output_ids()})
     art = hip.build(km)
     steps = art.num_steps()
-    for form in (0, 1, 2, 3):
+    for form in (0, 1, 2, 3, 4):
         pinned = 0
         for s in range(steps):
             space = art.step_variants(s)
