@@ -121,8 +121,10 @@ def _gemm_call_acc_case(m=256, k=128, n=512):
 
 
 def _nest_case(m=64, n=256, k=41):
-    # The generic loop-nest kernel with LDS slabs (form 0) and without (1):
-    # the same reads from another place, so both are bit-exact.
+    # The generic loop-nest kernel with LDS slabs (form 0), without them (1),
+    # at 512 and 64 threads per workgroup (2, 3) and with one fewer collapsed
+    # loop (4): each instance computed with the same operations, so every
+    # form is bit-exact.
     from test_nest import generic, weighted_rows_inputs, weighted_rows_module
     km = generic(weighted_rows_module(M=m, N=n, K=k, off=7, dtype="f32"))
     arr = weighted_rows_inputs(km)
