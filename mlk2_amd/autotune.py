@@ -18,8 +18,11 @@ covers the five configs as well as the reference's GEMM:
         [--tier=1|2] [--reps=R] [--cache-dir=D] [--arch=gfx950] [--json-out=F]
 
 c4a and c4b take --m/--k/--n too (1024^3 and 4096^3 by default). The
-inputs are the configs' seeded synthetic data (mlk2_amd.inputs). Exit
-codes: 0 done, 1 a search failed, 2 usage error or no device.
+inputs are the configs' seeded synthetic data (mlk2_amd.inputs).
+`--module=doc.json` searches any mlk-kernel document instead (seeded
+uniform [-1, 1] inputs; `--elements` for a dynamic extent, `--scalar` for
+scalar parameters). Exit codes: 0 done, 1 a search failed, 2 usage error or
+no device.
 """
 from __future__ import annotations
 
@@ -34,7 +37,7 @@ import numpy as np
 from . import backend as be
 from . import fixtures as fx
 from . import inputs
-from .kernel_ir import KernelModule
+from .kernel_ir import KernelBuffer, KernelModule
 
 CONFIGS = ("gemm", "c1", "c2", "c3", "c4a", "c4b", "c5")
 
@@ -61,6 +64,8 @@ class TuneArgs:
     cache_dir: Optional[str] = None
     arch: str = "gfx950"
     json_out: Optional[str] = None
+    module: Optional[str] = None
+    scalars: Sequence[float] = ()
 
 
 def parse_args(argv: Sequence[str]) -> TuneArgs:
@@ -74,13 +79,15 @@ def parse_args(argv: Sequence[str]) -> TuneArgs:
     p.add_argument("--cache-dir", default=None)
     p.add_argument("--arch", default="gfx950")
     p.add_argument("--json-out", default=None)
+    p.add_argument("--module", default=None)
+    p.add_argument("--scalar", action="append", default=[], type=float)
     try:
         ns = p.parse_args(list(argv))
     except SystemExit as e:
         raise UsageError(f"bad arguments ({e.code})")
-    configs = list(CONFIGS) if ns.config == "all" else ns.config.split(",")
+    configs = ["module"] if ns.module else (list(CONFIGS) if ns.config == "all" else ns.config.split(","))
     for c in configs:
-        if c not in CONFIGS:
+        if c not in CONFIGS and c != "module":
             raise UsageError(f"unknown --config {c} (one of {', '.join(CONFIGS)} or all)")
     if ns.dtype not in ("f64", "f32", "f16"):
         raise UsageError("--dtype must be f64, f32 or f16")
@@ -94,16 +101,61 @@ def parse_args(argv: Sequence[str]) -> TuneArgs:
             raise UsageError(f"--{name} must be positive")
     return TuneArgs(configs=configs, m=ns.m, k=ns.k, n=ns.n, dtype=ns.dtype, elements=ns.elements, rows=ns.rows,
                     cols=ns.cols, batch=ns.batch, seq=ns.seq, dim=ns.dim, tier=ns.tier, reps=ns.reps,
-                    cache_dir=ns.cache_dir, arch=ns.arch, json_out=ns.json_out)
+                    cache_dir=ns.cache_dir, arch=ns.arch, json_out=ns.json_out, module=ns.module,
+                    scalars=tuple(ns.scalar))
 
 
 def _pick(v: Optional[int], default: int) -> int:
     return default if v is None else v
 
 
+class DocumentModule:
+    """An mlk-kernel document as written: its text goes to the library
+    unchanged, and its buffer table says what the search binds."""
+
+    def __init__(self, text: str):
+        try:
+            doc = json.loads(text)
+        except ValueError as e:
+            raise UsageError(f"not JSON: {e}")
+        if not isinstance(doc, dict) or doc.get("format") != "mlk-kernel" or "buffers" not in doc:
+            raise UsageError("not an mlk-kernel document")
+        self.text = text
+        self.buffers = [KernelBuffer(name=str(b.get("name", f"b{i}")), dtype=str(b.get("dtype", "f64")),
+                                     is_input=bool(b.get("input", False)), is_output=bool(b.get("output", False)),
+                                     is_temp=bool(b.get("temp", False)), elements=int(b.get("elements", -1)),
+                                     dims=[int(d) for d in b.get("dims", [])])
+                        for i, b in enumerate(doc["buffers"])]
+
+    def to_json(self) -> str:
+        return self.text
+
+    def bindable_ids(self) -> List[int]:
+        return [i for i, b in enumerate(self.buffers) if b.is_input or b.is_output or b.is_temp]
+
+
+def _document_case(a: TuneArgs) -> Tuple[str, DocumentModule, List[np.ndarray]]:
+    try:
+        with open(a.module, "r", encoding="utf-8") as f:
+            km = DocumentModule(f.read())
+    except OSError as e:
+        raise UsageError(f"cannot read {a.module}: {e}")
+    arrays = []
+    for i, b in enumerate(km.buffers):
+        n = int(np.prod(b.dims)) if b.dims else (b.elements if b.elements >= 0 else (a.elements or -1))
+        if n < 0:
+            raise UsageError(f"buffer {i} has a dynamic extent: give --elements")
+        b.elements = n
+        if b.is_input and not b.is_temp:
+            arrays.append(inputs.uniform(0x5EED0200 + i, n, -1.0, 1.0, b.dtype))
+    return f"module {a.module}", km, arrays
+
+
 def config_case(name: str, a: TuneArgs) -> Tuple[str, KernelModule, List[np.ndarray]]:
     """(description, module, input arrays in the module's input order) of
     config `name` at the shape the arguments give."""
+    if name == "module":
+        return _document_case(a)
     if name == "gemm":
         m, k, n = _pick(a.m, 64), _pick(a.k, 48), _pick(a.n, 56)
         tier = _pick(a.tier, 2)
@@ -218,7 +270,10 @@ def main(argv: Optional[Sequence[str]] = None) -> int:
         bufs = bind(km, arrays)
         try:
             art = hip.build(km, cache_dir=a.cache_dir)
-            rep = art.autotune(bufs, reps=a.reps, cache_dir=a.cache_dir)
+            # --elements is the run's element count only for a document (for
+            # c1 it is the config's size).
+            rep = art.autotune(bufs, scalars=a.scalars, elements=(a.elements or 0) if name == "module" else 0,
+                               reps=a.reps, cache_dir=a.cache_dir)
         except be.MlkHipError as e:
             print(f"mlk2_amd.autotune: {name}: search failed: {e}", file=sys.stderr)
             rc = 1

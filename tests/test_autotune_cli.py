@@ -86,3 +86,39 @@ def test_search_over_configs_writes_its_report(tmp_path, capsys):
     assert rep["c4b"]["steps"][0]["launch"]["workgroups"] in (1, 2)
     assert "== fast-kernel search: c4b gemm f16 256x128x256" in text
     assert "<- chosen" in text
+
+
+def test_module_document_case(tmp_path):
+    # --module takes an mlk-kernel document as written; inputs are seeded
+    # and sized from its buffer table.
+    from test_nest import generic, weighted_rows_module
+    km = generic(weighted_rows_module())
+    doc = tmp_path / "nest.json"
+    doc.write_text(km.to_json())
+    a = at.parse_args([f"--module={doc}"])
+    assert a.configs == ["module"]
+    title, mod, arrays = at.config_case("module", a)
+    assert mod.to_json() == km.to_json()
+    assert mod.bindable_ids() == km.bindable_ids()
+    ins = [i for i, b in enumerate(km.buffers) if b.is_input and not b.is_temp]
+    assert [x.size for x in arrays] == [km.buffers[i].elements for i in ins]
+    bad = tmp_path / "bad.json"
+    bad.write_text('{"format": "other"}')
+    with pytest.raises(at.UsageError):
+        at.config_case("module", at.parse_args([f"--module={bad}"]))
+
+
+@pytest.mark.gpu
+def test_module_document_search(tmp_path, capsys):
+    from test_nest import generic, weighted_rows_module
+    km = generic(weighted_rows_module())
+    doc = tmp_path / "nest.json"
+    doc.write_text(km.to_json())
+    out = tmp_path / "report.json"
+    rc = at.main([f"--module={doc}", "--reps=3", f"--cache-dir={tmp_path}", f"--json-out={out}"])
+    print(capsys.readouterr().out, flush=True)
+    assert rc == 0
+    (st,) = json.loads(out.read_text())["module"]["steps"]
+    assert [c["variant"] for c in st["candidates"]] == [0, 1, 2, 3, 4]
+    chosen = [c for c in st["candidates"] if c["variant"] == st["chosen"]][0]
+    assert chosen["admissible"] and chosen["certificate"]["identity"]["certified"]
