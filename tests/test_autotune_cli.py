@@ -122,3 +122,21 @@ def test_module_document_search(tmp_path, capsys):
     assert [c["variant"] for c in st["candidates"]] == [0, 1, 2, 3, 4]
     chosen = [c for c in st["candidates"] if c["variant"] == st["chosen"]][0]
     assert chosen["admissible"] and chosen["certificate"]["identity"]["certified"]
+
+
+def test_module_document_dynamic_extent(tmp_path):
+    # The legacy 1-D form's extent is the run's element count: the document
+    # needs --elements, which then sizes every dynamic buffer.
+    from mlk2_amd import fixtures as fx
+    km = fx.config1_module(n=1)
+    km.nodes[2].end = -1
+    for b in km.buffers:
+        b.elements = -1
+        b.dims = []
+    doc = tmp_path / "dyn.json"
+    doc.write_text(km.to_json())
+    with pytest.raises(at.UsageError):
+        at.config_case("module", at.parse_args([f"--module={doc}"]))
+    _, mod, arrays = at.config_case("module", at.parse_args([f"--module={doc}", "--elements=5000"]))
+    assert [a.size for a in arrays] == [5000]
+    assert all(b.elements == 5000 for b in mod.buffers)
