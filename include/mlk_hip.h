@@ -112,6 +112,15 @@ int mlkhip_emit_artifact(const char* module_json, size_t len, const char* arch, 
 
 void mlkhip_release(mlkhip_artifact* a);
 
+/* No counterpart in the reference (its artifact allocates per call): frees
+ * the scratch set mlkhip_run_device keeps for `stream` (temps, row
+ * statistics, column flags), after waiting for that stream. A caller that
+ * runs an artifact on many short-lived streams releases each one's set
+ * before destroying the stream; the next run on a released stream
+ * allocates a new set. Must not overlap a run of `a` on `stream` from
+ * another thread. Returns 0, or MLKHIP_LAUNCH when the wait fails. */
+int mlkhip_release_stream_scratch(mlkhip_artifact* a, void* stream);
+
 int mlkhip_is_multidim(const mlkhip_artifact* a);
 const char* mlkhip_class_name(const mlkhip_artifact* a);
 
@@ -143,8 +152,14 @@ int mlkhip_kernel_1d(const mlkhip_artifact* a, double* const* ptrs, int n_ptrs, 
                      const double* scalars, int64_t n_scalars);
 
 /* Device-resident typed entry (the timing path): no copies, no allocation
- * except artifact-owned temp scratch; enqueued on `stream` (a hipStream_t,
- * NULL = default stream), asynchronous. */
+ * except artifact-owned scratch (temps, the score-softmax row statistics, the
+ * Call(MatMul) column flags), one set per stream; enqueued on `stream` (a
+ * hipStream_t, NULL = default stream), asynchronous: no step reads anything
+ * back to the host except a loop nest with run-time bounds checks, which
+ * waits for its status word. A Call(MatMul) step decides its skip-zero-A
+ * handling on the device (kernel_buffers.cpp:422): B's column groups with a
+ * non-finite value are flagged, the MFMA form computes the other tiles and
+ * the exact kernel the flagged ones. */
 int mlkhip_run_device(const mlkhip_artifact* a, const mlkhip_binding* binds, int n_binds,
                       const double* scalars, int64_t n_scalars, int64_t elements, void* stream);
 
@@ -158,8 +173,8 @@ int mlkhip_run_device(const mlkhip_artifact* a, const mlkhip_binding* binds, int
  * that each GPU holds until the process ends. A run that needs more is
  * refused (MLKHIP_REFUSED, see mlkhip_last_error) before anything is
  * launched, as is a step that needs a host read-back (a loop nest with
- * run-time bounds checks). A Call(MatMul) step always runs the exact
- * skip-zero-A kernel here (the non-finite scan of B needs a read-back). Calls
+ * run-time bounds checks). A Call(MatMul) step keeps its skip-zero-A column
+ * flags in the array and runs the same kernels as mlkhip_run_device. Calls
  * no hipMalloc or hipFree. Every call on one GPU shares that GPU's array,
  * which keeps the last call's contents: calls that overlap on one GPU (on
  * different streams, or from different threads) race. Enqueued on `stream`,
@@ -208,9 +223,14 @@ int mlkhip_step_variants(const mlkhip_artifact* a, int step, int* out, int cap);
  * variant space. */
 int mlkhip_plan_variants(const char* module_json, size_t len, int step, int* out, int cap);
 
-/* Kernel symbol of step `step` when the step is a hipRTC instance (an
- * elementwise chain: mlk_elementwise_<12 hex digits of its source hash>; a
- * generic loop nest: mlk_nest), else "". Profiles name kernels by it. */
+/* Kernel symbol of step `step`, as profiles name kernels: a hipRTC
+ * instance's (an elementwise chain: mlk_elementwise_<12 hex digits of its
+ * source hash>; a generic loop nest: mlk_nest), or the precompiled kernel
+ * the step's launcher picks for its shape, dtypes and pinned form on
+ * 256-byte aligned buffers, with template arguments and without parameters
+ * (gemmF16Dma8<true>, softmaxWaveRowPair<16, true>; a two-kernel launch
+ * joins them with '+': scoreStatsQ+scoreStoreQ). The text lives as long as
+ * the artifact. */
 const char* mlkhip_step_kernel_name(const mlkhip_artifact* a, int step);
 
 /* Form step `step` launches with (-1 = the kernel's default); -2 when the

@@ -66,6 +66,7 @@ def lib():
                                        c.c_size_t]
     L.mlkhip_release.argtypes = [c.c_void_p]
     L.mlkhip_release.restype = None
+    L.mlkhip_release_stream_scratch.argtypes = [c.c_void_p, c.c_void_p]
     L.mlkhip_is_multidim.argtypes = [c.c_void_p]
     L.mlkhip_class_name.argtypes = [c.c_void_p]
     L.mlkhip_class_name.restype = c.c_char_p
@@ -397,6 +398,10 @@ class LoadedKernel:
 
 
     # ---- launch-form search (fastkernel analogue) ----
+    def release_stream_scratch(self, stream=None) -> None:
+        """Waits for `stream`, then frees the scratch set runs on it allocated."""
+        _check(lib().mlkhip_release_stream_scratch(self._h, stream))
+
     def num_steps(self) -> int:
         return int(lib().mlkhip_num_steps(self._h))
 

@@ -32,6 +32,8 @@
 
 #include <stdint.h>
 
+#include <algorithm>
+
 #include "mlk_device_math.h"
 #include "runtime_abi.h"
 
@@ -46,6 +48,17 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kBM = 256, kBN = 256, kBK = 64;
 constexpr int kPadK = kBK + 8;           // halves per LDS row (16-byte pad)
 constexpr int kTileHalves = 256 * kPadK;  // one LDS tile (A or B)
+
+/// Skip-zero-A Call form: bad[g] is 1 when column group [64g, 64g + 64) of
+/// B holds an infinity or a NaN. A workgroup whose columns [col0, col0 +
+/// width) meet such a group leaves its tile untouched (C keeps its value
+/// going in), and the exact fix-up kernel computes it. nullptr: no check.
+__device__ __forceinline__ bool skipTile(const uint8_t* bad, int64_t col0, int width) {
+    if (bad == nullptr) return false;
+    uint32_t any = 0;
+    for (int g = 0; g < width / 64; ++g) any |= bad[col0 / 64 + g];
+    return any != 0;
+}
 
 __device__ __forceinline__ void xcdTile(int tilesM, int tilesN, int& tm, int& tn) {
     const int id = blockIdx.x;
@@ -74,7 +87,7 @@ __global__ __launch_bounds__(512) void gemmF16Mfma(const _Float16* __restrict__ 
                                                    const _Float16* __restrict__ B,
                                                    float* __restrict__ C, int M, int N, int K,
                                                    int64_t lda, int64_t ldb, int64_t ldc,
-                                                   int /*accumulate: template ACC*/) {
+                                                   int /*accumulate: template ACC*/, const uint8_t* __restrict__ bad) {
     extern __shared__ __align__(16) _Float16 lds[];
     _Float16* As = lds;                      // [2][256][kPadK]
     _Float16* Bs = lds + 2 * kTileHalves;    // [2][256][kPadK]
@@ -88,6 +101,7 @@ __global__ __launch_bounds__(512) void gemmF16Mfma(const _Float16* __restrict__ 
     xcdTile(M / kBM, N / kBN, tm, tn);
     const int64_t row0 = static_cast<int64_t>(tm) * kBM;
     const int64_t col0 = static_cast<int64_t>(tn) * kBN;
+    if (skipTile(bad, col0, kBN)) return;  // columns the fix-up computes
 
     // Loader roles: threads 0..255 load A (8 x 16 B each), 256..511 load a
     // 8 (k) x 8 (n) block of B each.
@@ -231,7 +245,7 @@ template <bool ACC, bool AHEAD2>
 __global__ __launch_bounds__(256, 2) void gemmF16Mfma2cu(const _Float16* __restrict__ A,
                                                          const _Float16* __restrict__ B,
                                                          float* __restrict__ C, int M, int N, int K,
-                                                         int64_t lda, int64_t ldb, int64_t ldc) {
+                                                         int64_t lda, int64_t ldb, int64_t ldc, const uint8_t* __restrict__ bad) {
     extern __shared__ __align__(16) _Float16 lds[];
     _Float16* As = lds;                     // [2][128][40]
     _Float16* Bs = lds + 2 * kTileA2;       // [2][256][40]
@@ -242,6 +256,7 @@ __global__ __launch_bounds__(256, 2) void gemmF16Mfma2cu(const _Float16* __restr
     xcdTile2(M / kBM2, N / kBN2, tm, tn);
     const int64_t row0 = static_cast<int64_t>(tm) * kBM2;
     const int64_t col0 = static_cast<int64_t>(tn) * kBN2;
+    if (skipTile(bad, col0, kBN2)) return;  // columns the fix-up computes
     const int bk = t & 7;    // B block: k rows bk*4 .. +3
     const int bn = t >> 3;   // B block: n cols bn*8 .. +7
     u32x4 ra0[2], rb0[4], ra1[2], rb1[4];
@@ -358,7 +373,7 @@ __global__ __launch_bounds__(256) void gemmF16Mfma4w(const _Float16* __restrict_
                                                      const _Float16* __restrict__ B,
                                                      float* __restrict__ C, int M, int N, int K,
                                                      int64_t lda, int64_t ldb, int64_t ldc,
-                                                     int /*accumulate: template ACC*/) {
+                                                     int /*accumulate: template ACC*/, const uint8_t* __restrict__ bad) {
     extern __shared__ __align__(16) _Float16 lds[];
     _Float16* As = lds;
     _Float16* Bs = lds + 2 * kTileHalves;
@@ -371,6 +386,7 @@ __global__ __launch_bounds__(256) void gemmF16Mfma4w(const _Float16* __restrict_
     xcdTile(M / kBM, N / kBN, tm, tn);
     const int64_t row0 = static_cast<int64_t>(tm) * kBM;
     const int64_t col0 = static_cast<int64_t>(tn) * kBN;
+    if (skipTile(bad, col0, kBN)) return;  // columns the fix-up computes
     const int bk = t & 7;
     const int bn = t >> 3;
     u32x4 ra[8], rb[8];
@@ -474,7 +490,7 @@ __global__ __launch_bounds__(256) void gemmF16Mfma4wDirect(const _Float16* __res
                                                            const _Float16* __restrict__ B,
                                                            float* __restrict__ C, int M, int N, int K,
                                                            int64_t lda, int64_t ldb, int64_t ldc,
-                                                           int /*accumulate: template ACC*/) {
+                                                           int /*accumulate: template ACC*/, const uint8_t* __restrict__ bad) {
     extern __shared__ __align__(16) _Float16 lds[];
     _Float16* As = lds;                    // [2][256][64] swizzled
     _Float16* Bs = lds + 2 * kTileA;       // [2][256][kPadK]
@@ -487,6 +503,7 @@ __global__ __launch_bounds__(256) void gemmF16Mfma4wDirect(const _Float16* __res
     xcdTile(M / kBM, N / kBN, tm, tn);
     const int64_t row0 = static_cast<int64_t>(tm) * kBM;
     const int64_t col0 = static_cast<int64_t>(tn) * kBN;
+    if (skipTile(bad, col0, kBN)) return;  // columns the fix-up computes
     const int bk = t & 7;
     const int bn = t >> 3;
     u32x4 rb[8];
@@ -597,7 +614,7 @@ template <bool ACC>
 __global__ __launch_bounds__(256) void gemmF16Mfma4wPipe(const _Float16* __restrict__ A,
                                                          const _Float16* __restrict__ B,
                                                          float* __restrict__ C, int M, int N, int K,
-                                                         int64_t lda, int64_t ldb, int64_t ldc) {
+                                                         int64_t lda, int64_t ldb, int64_t ldc, const uint8_t* __restrict__ bad) {
     extern __shared__ __align__(16) _Float16 lds[];
     _Float16* As = lds;
     _Float16* Bs = lds + 2 * kTileA;
@@ -610,6 +627,7 @@ __global__ __launch_bounds__(256) void gemmF16Mfma4wPipe(const _Float16* __restr
     xcdTile(M / kBM, N / kBN, tm, tn);
     const int64_t row0 = static_cast<int64_t>(tm) * kBM;
     const int64_t col0 = static_cast<int64_t>(tn) * kBN;
+    if (skipTile(bad, col0, kBN)) return;  // columns the fix-up computes
     const int bk = t & 7;
     const int bn = t >> 3;
     const int lrow = lane & 31;
@@ -786,7 +804,7 @@ template <bool ACC>
 __global__ __launch_bounds__(256, 1) void gemmF16Dma(const _Float16* __restrict__ A,
                                                      const _Float16* __restrict__ B,
                                                      float* __restrict__ C, int M, int N, int K,
-                                                     int64_t lda, int64_t ldb, int64_t ldc) {
+                                                     int64_t lda, int64_t ldb, int64_t ldc, const uint8_t* __restrict__ bad) {
     extern __shared__ __align__(16) _Float16 lds[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave >> 1, wn = wave & 1;
@@ -794,6 +812,7 @@ __global__ __launch_bounds__(256, 1) void gemmF16Dma(const _Float16* __restrict_
     xcdTile(M / kBM, N / kBN, tm, tn);
     const int64_t row0 = static_cast<int64_t>(tm) * kBM;
     const int64_t col0 = static_cast<int64_t>(tn) * kBN;
+    if (skipTile(bad, col0, kBN)) return;  // columns the fix-up computes
     const int steps = K / kDmaBK;
 
     // Stage `slot` receives K step min(slot, steps - 1) in ring slot
@@ -943,7 +962,7 @@ template <bool ACC>
 __global__ __launch_bounds__(512, 1) void gemmF16Dma8(const _Float16* __restrict__ A,
                                                       const _Float16* __restrict__ B,
                                                       float* __restrict__ C, int M, int N, int K,
-                                                      int64_t lda, int64_t ldb, int64_t ldc) {
+                                                      int64_t lda, int64_t ldb, int64_t ldc, const uint8_t* __restrict__ bad) {
     extern __shared__ __align__(16) _Float16 lds[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave >> 2, wn = wave & 3;
@@ -951,6 +970,7 @@ __global__ __launch_bounds__(512, 1) void gemmF16Dma8(const _Float16* __restrict
     xcdTile(M / kBM, N / kBN, tm, tn);
     const int64_t row0 = static_cast<int64_t>(tm) * kBM;
     const int64_t col0 = static_cast<int64_t>(tn) * kBN;
+    if (skipTile(bad, col0, kBN)) return;  // columns the fix-up computes
     const int steps = K / kDmaBK;
 
     // Stage `slot` receives K step min(slot, steps - 1) in ring slot
@@ -1106,7 +1126,7 @@ __global__ __launch_bounds__(256) void gemmF32Mfma(const float* __restrict__ A,
                                                    const float* __restrict__ B,
                                                    float* __restrict__ C, int /*M: the grid covers it*/, int N,
                                                    int K, int64_t lda, int64_t ldb, int64_t ldc,
-                                                   int /*accumulate: template ACC*/) {
+                                                   int /*accumulate: template ACC*/, const uint8_t* __restrict__ bad) {
     __shared__ float At[2][kFK][kFM + 4];   // transposed: [k][m]
     __shared__ float Bs[2][kFK][kFN + 4];   // as loaded: [k][n]
     const int tid = threadIdx.x;
@@ -1116,6 +1136,7 @@ __global__ __launch_bounds__(256) void gemmF32Mfma(const float* __restrict__ A,
     const int tilesN = N / kFN;
     const int64_t row0 = static_cast<int64_t>(blockIdx.x / tilesN) * kFM;
     const int64_t col0 = static_cast<int64_t>(blockIdx.x % tilesN) * kFN;
+    if (skipTile(bad, col0, kFN)) return;  // columns the fix-up computes
 
     // A tile 64x32 floats = 512 float4 and B tile 32x64 = 512 float4: 2 of
     // each per thread. Item c of A: wave-slice q = c / 64 covers rows
@@ -1210,13 +1231,14 @@ constexpr size_t kLdsF32Dma = static_cast<size_t>(kQStages) * kQStage * sizeof(f
 template <bool ACC>
 __global__ __launch_bounds__(256, 1) void gemmF32Dma(const float* __restrict__ A, const float* __restrict__ B,
                                                      float* __restrict__ C, int N, int K, int64_t lda,
-                                                     int64_t ldb, int64_t ldc) {
+                                                     int64_t ldb, int64_t ldc, const uint8_t* __restrict__ bad) {
     extern __shared__ __align__(16) float ldsF[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int tilesN = N / kFN;
     const int64_t row0 = static_cast<int64_t>(blockIdx.x / tilesN) * kFM;
     const int64_t col0 = static_cast<int64_t>(blockIdx.x % tilesN) * kFN;
+    if (skipTile(bad, col0, kFN)) return;  // columns the fix-up computes
     const int steps = K / kQK;
     // Stage `slot` receives K step min(slot, steps - 1) in ring slot
     // slot % kQStages. A is 64 rows of 256 bytes and B 64 k-rows of 256
@@ -1312,18 +1334,15 @@ __device__ __forceinline__ void stAny(void* p, int dt, int64_t i, T v) {
     }
 }
 
-/// 64x64 output tile per 256 threads, 4x4 per thread, K slabs of 16 through
-/// LDS; k ascending per output element, starting from C's old value in the
-/// accumulate form (the reference's order, kernel_buffers.cpp:406-432). With
-/// skip_zero_a the products of A[i,p] == 0 are left out, as there (:422).
+/// One 64x64 output tile by 256 threads, 4x4 per thread, K slabs of 16
+/// through LDS; k ascending per output element, starting from C's old value
+/// in the accumulate form (the reference's order, kernel_buffers.cpp:
+/// 406-432). With skip_zero_a the products of A[i,p] == 0 are left out, as
+/// there (:422).
 template <typename T>
-__global__ __launch_bounds__(256) void gemmGeneral(mlkd_gemm p) {
-    __shared__ T As[16][64 + 1];
-    __shared__ T Bs[16][64 + 1];
+__device__ __forceinline__ void generalTile(const mlkd_gemm& p, int64_t row0, int64_t col0, T (&As)[16][65],
+                                            T (&Bs)[16][65]) {
     const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
-    const int64_t tilesN = (p.n + 63) / 64;
-    const int64_t row0 = (blockIdx.x / tilesN) * 64;
-    const int64_t col0 = (blockIdx.x % tilesN) * 64;
     T acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -1369,6 +1388,70 @@ __global__ __launch_bounds__(256) void gemmGeneral(mlkd_gemm p) {
     }
 }
 
+/// Any shape and dtype mix: one 64x64 tile per workgroup.
+template <typename T>
+__global__ __launch_bounds__(256) void gemmGeneral(mlkd_gemm p) {
+    __shared__ T As[16][65];
+    __shared__ T Bs[16][65];
+    const int64_t tilesN = (p.n + 63) / 64;
+    generalTile<T>(p, (blockIdx.x / tilesN) * 64, (blockIdx.x % tilesN) * 64, As, Bs);
+}
+
+/// Zeroes n 32-bit words.
+__global__ __launch_bounds__(256) void clearWords(uint32_t* __restrict__ p, int64_t n) {
+    const int64_t i = blockIdx.x * 256ll + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+/// Column-group flags of B for the skip-zero-A Call form: bad[(c / 64)] = 1
+/// for every column c with an infinity or a NaN in any row. A product
+/// 0 * inf or 0 * NaN is the only one whose skip changes C beyond the sign
+/// of a zero sum, so only those columns need the exact kernel. Each thread
+/// checks 16-byte chunks of B's rows (a chunk lies inside one group: N and
+/// ldb are multiples of the chunk, B is 16-byte aligned); the flags start
+/// at zero and every writer stores 1.
+template <int DT>
+__global__ __launch_bounds__(256) void scanBadColumns(const void* __restrict__ B, int64_t K, int64_t N, int64_t ldb,
+                                                      uint8_t* __restrict__ bad) {
+    constexpr int per = DT == MLKD_F16 ? 8 : 4;  // elements per 16-byte chunk
+    const int64_t chunksRow = N / per;
+    const int64_t total = K * chunksRow;
+    for (int64_t c = blockIdx.x * 256ll + threadIdx.x; c < total; c += static_cast<int64_t>(gridDim.x) * 256) {
+        const int64_t k = c / chunksRow, col = (c - k * chunksRow) * per;
+        const u32x4 w = *reinterpret_cast<const u32x4*>(static_cast<const char*>(B) +
+                                                        (k * ldb + col) * (DT == MLKD_F16 ? 2 : 4));
+        bool nonFinite = false;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if constexpr (DT == MLKD_F16) {
+                nonFinite = nonFinite || (w[i] & 0x7C00u) == 0x7C00u || (w[i] & 0x7C000000u) == 0x7C000000u;
+            } else {
+                nonFinite = nonFinite || (w[i] & 0x7F800000u) == 0x7F800000u;
+            }
+        }
+        if (nonFinite) bad[col / 64] = 1;
+    }
+}
+
+/// The exact fix-up of the skip-zero-A Call form: every 64x64 tile whose
+/// column group lies in a `blockCols`-wide block of the MFMA form's tiles
+/// that met a flagged group (those the MFMA form left untouched) is computed
+/// by generalTile with the skip; the other workgroups return at once.
+/// grid.x: column groups; grid.y: row-tile strides.
+template <typename T>
+__global__ __launch_bounds__(256) void gemmFixBadColumns(mlkd_gemm p, const uint8_t* __restrict__ bad, int blockCols) {
+    __shared__ T As[16][65];
+    __shared__ T Bs[16][65];
+    const int64_t g = blockIdx.x;
+    const int per = blockCols / 64;
+    const int64_t first = g - g % per;
+    uint32_t any = 0;
+    for (int i = 0; i < per; ++i) any |= bad[first + i];
+    if (any == 0) return;
+    const int64_t rowTiles = (p.m + 63) / 64;
+    for (int64_t r = blockIdx.y; r < rowTiles; r += gridDim.y) generalTile<T>(p, r * 64, g * 64, As, Bs);
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Process default of the f16 GEMM launch form (a launch's own `variant`
@@ -1380,172 +1463,194 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 // fastest on gfx950).
 int gGemmF16Variant = 8;
 
+/// Raises the dynamic-LDS limit of every form that needs more than the
+/// default, once per process (a function-local static: its initialization
+/// is thread-safe); returns 0 or MLKD_RT_LAUNCH.
+int raiseLdsLimits() {
+    static const int rc = [] {
+        struct Need {
+            const void* fn;
+            size_t bytes;
+        };
+        const size_t ldsBytes = 4 * kTileHalves * sizeof(_Float16);
+        const size_t ldsDirect = (2 * kTileA + 2 * kTileHalves) * sizeof(_Float16);
+        const Need needs[] = {
+            {reinterpret_cast<const void*>(gemmF16Mfma<true>), ldsBytes},
+            {reinterpret_cast<const void*>(gemmF16Mfma<false>), ldsBytes},
+            {reinterpret_cast<const void*>(gemmF16Mfma4w<true>), ldsBytes},
+            {reinterpret_cast<const void*>(gemmF16Mfma4w<false>), ldsBytes},
+            {reinterpret_cast<const void*>(gemmF16Mfma4wDirect<true>), ldsDirect},
+            {reinterpret_cast<const void*>(gemmF16Mfma4wDirect<false>), ldsDirect},
+            {reinterpret_cast<const void*>(gemmF16Mfma4wPipe<true>), ldsDirect},
+            {reinterpret_cast<const void*>(gemmF16Mfma4wPipe<false>), ldsDirect},
+            {reinterpret_cast<const void*>(gemmF16Dma<true>), kLdsDma},
+            {reinterpret_cast<const void*>(gemmF16Dma<false>), kLdsDma},
+            {reinterpret_cast<const void*>(gemmF16Dma8<true>), kLdsDma},
+            {reinterpret_cast<const void*>(gemmF16Dma8<false>), kLdsDma},
+            {reinterpret_cast<const void*>(gemmF32Dma<true>), kLdsF32Dma},
+            {reinterpret_cast<const void*>(gemmF32Dma<false>), kLdsF32Dma},
+        };
+        for (const Need& n : needs) {
+            if (hipFuncSetAttribute(n.fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(n.bytes)) !=
+                hipSuccess) {
+                return static_cast<int>(MLKD_RT_LAUNCH);
+            }
+        }
+        return 0;
+    }();
+    return rc;
+}
+
+/// The MFMA form a launch takes: the f16 form (0-3, 5-8) or 100 + the f32
+/// form (0, 1); -1 when the shape, dtypes or alignment fit none of them.
+int mfmaForm(const mlkd_gemm* p) {
+    const bool fits32 = p->m < (1LL << 31) && p->n < (1LL << 31) && p->k < (1LL << 31);
+    if (p->k <= 0 || !fits32) return -1;
+    if (p->a_dtype == MLKD_F16 && p->b_dtype == MLKD_F16 && p->c_dtype == MLKD_F32 && p->m % kBM == 0 &&
+        p->n % kBN == 0 && p->k % kBK == 0 && p->lda % 8 == 0 && p->ldb % 8 == 0 && aligned16(p->a) &&
+        aligned16(p->b)) {
+        const int v = p->variant >= 0 ? p->variant : gGemmF16Variant;
+        if (v == 8) return (p->ldc % 4) == 0 && aligned16(p->c) ? 8 : 7;
+        return v == 7 || v == 5 || v == 6 || v == 3 || v == 2 || v == 1 ? v : 0;
+    }
+    if (p->a_dtype == MLKD_F32 && p->b_dtype == MLKD_F32 && p->c_dtype == MLKD_F32 && p->m % kFM == 0 &&
+        p->n % kFN == 0 && p->k % kFK == 0 && p->lda % 4 == 0 && p->ldb % 4 == 0 && aligned16(p->a) &&
+        aligned16(p->b)) {
+        const int fv = p->variant >= 0 ? p->variant : 0;
+        return fv != 1 && p->k % kQK == 0 ? 100 : 101;
+    }
+    return -1;
+}
+
+/// Output columns per workgroup tile of an MFMA form.
+int formTileCols(int form) { return form >= 100 ? kFN : (form == 5 || form == 6 ? kBN2 : kBN); }
+
+int launchMfma(const mlkd_gemm* p, int form, const uint8_t* bad, hipStream_t st) {
+    if (raiseLdsLimits() != 0) return MLKD_RT_LAUNCH;
+    const _Float16* a16 = static_cast<const _Float16*>(p->a);
+    const _Float16* b16 = static_cast<const _Float16*>(p->b);
+    float* c = static_cast<float*>(p->c);
+    const int m = static_cast<int>(p->m), n = static_cast<int>(p->n), k = static_cast<int>(p->k);
+    const bool acc = p->accumulate != 0;
+    const int tiles = static_cast<int>((p->m / kBM) * (p->n / kBN));
+    const size_t ldsBytes = 4 * kTileHalves * sizeof(_Float16);
+    const size_t ldsDirect = (2 * kTileA + 2 * kTileHalves) * sizeof(_Float16);
+    switch (form) {
+        case 8:
+            hipLaunchKernelGGL((acc ? gemmF16Dma8<true> : gemmF16Dma8<false>), dim3(tiles), dim3(512), kLdsDma, st,
+                               a16, b16, c, m, n, k, p->lda, p->ldb, p->ldc, bad);
+            break;
+        case 7:
+            hipLaunchKernelGGL((acc ? gemmF16Dma<true> : gemmF16Dma<false>), dim3(tiles), dim3(256), kLdsDma, st,
+                               a16, b16, c, m, n, k, p->lda, p->ldb, p->ldc, bad);
+            break;
+        case 5:
+        case 6: {
+            const int tiles2 = static_cast<int>((p->m / kBM2) * (p->n / kBN2));
+            auto kern = form == 5 ? (acc ? gemmF16Mfma2cu<true, true> : gemmF16Mfma2cu<false, true>)
+                                  : (acc ? gemmF16Mfma2cu<true, false> : gemmF16Mfma2cu<false, false>);
+            hipLaunchKernelGGL(kern, dim3(tiles2), dim3(256), kLdsGemm2, st, a16, b16, c, m, n, k, p->lda, p->ldb,
+                               p->ldc, bad);
+            break;
+        }
+        case 3:
+            hipLaunchKernelGGL((acc ? gemmF16Mfma4wPipe<true> : gemmF16Mfma4wPipe<false>), dim3(tiles), dim3(256),
+                               ldsDirect, st, a16, b16, c, m, n, k, p->lda, p->ldb, p->ldc, bad);
+            break;
+        case 2:
+            hipLaunchKernelGGL((acc ? gemmF16Mfma4wDirect<true> : gemmF16Mfma4wDirect<false>), dim3(tiles),
+                               dim3(256), ldsDirect, st, a16, b16, c, m, n, k, p->lda, p->ldb, p->ldc, p->accumulate,
+                               bad);
+            break;
+        case 1:
+            hipLaunchKernelGGL((acc ? gemmF16Mfma4w<true> : gemmF16Mfma4w<false>), dim3(tiles), dim3(256), ldsBytes,
+                               st, a16, b16, c, m, n, k, p->lda, p->ldb, p->ldc, p->accumulate, bad);
+            break;
+        case 0:
+            hipLaunchKernelGGL((acc ? gemmF16Mfma<true> : gemmF16Mfma<false>), dim3(tiles), dim3(512), ldsBytes, st,
+                               a16, b16, c, m, n, k, p->lda, p->ldb, p->ldc, p->accumulate, bad);
+            break;
+        case 100:
+        case 101: {
+            const int ftiles = static_cast<int>((p->m / kFM) * (p->n / kFN));
+            const float* a32 = static_cast<const float*>(p->a);
+            const float* b32 = static_cast<const float*>(p->b);
+            if (form == 100) {
+                hipLaunchKernelGGL((acc ? gemmF32Dma<true> : gemmF32Dma<false>), dim3(ftiles), dim3(256), kLdsF32Dma,
+                                   st, a32, b32, c, n, k, p->lda, p->ldb, p->ldc, bad);
+            } else {
+                hipLaunchKernelGGL((acc ? gemmF32Mfma<true> : gemmF32Mfma<false>), dim3(ftiles), dim3(256), 0, st,
+                                   a32, b32, c, m, n, k, p->lda, p->ldb, p->ldc, p->accumulate, bad);
+            }
+            break;
+        }
+        default:
+            return MLKD_RT_LAUNCH;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
+}
+
+/// Bytes of the column-group flags (one byte per 64 columns, whole 4-byte
+/// words for the fill kernel).
+int64_t flagBytes(int64_t n) { return (((n + 63) / 64) + 3) & ~int64_t{3}; }
+
 }  // namespace
 
 extern "C" void mlkd_gemm_set_variant(int variant) { gGemmF16Variant = variant; }
+
+extern "C" int64_t mlkd_gemm_scratch_bytes(const mlkd_gemm* p) {
+    if (p == nullptr || p->skip_zero_a == 0 || p->m <= 0 || p->n <= 0 || mfmaForm(p) < 0) return 0;
+    return (flagBytes(p->n) + 255) & ~int64_t{255};
+}
+
+extern "C" const char* mlkd_gemm_kernel_name(const mlkd_gemm* p) {
+    const bool acc = p->accumulate != 0;
+    switch (mfmaForm(p)) {
+        case 8: return acc ? "gemmF16Dma8<true>" : "gemmF16Dma8<false>";
+        case 7: return acc ? "gemmF16Dma<true>" : "gemmF16Dma<false>";
+        case 6: return acc ? "gemmF16Mfma2cu<true, false>" : "gemmF16Mfma2cu<false, false>";
+        case 5: return acc ? "gemmF16Mfma2cu<true, true>" : "gemmF16Mfma2cu<false, true>";
+        case 3: return acc ? "gemmF16Mfma4wPipe<true>" : "gemmF16Mfma4wPipe<false>";
+        case 2: return acc ? "gemmF16Mfma4wDirect<true>" : "gemmF16Mfma4wDirect<false>";
+        case 1: return acc ? "gemmF16Mfma4w<true>" : "gemmF16Mfma4w<false>";
+        case 0: return acc ? "gemmF16Mfma<true>" : "gemmF16Mfma<false>";
+        case 100: return acc ? "gemmF32Dma<true>" : "gemmF32Dma<false>";
+        case 101: return acc ? "gemmF32Mfma<true>" : "gemmF32Mfma<false>";
+        default: break;
+    }
+    const bool wide = p->a_dtype == MLKD_F64 || p->b_dtype == MLKD_F64 || p->c_dtype == MLKD_F64;
+    return wide ? "gemmGeneral<double>" : "gemmGeneral<float>";
+}
 
 extern "C" int mlkd_launch_gemm(const mlkd_gemm* p, void* stream) {
     if (p == nullptr || p->m < 0 || p->n < 0 || p->k < 0) return MLKD_RT_LAUNCH;
     if (p->m == 0 || p->n == 0) return 0;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const int variant = p->variant >= 0 ? p->variant : gGemmF16Variant;
-    const bool fits32 = p->m < (1LL << 31) && p->n < (1LL << 31) && p->k < (1LL << 31);
-    const bool mfma = p->skip_zero_a == 0;  // the skip runs on the general kernel only
-    if (mfma && p->k > 0 && fits32 && p->a_dtype == MLKD_F16 && p->b_dtype == MLKD_F16 &&
-        p->c_dtype == MLKD_F32 && p->m % kBM == 0 && p->n % kBN == 0 && p->k % kBK == 0 &&
-        p->lda % 8 == 0 && p->ldb % 8 == 0 && aligned16(p->a) && aligned16(p->b)) {
-        const int tiles = static_cast<int>((p->m / kBM) * (p->n / kBN));
-        const size_t ldsBytes = 4 * kTileHalves * sizeof(_Float16);
-        static bool ldsRaised = false;
-        if (!ldsRaised) {
-            if (hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF16Mfma<true>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    static_cast<int>(ldsBytes)) != hipSuccess ||
-                hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF16Mfma<false>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    static_cast<int>(ldsBytes)) != hipSuccess ||
-                hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF16Mfma4w<true>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    static_cast<int>(ldsBytes)) != hipSuccess ||
-                hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF16Mfma4w<false>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    static_cast<int>(ldsBytes)) != hipSuccess) {
-                return MLKD_RT_LAUNCH;
-            }
-            ldsRaised = true;
+    const int form = mfmaForm(p);
+    if (form >= 0 && p->skip_zero_a == 0) return launchMfma(p, form, nullptr, st);
+    if (form >= 0 && p->scratch != nullptr && p->scratch_bytes >= flagBytes(p->n)) {
+        // The skip decided on the device, per column group: flags cleared by
+        // a kernel (no memset node under capture), B scanned, the MFMA form
+        // over every tile whose columns are all finite in B, then the exact
+        // kernel over the rest. No host read-back.
+        uint8_t* bad = static_cast<uint8_t*>(p->scratch);
+        const int64_t words = flagBytes(p->n) / 4;
+        hipLaunchKernelGGL(clearWords, dim3(static_cast<unsigned>((words + 255) / 256)), dim3(256), 0, st,
+                           reinterpret_cast<uint32_t*>(bad), words);
+        const int64_t chunks = p->k * (p->n / (p->b_dtype == MLKD_F16 ? 8 : 4));
+        const unsigned scanBlocks = static_cast<unsigned>(std::min<int64_t>((chunks + 1023) / 1024, 4096));
+        if (p->b_dtype == MLKD_F16) {
+            hipLaunchKernelGGL(scanBadColumns<MLKD_F16>, dim3(scanBlocks), dim3(256), 0, st, p->b, p->k, p->n, p->ldb,
+                               bad);
+        } else {
+            hipLaunchKernelGGL(scanBadColumns<MLKD_F32>, dim3(scanBlocks), dim3(256), 0, st, p->b, p->k, p->n, p->ldb,
+                               bad);
         }
-        if (variant == 8 && (p->ldc % 4) == 0 && aligned16(p->c)) {
-            static bool raised8 = false;
-            if (!raised8) {
-                if (hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF16Dma8<true>),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        static_cast<int>(kLdsDma)) != hipSuccess ||
-                    hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF16Dma8<false>),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        static_cast<int>(kLdsDma)) != hipSuccess) {
-                    return MLKD_RT_LAUNCH;
-                }
-                raised8 = true;
-            }
-            hipLaunchKernelGGL((p->accumulate ? gemmF16Dma8<true> : gemmF16Dma8<false>), dim3(tiles), dim3(512),
-                               kLdsDma, st, static_cast<const _Float16*>(p->a), static_cast<const _Float16*>(p->b),
-                               static_cast<float*>(p->c), static_cast<int>(p->m), static_cast<int>(p->n),
-                               static_cast<int>(p->k), p->lda, p->ldb, p->ldc);
-            return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
-        }
-        if (variant == 7 || variant == 8) {
-            static bool raised7 = false;
-            if (!raised7) {
-                if (hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF16Dma<true>),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        static_cast<int>(kLdsDma)) != hipSuccess ||
-                    hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF16Dma<false>),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        static_cast<int>(kLdsDma)) != hipSuccess) {
-                    return MLKD_RT_LAUNCH;
-                }
-                raised7 = true;
-            }
-            hipLaunchKernelGGL((p->accumulate ? gemmF16Dma<true> : gemmF16Dma<false>), dim3(tiles), dim3(256),
-                               kLdsDma, st, static_cast<const _Float16*>(p->a), static_cast<const _Float16*>(p->b),
-                               static_cast<float*>(p->c), static_cast<int>(p->m), static_cast<int>(p->n),
-                               static_cast<int>(p->k), p->lda, p->ldb, p->ldc);
-            return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
-        }
-        if (variant == 5 || variant == 6) {
-            const int tiles2 = static_cast<int>((p->m / kBM2) * (p->n / kBN2));
-            auto kern = variant == 5
-                            ? (p->accumulate ? gemmF16Mfma2cu<true, true> : gemmF16Mfma2cu<false, true>)
-                            : (p->accumulate ? gemmF16Mfma2cu<true, false> : gemmF16Mfma2cu<false, false>);
-            hipLaunchKernelGGL(kern, dim3(tiles2), dim3(256), kLdsGemm2, st, static_cast<const _Float16*>(p->a),
-                               static_cast<const _Float16*>(p->b), static_cast<float*>(p->c),
-                               static_cast<int>(p->m), static_cast<int>(p->n), static_cast<int>(p->k), p->lda,
-                               p->ldb, p->ldc);
-            return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
-        }
-        if (variant == 3) {
-            const size_t ldsDirect = (2 * kTileA + 2 * kTileHalves) * sizeof(_Float16);
-            static bool raised3 = false;
-            if (!raised3) {
-                if (hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF16Mfma4wPipe<true>),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        static_cast<int>(ldsDirect)) != hipSuccess ||
-                    hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF16Mfma4wPipe<false>),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        static_cast<int>(ldsDirect)) != hipSuccess) {
-                    return MLKD_RT_LAUNCH;
-                }
-                raised3 = true;
-            }
-            hipLaunchKernelGGL((p->accumulate ? gemmF16Mfma4wPipe<true> : gemmF16Mfma4wPipe<false>), dim3(tiles),
-                               dim3(256), ldsDirect, st, static_cast<const _Float16*>(p->a),
-                               static_cast<const _Float16*>(p->b), static_cast<float*>(p->c),
-                               static_cast<int>(p->m), static_cast<int>(p->n), static_cast<int>(p->k), p->lda,
-                               p->ldb, p->ldc);
-            return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
-        }
-        if (variant == 2) {
-            const size_t ldsDirect = (2 * kTileA + 2 * kTileHalves) * sizeof(_Float16);
-            static bool raised2 = false;
-            if (!raised2) {
-                if (hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF16Mfma4wDirect<true>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    static_cast<int>(ldsDirect)) != hipSuccess ||
-                hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF16Mfma4wDirect<false>),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        static_cast<int>(ldsDirect)) != hipSuccess) {
-                    return MLKD_RT_LAUNCH;
-                }
-                raised2 = true;
-            }
-            hipLaunchKernelGGL((p->accumulate ? gemmF16Mfma4wDirect<true> : gemmF16Mfma4wDirect<false>), dim3(tiles), dim3(256), ldsDirect, st,
-                               static_cast<const _Float16*>(p->a), static_cast<const _Float16*>(p->b),
-                               static_cast<float*>(p->c), static_cast<int>(p->m), static_cast<int>(p->n),
-                               static_cast<int>(p->k), p->lda, p->ldb, p->ldc, p->accumulate);
-            return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
-        }
-        if (variant == 1) {
-            hipLaunchKernelGGL((p->accumulate ? gemmF16Mfma4w<true> : gemmF16Mfma4w<false>), dim3(tiles), dim3(256), ldsBytes, st,
-                               static_cast<const _Float16*>(p->a), static_cast<const _Float16*>(p->b),
-                               static_cast<float*>(p->c), static_cast<int>(p->m), static_cast<int>(p->n),
-                               static_cast<int>(p->k), p->lda, p->ldb, p->ldc, p->accumulate);
-            return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
-        }
-        hipLaunchKernelGGL((p->accumulate ? gemmF16Mfma<true> : gemmF16Mfma<false>), dim3(tiles), dim3(512), ldsBytes, st,
-                           static_cast<const _Float16*>(p->a), static_cast<const _Float16*>(p->b),
-                           static_cast<float*>(p->c), static_cast<int>(p->m), static_cast<int>(p->n),
-                           static_cast<int>(p->k), p->lda, p->ldb, p->ldc, p->accumulate);
-        return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
-    }
-    if (mfma && p->k > 0 && fits32 && p->a_dtype == MLKD_F32 && p->b_dtype == MLKD_F32 &&
-        p->c_dtype == MLKD_F32 && p->m % kFM == 0 && p->n % kFN == 0 && p->k % kFK == 0 &&
-        p->lda % 4 == 0 && p->ldb % 4 == 0 && aligned16(p->a) && aligned16(p->b)) {
-        const int tiles = static_cast<int>((p->m / kFM) * (p->n / kFN));
-        // f32 forms: 0 (the default) direct to the LDS ring, 1 register-staged.
-        const int fv = p->variant >= 0 ? p->variant : 0;
-        if (fv != 1 && p->k % kQK == 0) {
-            static bool raisedF = false;
-            if (!raisedF) {
-                if (hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF32Dma<true>),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        static_cast<int>(kLdsF32Dma)) != hipSuccess ||
-                    hipFuncSetAttribute(reinterpret_cast<const void*>(gemmF32Dma<false>),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        static_cast<int>(kLdsF32Dma)) != hipSuccess) {
-                    return MLKD_RT_LAUNCH;
-                }
-                raisedF = true;
-            }
-            hipLaunchKernelGGL((p->accumulate ? gemmF32Dma<true> : gemmF32Dma<false>), dim3(tiles), dim3(256),
-                               kLdsF32Dma, st, static_cast<const float*>(p->a), static_cast<const float*>(p->b),
-                               static_cast<float*>(p->c), static_cast<int>(p->n), static_cast<int>(p->k), p->lda,
-                               p->ldb, p->ldc);
-            return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
-        }
-        hipLaunchKernelGGL((p->accumulate ? gemmF32Mfma<true> : gemmF32Mfma<false>), dim3(tiles), dim3(256), 0, st,
-                           static_cast<const float*>(p->a), static_cast<const float*>(p->b),
-                           static_cast<float*>(p->c), static_cast<int>(p->m), static_cast<int>(p->n),
-                           static_cast<int>(p->k), p->lda, p->ldb, p->ldc, p->accumulate);
+        if (hipGetLastError() != hipSuccess) return MLKD_RT_LAUNCH;
+        if (const int rc = launchMfma(p, form, bad, st); rc != 0) return rc;
+        const int64_t rowTiles = (p->m + 63) / 64;
+        const dim3 grid(static_cast<unsigned>(p->n / 64), static_cast<unsigned>(std::min<int64_t>(rowTiles, 16)));
+        hipLaunchKernelGGL(gemmFixBadColumns<float>, grid, dim3(256), 0, st, *p, bad, formTileCols(form));
         return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
     }
     const int64_t tiles = ((p->m + 63) / 64) * ((p->n + 63) / 64);

@@ -33,17 +33,6 @@ __global__ void fillKernel(uint32_t* p, uint32_t v, int64_t n) {
     }
 }
 
-/// Sets *flag to 1 when any of the n elements is an infinity or a NaN.
-template <typename T>
-__global__ void nonfiniteKernel(const T* p, int64_t n, uint32_t* flag) {
-    bool any = false;
-    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
-         i += (int64_t)gridDim.x * blockDim.x) {
-        any = any || !__builtin_isfinite(static_cast<double>(p[i]));
-    }
-    if (any) *flag = 1u;
-}
-
 }  // namespace
 
 extern "C" {
@@ -64,22 +53,6 @@ int mlkd_rt_noalloc_scratch(void** ptr, size_t* bytes) {
     *ptr = gScratchPtr[dev];
     *bytes = kNoAllocScratchBytes;
     return 0;
-}
-
-int mlkd_rt_scan_nonfinite(const void* p, int dtype, int64_t n, uint32_t* flag, void* stream) {
-    if (n <= 0) return 0;
-    int64_t blocks = (n + 255) / 256;
-    if (blocks > 4096) blocks = 4096;
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    const dim3 g(static_cast<unsigned>(blocks)), b(256);
-    if (dtype == MLKD_F32) {
-        hipLaunchKernelGGL(nonfiniteKernel<float>, g, b, 0, st, static_cast<const float*>(p), n, flag);
-    } else if (dtype == MLKD_F16) {
-        hipLaunchKernelGGL(nonfiniteKernel<_Float16>, g, b, 0, st, static_cast<const _Float16*>(p), n, flag);
-    } else {
-        hipLaunchKernelGGL(nonfiniteKernel<double>, g, b, 0, st, static_cast<const double*>(p), n, flag);
-    }
-    return mapErr(hipGetLastError(), MLKD_RT_LAUNCH);
 }
 
 int mlkd_rt_device_count(void) {

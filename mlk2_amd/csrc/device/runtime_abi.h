@@ -35,9 +35,6 @@ int mlkd_rt_fill32(void* p, uint32_t value, size_t bytes, void* stream);
 /// address (hipGetSymbolAddress of the file-scope array, taken once per
 /// device) and size. Allocates nothing.
 int mlkd_rt_noalloc_scratch(void** ptr, size_t* bytes);
-/// Sets *flag (which the caller zeroes) to 1 when any of the n elements of
-/// `p` (dtype MLKD_F32 / F16 / F64) is an infinity or a NaN.
-int mlkd_rt_scan_nonfinite(const void* p, int dtype, int64_t n, uint32_t* flag, void* stream);
 int mlkd_rt_sync(void* stream);
 int mlkd_rt_device_sync(void);
 int mlkd_rt_stream_create(void** s);
@@ -85,8 +82,21 @@ int mlkd_launch_softmax(const mlkd_softmax* p, void* stream);
 /// with plain stores; waves <= 0 keeps the default grid).
 void mlkd_softmax_set_variant(int variant, int64_t waves);
 int mlkd_launch_gemm(const mlkd_gemm* p, void* stream);
-/// Process default of the f16 GEMM launch form (7: direct-to-LDS ring, the
-/// default; 0: 8 waves x 128x64; 1: 4 waves x 128x128; 2: A direct to LDS;
+/// The symbol of the kernel mlkd_launch_gemm runs for `p` (the MFMA form, or
+/// the general kernel; a skip-zero-A launch adds the column scan and the
+/// fix-up around the form), as profilers print it without the parameters.
+const char* mlkd_gemm_kernel_name(const mlkd_gemm* p);
+/// Likewise for the softmax launch (valid until this thread's next call).
+const char* mlkd_softmax_kernel_name(const mlkd_softmax* p);
+/// Likewise for score-softmax: its kernels joined by '+' (valid until this
+/// thread's next call).
+const char* mlkd_score_kernel_names(const mlkd_score_softmax* p);
+/// Scratch bytes the skip-zero-A form of `p` needs to take an MFMA form (the
+/// column-group flags of B); 0 when it runs on the general kernel anyway.
+int64_t mlkd_gemm_scratch_bytes(const mlkd_gemm* p);
+/// Process default of the f16 GEMM launch form (8: direct-to-LDS ring with 8
+/// waves of 16x16x32 tiles, the default; 7: the same ring with 4 waves of
+/// 32x32x16; 0: 8 waves x 128x64; 1: 4 waves x 128x128; 2: A direct to LDS;
 /// 3: pipelined step; 5/6: 128x256 tiles, two workgroups per CU).
 void mlkd_gemm_set_variant(int variant);
 int mlkd_launch_score_softmax(const mlkd_score_softmax* p, void* stream);

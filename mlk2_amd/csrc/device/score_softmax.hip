@@ -12,6 +12,8 @@
 //   * a scalar f64 path for other dtypes.
 #include <hip/hip_runtime.h>
 
+#include <cstdio>
+
 #include <stdint.h>
 
 #include "mlk_device_math.h"
@@ -313,17 +315,15 @@ __global__ __launch_bounds__(256, 2) void scoreStoreQ(const _Float16* __restrict
 
 int launchQ(const mlkd_score_softmax* p, hipStream_t st) {
     const size_t ldsStats = kLdsStoreQ + static_cast<size_t>(p->seq / 2) * sizeof(float);
-    static bool attrs = false;
-    if (!attrs) {
+    // Once per process; a function-local static initializes thread-safely.
+    static const bool attrs = [] {
         const size_t maxStats = kLdsStoreQ + static_cast<size_t>(kMaxSeqQ / 2) * sizeof(float);
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(scoreStatsQ), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                static_cast<int>(maxStats)) != hipSuccess ||
-            hipFuncSetAttribute(reinterpret_cast<const void*>(scoreStoreQ), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                static_cast<int>(kLdsStoreQ)) != hipSuccess) {
-            return MLKD_RT_LAUNCH;
-        }
-        attrs = true;
-    }
+        return hipFuncSetAttribute(reinterpret_cast<const void*>(scoreStatsQ), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   static_cast<int>(maxStats)) == hipSuccess &&
+               hipFuncSetAttribute(reinterpret_cast<const void*>(scoreStoreQ), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   static_cast<int>(kLdsStoreQ)) == hipSuccess;
+    }();
+    if (!attrs) return MLKD_RT_LAUNCH;
     const unsigned blocks = static_cast<unsigned>(p->batch * (p->seq / 128) * 2);
     // Both passes work in base 2: v2 = acc * (log2(e) / div) + bias * log2(e),
     // exp(v - max) = exp2(v2 - max2).
@@ -390,6 +390,32 @@ extern "C" void mlkd_score_set_variant(int variant) { gScoreVariant = variant; }
 
 extern "C" int64_t mlkd_score_scratch_bytes(const mlkd_score_softmax* p) {
     return p != nullptr && twoPassApplies(p) ? scratch2(p) : 0;
+}
+
+extern "C" const char* mlkd_score_kernel_names(const mlkd_score_softmax* p) {
+    static thread_local char name[160];
+    const int variant = p->variant >= 0 ? p->variant : gScoreVariant;
+    if (variant != 1 && twoPassApplies(p) && p->scratch != nullptr &&
+        (reinterpret_cast<uintptr_t>(p->scratch) & 7u) == 0 && p->scratch_bytes >= scratch2(p)) {
+        return "scoreStatsQ+scoreStoreQ";
+    }
+    const bool fast = p->qk_dtype == MLKD_F16 && p->bias_dtype == MLKD_F32 && p->s_dtype == MLKD_F32 &&
+                      p->seq % 128 == 0 && p->dim % 16 == 0 && p->dim > 0 && p->seq < (1 << 20) &&
+                      (reinterpret_cast<uintptr_t>(p->q) & 15u) == 0 &&
+                      (reinterpret_cast<uintptr_t>(p->k) & 15u) == 0 && p->dim % 8 == 0;
+    mlkd_softmax sm;
+    sm.variant = -1;
+    sm.pad = 0;
+    sm.x = p->s;
+    sm.y = p->s;
+    sm.x_dtype = p->s_dtype;
+    sm.y_dtype = p->s_dtype;
+    sm.rows = p->batch * p->seq;
+    sm.cols = p->seq;
+    sm.x_row_stride = p->seq;
+    sm.y_row_stride = p->seq;
+    std::snprintf(name, sizeof(name), "%s+%s", fast ? "scoresF16" : "scoresGeneral", mlkd_softmax_kernel_name(&sm));
+    return name;
 }
 
 extern "C" int mlkd_launch_score_softmax(const mlkd_score_softmax* p, void* stream) {

@@ -16,6 +16,8 @@
 // the row with LDS reductions, f64 throughout.
 #include <hip/hip_runtime.h>
 
+#include <cstdio>
+
 #include <math.h>
 #include <stdint.h>
 
@@ -304,6 +306,29 @@ int launchWave(const mlkd_softmax& p, hipStream_t st) {
 extern "C" void mlkd_softmax_set_variant(int variant, int64_t waves) {
     gSoftmaxVariant = variant;
     gSoftmaxWaves = waves;
+}
+
+extern "C" const char* mlkd_softmax_kernel_name(const mlkd_softmax* p) {
+    static thread_local char name[96];
+    const bool aligned = (reinterpret_cast<uintptr_t>(p->x) & 15u) == 0 &&
+                         (reinterpret_cast<uintptr_t>(p->y) & 15u) == 0 &&
+                         (p->x_row_stride & 3) == 0 && (p->y_row_stride & 3) == 0;
+    if (!(p->x_dtype == MLKD_F32 && p->y_dtype == MLKD_F32 && (p->cols & 3) == 0 && aligned && p->cols <= 8192)) {
+        return "softmaxBlockRow";
+    }
+    int ch = 1;
+    while (256 * ch < p->cols) ch *= 2;
+    const int variant = p->variant >= 0 ? p->variant : gSoftmaxVariant;
+    if (variant == 1) {
+        std::snprintf(name, sizeof(name), "softmaxWaveRowPipelined<%d>", ch);
+    } else if (variant == 5) {
+        std::snprintf(name, sizeof(name), "softmaxWaveRowPair<%d, %s>", ch, p->cols == 256 * ch ? "true" : "false");
+    } else {
+        const bool fastExp = variant != 2 && variant != 4, nt = variant != 3 && variant != 4;
+        std::snprintf(name, sizeof(name), "softmaxWaveRow<%d, %s, %s>", ch, fastExp ? "true" : "false",
+                      nt ? "true" : "false");
+    }
+    return name;
 }
 
 extern "C" int mlkd_launch_softmax(const mlkd_softmax* p, void* stream) {

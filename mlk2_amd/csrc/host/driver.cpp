@@ -119,20 +119,48 @@ Result<std::unique_ptr<HipLoadedKernel>> buildHipKernelArtifact(const KernelModu
     k->fingerprint_ = artifactFingerprint(k->km_, k->plan_, config.arch);
     k->fromCache_ = applyCachedVariants(config.cacheDir, k->fingerprint_, k->km_, k->plan_);
     k->nestFormFn_.assign(k->plan_.steps.size(), std::array<void*, 5>{});
+    for (size_t si = 0; si < k->plan_.steps.size(); ++si) {
+        const Step& st = k->plan_.steps[si];
+        if (st.kind != StepKind::Nest || st.variant < 1 || st.variant > 4) continue;
+        void* fn = nullptr;
+        std::string why;
+        if (k->ensureNestForm(si, st.variant, fn, why) != MLKHIP_OK) {
+            return err(ErrorCode::UnsupportedCapability, "cached loop-nest launch form: " + why);
+        }
+    }
     return k;
+}
+
+void HipLoadedKernel::freeScratch(RunScratch& rs) {
+    for (void* p : rs.temp) {
+        if (p != nullptr) mlkd_rt_free(p);
+    }
+    if (rs.status != nullptr) mlkd_rt_free(rs.status);
+    for (void* p : rs.step) {
+        if (p != nullptr) mlkd_rt_free(p);
+    }
 }
 
 HipLoadedKernel::~HipLoadedKernel() {
     for (auto& [stream, rs] : scratchByStream_) {
         (void)stream;
-        for (void* p : rs->temp) {
-            if (p != nullptr) mlkd_rt_free(p);
-        }
-        if (rs->status != nullptr) mlkd_rt_free(rs->status);
-        for (void* p : rs->step) {
-            if (p != nullptr) mlkd_rt_free(p);
-        }
+        freeScratch(*rs);
     }
+}
+
+int HipLoadedKernel::releaseStreamScratch(void* stream, std::string& why) {
+    std::lock_guard<std::mutex> g(scratchLock_);
+    for (size_t i = 0; i < scratchByStream_.size(); ++i) {
+        if (scratchByStream_[i].first != stream) continue;
+        if (mlkd_rt_sync(stream) != 0) {
+            why = "stream wait failed";
+            return MLKHIP_LAUNCH;
+        }
+        freeScratch(*scratchByStream_[i].second);
+        scratchByStream_.erase(scratchByStream_.begin() + static_cast<std::ptrdiff_t>(i));
+        return MLKHIP_OK;
+    }
+    return MLKHIP_OK;
 }
 
 HipLoadedKernel::RunScratch& HipLoadedKernel::scratchFor(void* stream) const {
@@ -169,6 +197,96 @@ void HipLoadedKernel::fillScoreParams(const Step& st, const std::vector<void*>& 
     p.scratch_bytes = 0;
 }
 
+int HipLoadedKernel::ensureNestForm(size_t si, int form, void*& fn, std::string& why) const {
+    std::lock_guard<std::mutex> g(scratchLock_);
+    if (nestFormFn_[si][form] == nullptr) {
+        const std::string src = nestFormSource(plan_.steps[si], form);
+        if (src.empty()) {
+            why = "loop-nest launch form " + std::to_string(form) + " is not declared for this step";
+            return MLKHIP_REFUSED;
+        }
+        char log[4096] = {0};
+        uint64_t fp = 0;
+        if (mlkd_jit_build(src.data(), src.size(), "mlk_nest", arch_.c_str(), cacheDir_.c_str(),
+                           &nestFormFn_[si][form], &fp, log, sizeof(log)) != 0) {
+            nestFormFn_[si][form] = nullptr;
+            why = "loop-nest launch form " + std::to_string(form) + ": " + log;
+            return MLKHIP_RUNTIME;
+        }
+    }
+    fn = nestFormFn_[si][form];
+    return MLKHIP_OK;
+}
+
+void HipLoadedKernel::fillSoftmaxParams(const Step& st, const std::vector<void*>& ptr, mlkd_softmax& p) const {
+    p.variant = st.variant;
+    p.pad = 0;
+    p.x = ptr[st.x];
+    p.y = ptr[st.y];
+    p.x_dtype = dtypeCode(km_.buffers[st.x].dtype);
+    p.y_dtype = dtypeCode(km_.buffers[st.y].dtype);
+    p.rows = st.rows;
+    p.cols = st.cols;
+    p.x_row_stride = st.cols;
+    p.y_row_stride = st.kind == StepKind::Softmax ? st.cols : 1;
+}
+
+const char* HipLoadedKernel::stepKernelName(size_t si) const {
+    const Step& st = plan_.steps[si];
+    std::string name = st.kernelName;
+    if (name.empty()) {
+        // What the launcher picks for this step's shape, dtypes and pinned
+        // form, on device buffers as the runtime allocates them (256-byte
+        // aligned) with the scratch the driver gives it.
+        std::vector<void*> ptr(km_.buffers.size(), reinterpret_cast<void*>(uintptr_t{1} << 12));
+        if (st.kind == StepKind::Softmax) {
+            mlkd_softmax p;
+            fillSoftmaxParams(st, ptr, p);
+            name = mlkd_softmax_kernel_name(&p);
+        } else if (st.kind == StepKind::RowSum) {
+            name = "rowSumWave";
+        } else if (st.kind == StepKind::Gemm) {
+            mlkd_gemm p;
+            fillGemmParams(st, ptr, p);
+            if (const int64_t need = mlkd_gemm_scratch_bytes(&p); need > 0) {
+                p.scratch = ptr[0];
+                p.scratch_bytes = need;
+            }
+            name = mlkd_gemm_kernel_name(&p);
+        } else if (st.kind == StepKind::ScoreSoftmax) {
+            mlkd_score_softmax p;
+            fillScoreParams(st, ptr, p);
+            if (const int64_t need = mlkd_score_scratch_bytes(&p); need > 0) {
+                p.scratch = ptr[0];
+                p.scratch_bytes = need;
+            }
+            name = mlkd_score_kernel_names(&p);
+        }
+    }
+    std::lock_guard<std::mutex> g(scratchLock_);
+    return kernelNames_.insert(name).first->c_str();
+}
+
+void HipLoadedKernel::fillGemmParams(const Step& st, const std::vector<void*>& ptr, mlkd_gemm& p) const {
+    p.variant = st.variant;
+    p.skip_zero_a = st.skipZeroA && st.k > 0 ? 1 : 0;
+    p.a = ptr[st.a];
+    p.b = ptr[st.b];
+    p.c = ptr[st.c];
+    p.a_dtype = dtypeCode(km_.buffers[st.a].dtype);
+    p.b_dtype = dtypeCode(km_.buffers[st.b].dtype);
+    p.c_dtype = dtypeCode(km_.buffers[st.c].dtype);
+    p.accumulate = st.accumulate ? 1 : 0;
+    p.m = st.m;
+    p.n = st.n;
+    p.k = st.k;
+    p.lda = st.lda;
+    p.ldb = st.ldb;
+    p.ldc = st.ldc;
+    p.scratch = nullptr;
+    p.scratch_bytes = 0;
+}
+
 int HipLoadedKernel::arenaLayout(const DeviceBinding* binds, int64_t elements, const ScratchArena& arena,
                                  std::vector<size_t>& tempOff, std::vector<size_t>& stepOff,
                                  std::string& why) const {
@@ -192,19 +310,29 @@ int HipLoadedKernel::arenaLayout(const DeviceBinding* binds, int64_t elements, c
                   "read-back, which the allocation-free entry does not do";
             return MLKHIP_REFUSED;
         }
-        if (st.kind == StepKind::Nest && st.variant >= 1 && st.variant <= 4 && nestFormFn_[si][st.variant] == nullptr) {
-            why = "step " + std::to_string(si) + " pins loop-nest launch form " + std::to_string(st.variant) +
-                  ", which is not loaded yet";
-            return MLKHIP_REFUSED;
+        if (st.kind == StepKind::Nest && st.variant >= 1 && st.variant <= 4) {
+            // Pinned forms are compiled when they are pinned (at build from
+            // the variant cache, or by setStepVariant); this is a guard.
+            std::lock_guard<std::mutex> g(scratchLock_);
+            if (nestFormFn_[si][st.variant] == nullptr) {
+                why = "step " + std::to_string(si) + " pins loop-nest launch form " + std::to_string(st.variant) +
+                      ", which is not loaded";
+                return MLKHIP_REFUSED;
+            }
         }
+        int64_t need = 0;
         if (st.kind == StepKind::ScoreSoftmax) {
             mlkd_score_softmax p;
             fillScoreParams(st, ptr, p);
-            const int64_t need = mlkd_score_scratch_bytes(&p);
-            if (need > 0) {
-                stepOff[si] = used;
-                used += align256(static_cast<size_t>(need));
-            }
+            need = mlkd_score_scratch_bytes(&p);
+        } else if (st.kind == StepKind::Gemm) {
+            mlkd_gemm p;
+            fillGemmParams(st, ptr, p);
+            need = mlkd_gemm_scratch_bytes(&p);
+        }
+        if (need > 0) {
+            stepOff[si] = used;
+            used += align256(static_cast<size_t>(need));
         }
     }
     if (used > arena.bytes) {
@@ -336,56 +464,34 @@ int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* 
             case StepKind::Softmax:
             case StepKind::RowSum: {
                 mlkd_softmax p;
-                p.variant = st.variant;
-                p.pad = 0;
-                p.x = ptr[st.x];
-                p.y = ptr[st.y];
-                p.x_dtype = dtypeCode(km_.buffers[st.x].dtype);
-                p.y_dtype = dtypeCode(km_.buffers[st.y].dtype);
-                p.rows = st.rows;
-                p.cols = st.cols;
-                p.x_row_stride = st.cols;
-                p.y_row_stride = st.kind == StepKind::Softmax ? st.cols : 1;
+                fillSoftmaxParams(st, ptr, p);
                 rc = st.kind == StepKind::Softmax ? mlkd_launch_softmax(&p, stream) : mlkd_launch_rowsum(&p, stream);
                 break;
             }
             case StepKind::Gemm: {
                 mlkd_gemm p;
-                p.variant = st.variant;
-                p.skip_zero_a = 0;
-                p.a = ptr[st.a];
-                p.b = ptr[st.b];
-                p.c = ptr[st.c];
-                p.a_dtype = dtypeCode(km_.buffers[st.a].dtype);
-                p.b_dtype = dtypeCode(km_.buffers[st.b].dtype);
-                p.c_dtype = dtypeCode(km_.buffers[st.c].dtype);
-                p.accumulate = st.accumulate ? 1 : 0;
-                p.m = st.m;
-                p.n = st.n;
-                p.k = st.k;
-                p.lda = st.lda;
-                p.ldb = st.ldb;
-                p.ldc = st.ldc;
-                if (st.skipZeroA && st.k > 0 && arena != nullptr) {
-                    // No host read-back here: always the exact skip kernel.
-                    p.skip_zero_a = 1;
-                } else if (st.skipZeroA && st.k > 0) {
-                    // 0 * inf and 0 * NaN are the only products whose skip
-                    // changes C beyond the sign of a zero sum, so the MFMA
-                    // forms run unless B holds a non-finite value.
-                    void* flag = statusWord();
-                    uint32_t any = 0;
-                    if (flag == nullptr) {
-                        why = "status word allocation failed";
-                        return MLKHIP_RUNTIME;
+                fillGemmParams(st, ptr, p);
+                // The skip-zero-A decision (0 * inf and 0 * NaN are the only
+                // products whose skip changes C beyond the sign of a zero
+                // sum) is taken on the device per column block of B, in the
+                // flags this scratch holds; no host read-back.
+                if (const int64_t need = mlkd_gemm_scratch_bytes(&p); need > 0 && arena != nullptr) {
+                    p.scratch = arena->base + stepOff[si];
+                    p.scratch_bytes = need;
+                } else if (need > 0) {
+                    std::lock_guard<std::mutex> g(scratchLock_);
+                    if (rs->step[si] == nullptr || rs->stepBytes[si] < need) {
+                        if (rs->step[si] != nullptr) mlkd_rt_free(rs->step[si]);
+                        rs->step[si] = nullptr;
+                        if (mlkd_rt_malloc(&rs->step[si], static_cast<size_t>(need)) != 0) {
+                            rs->step[si] = nullptr;
+                            why = "matmul flag scratch allocation failed";
+                            return MLKHIP_RUNTIME;
+                        }
+                        rs->stepBytes[si] = need;
                     }
-                    if (mlkd_rt_fill32(flag, 0u, 4, stream) != 0 ||
-                        mlkd_rt_scan_nonfinite(p.b, p.b_dtype, st.k * st.n, static_cast<uint32_t*>(flag), stream) != 0 ||
-                        mlkd_rt_d2h(&any, flag, sizeof(any), stream) != 0 || mlkd_rt_sync(stream) != 0) {
-                        why = "non-finite scan of B failed";
-                        return MLKHIP_LAUNCH;
-                    }
-                    p.skip_zero_a = any != 0 ? 1 : 0;
+                    p.scratch = rs->step[si];
+                    p.scratch_bytes = rs->stepBytes[si];
                 }
                 rc = mlkd_launch_gemm(&p, stream);
                 break;
@@ -421,23 +527,7 @@ int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* 
                 void* fn = st.fn;
                 const unsigned wg = nestFormThreads(form);
                 if (form != 0) {
-                    std::lock_guard<std::mutex> g(scratchLock_);
-                    if (nestFormFn_[si][form] == nullptr) {
-                        const std::string src = nestFormSource(st, form);
-                        if (src.empty()) {
-                            why = "loop-nest launch form " + std::to_string(form) + " is not declared for this step";
-                            return MLKHIP_REFUSED;
-                        }
-                        char log[4096] = {0};
-                        uint64_t fp = 0;
-                        if (mlkd_jit_build(src.data(), src.size(), "mlk_nest", arch_.c_str(), cacheDir_.c_str(),
-                                           &nestFormFn_[si][form], &fp, log, sizeof(log)) != 0) {
-                            nestFormFn_[si][form] = nullptr;
-                            why = "loop-nest launch form " + std::to_string(form) + ": " + log;
-                            return MLKHIP_RUNTIME;
-                        }
-                    }
-                    fn = nestFormFn_[si][form];
+                    if (const int frc = ensureNestForm(si, form, fn, why); frc != MLKHIP_OK) return frc;
                 }
                 rc = mlkd_jit_launch_nest(fn, gridFor(instances, wg), wg, &na, &sc, instances, stream);
                 if (rc == 0 && checked) {
@@ -693,6 +783,13 @@ int mlkhip_jit_options(const char* arch, char* buf, size_t cap) { return mlkd_ji
 
 void mlkhip_release(mlkhip_artifact* a) { delete a; }
 
+int mlkhip_release_stream_scratch(mlkhip_artifact* a, void* stream) {
+    if (a == nullptr) return setError(MLKHIP_BAD_BINDING, "null artifact");
+    std::string why;
+    const int rc = a->k->releaseStreamScratch(stream, why);
+    return rc == MLKHIP_OK ? rc : setError(rc, why);
+}
+
 int mlkhip_is_multidim(const mlkhip_artifact* a) { return a != nullptr && a->k->plan().multiDim ? 1 : 0; }
 
 const char* mlkhip_class_name(const mlkhip_artifact* a) { return a != nullptr ? a->k->plan().className.c_str() : ""; }
@@ -854,7 +951,7 @@ int mlkhip_plan_variants(const char* module_json, size_t len, int step, int* out
 
 const char* mlkhip_step_kernel_name(const mlkhip_artifact* a, int step) {
     if (a == nullptr || step < 0 || static_cast<size_t>(step) >= a->k->plan().steps.size()) return "";
-    return a->k->plan().steps[static_cast<size_t>(step)].kernelName.c_str();
+    return a->k->stepKernelName(static_cast<size_t>(step));
 }
 
 int mlkhip_step_variant(const mlkhip_artifact* a, int step) {

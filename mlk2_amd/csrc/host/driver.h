@@ -10,6 +10,7 @@
 #include <memory>
 #include <array>
 #include <mutex>
+#include <set>
 #include <string>
 #include <vector>
 
@@ -51,9 +52,9 @@ public:
 
     /// Device-resident run on `stream`; returns an ABI status code and sets
     /// `why` on failure. With `arena`, every scratch buffer (temps, launcher
-    /// scratch) is carved out of it and nothing is allocated; steps that
-    /// need a host read-back are refused (checked loop nests), and a
-    /// Call(MatMul) step runs the exact skip kernel without the scan.
+    /// scratch, the Call(MatMul) column flags) is carved out of it and
+    /// nothing is allocated; steps that need a host read-back are refused
+    /// (checked loop nests).
     int runDevice(const DeviceBinding* binds, int n, const double* scalars, int64_t nScalars,
                   int64_t elements, void* stream, std::string& why, const ScratchArena* arena = nullptr) const;
 
@@ -70,6 +71,14 @@ public:
     /// Pins step `step` to launch form `variant` (-1: the kernel's default);
     /// refuses a form outside the step's variant space.
     int setStepVariant(int step, int variant, std::string& why);
+
+    /// The kernel symbol step `si` launches (its hipRTC instance, or the
+    /// precompiled kernel its launcher picks for the step's shape, dtypes
+    /// and pinned form); the text lives as long as the artifact.
+    const char* stepKernelName(size_t si) const;
+
+    /// Waits for `stream`, then frees the scratch set runs on it allocated.
+    int releaseStreamScratch(void* stream, std::string& why);
 
     /// Times every launch form of every step that has more than one on the
     /// caller's device buffers, certifies each against the default form's
@@ -94,11 +103,12 @@ private:
     std::vector<int> bindIndex_;        // buffer id -> bindable index or -1
     // Artifact-owned device scratch of the runs on one stream: temps (zeroed
     // on every run like the reference's fresh temp storage), the status word
-    // of loop-nest steps with run-time bounds checks and of the non-finite
-    // scan, and per-step scratch a launcher asks for (score-softmax row
-    // statistics). Allocated on first use and kept until the artifact is
-    // released. Each stream gets its own set, so runs on different streams
-    // never share device memory; runs on one stream are ordered by it.
+    // of loop-nest steps with run-time bounds checks, and per-step scratch a
+    // launcher asks for (score-softmax row statistics, the Call(MatMul)
+    // column flags). Allocated on first use and kept until the artifact or
+    // the stream's set is released (releaseStreamScratch). Each stream gets
+    // its own set, so runs on different streams never share device memory;
+    // runs on one stream are ordered by it.
     struct RunScratch {
         std::vector<void*> temp;
         std::vector<int64_t> tempElems;
@@ -107,11 +117,18 @@ private:
         std::vector<int64_t> stepBytes;
     };
     RunScratch& scratchFor(void* stream) const;  // caller holds scratchLock_
+    static void freeScratch(RunScratch& rs);
     /// Offsets of a run's scratch in `arena`; refuses what does not fit or
     /// needs a host read-back.
     int arenaLayout(const DeviceBinding* binds, int64_t elements, const ScratchArena& arena,
                     std::vector<size_t>& tempOff, std::vector<size_t>& stepOff, std::string& why) const;
     void fillScoreParams(const Step& st, const std::vector<void*>& ptr, mlkd_score_softmax& p) const;
+    void fillGemmParams(const Step& st, const std::vector<void*>& ptr, mlkd_gemm& p) const;
+    void fillSoftmaxParams(const Step& st, const std::vector<void*>& ptr, mlkd_softmax& p) const;
+    mutable std::set<std::string> kernelNames_;  // under scratchLock_
+    /// Loop-nest launch form `form` (1-4) of step `si`, compiled on first
+    /// use under scratchLock_.
+    int ensureNestForm(size_t si, int form, void*& fn, std::string& why) const;
     mutable std::mutex scratchLock_;
     mutable std::vector<std::pair<void*, std::unique_ptr<RunScratch>>> scratchByStream_;
     // Loop-nest launch forms 1-4 (no LDS slabs; 512 and 64 threads per

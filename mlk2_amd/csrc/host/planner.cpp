@@ -428,10 +428,16 @@ Result<Step> elementwiseNest(const KernelModule& km, const NestInfo& ni) {
     auto bits = [&km](const KernelOperand& o) {
         return o.kind == K::ElemIdx ? streamBits(km, o.index) : 99;
     };
-    auto body = chainCode(cp.exprs, cp.family == "poly7", f32Out, streamCode(streamOf), "return ", bits);
-    if (!body.has_value()) return err(body.error().code, body.error().message);
     auto exact = chainCode(cp.exprs, cp.family == "poly7", false, streamCode(streamOf), "return ", bits);
     if (!exact.has_value()) return err(exact.error().code, exact.error().message);
+    // The fast forms' exact pass re-reads its inputs after the vector stores.
+    // A chain that reads the buffer it stores would re-read its own results,
+    // so it runs the exact forms from the start.
+    bool inPlace = false;
+    for (const StreamRef& s : ins) inPlace = inPlace || s.buffer == so.bufferOut;
+    auto body = inPlace ? exact
+                        : chainCode(cp.exprs, cp.family == "poly7", f32Out, streamCode(streamOf), "return ", bits);
+    if (!body.has_value()) return err(body.error().code, body.error().message);
     if (*exact != *body) st.chainExact = *exact;
     if (bad) return err(ErrorCode::UnsupportedCapability, "more than 4 distinct element streams");
     for (const StreamRef& s : ins) {
@@ -525,10 +531,15 @@ Result<std::vector<Step>> tier1Loop(const KernelModule& km, const KernelNode& lo
             return o.kind == K::ElemA ? streamBits(km, c.bufferA == kInvalidId ? -1 : static_cast<int64_t>(c.bufferA))
                                       : (o.kind == K::ElemB ? streamBits(km, c.bufferB == kInvalidId ? -1 : static_cast<int64_t>(c.bufferB)) : 99);
         };
-        auto body = chainCode(exprs, c.family == "poly7", od == Dtype::F32, streamCode(streamOf), "return ", bits);
-        if (!body.has_value()) return err(body.error().code, body.error().message);
         auto exact = chainCode(exprs, c.family == "poly7", false, streamCode(streamOf), "return ", bits);
         if (!exact.has_value()) return err(exact.error().code, exact.error().message);
+        // In place: exact forms throughout, as in the n-D path (the fast
+        // forms' exact pass would re-read stored results).
+        bool inPlace = false;
+        for (const StreamRef& s : st.inputs) inPlace = inPlace || s.buffer == so.bufferOut;
+        auto body = inPlace ? exact
+                            : chainCode(exprs, c.family == "poly7", od == Dtype::F32, streamCode(streamOf), "return ", bits);
+        if (!body.has_value()) return err(body.error().code, body.error().message);
         st.chainBody = *body;
         if (*exact != *body) st.chainExact = *exact;
         st.out = ref(so.bufferOut);

@@ -502,6 +502,12 @@ int HipLoadedKernel::setStepVariant(int step, int variant, std::string& why) {
             return MLKHIP_BAD_BINDING;
         }
     }
+    const Step& st = plan_.steps[static_cast<size_t>(step)];
+    if (st.kind == StepKind::Nest && variant >= 1 && variant <= 4) {
+        // Compiled now, so the allocation-free entry finds it loaded.
+        void* fn = nullptr;
+        if (const int rc = ensureNestForm(static_cast<size_t>(step), variant, fn, why); rc != MLKHIP_OK) return rc;
+    }
     plan_.steps[static_cast<size_t>(step)].variant = variant;
     return MLKHIP_OK;
 }

@@ -2,8 +2,9 @@
 
 * Call(MatMul) skips A[i,p] == 0 (gemmRowBlock, runtime/src/execution/
   kernel_buffers.cpp:422): 0 * inf or 0 * NaN in B must not reach C. The
-  backend scans B for non-finite values and runs the exact skip kernel when
-  there are any; otherwise the MFMA forms.
+  backend flags, on the device, the column groups of B that hold non-finite
+  values; the MFMA form computes the other tiles and the exact skip kernel
+  the flagged ones.
 * A fused class keeps its temps on chip only when no other root reads them;
   a later root that reads the softmax row max, or the scaled scores, makes
   the nest run with the walker's materialized temps (kernel_buffers.cpp:
@@ -90,6 +91,38 @@ def test_skip_zero_a_with_nonfinite_b(hip, dt_in, dt_out, m, k, n):
     ref2 = oracle.run(call, {0: A.reshape(-1), 1: Bf.reshape(-1)}, init={2: C0})[2]
     got2 = hip.build(call).run({0: A, 1: Bf, 2: C0})[2]
     assert np.isfinite(got2).all() and max_rel(got2, ref2) <= tol
+
+
+@pytest.mark.parametrize("dt_in,m,k,n,variant", [("f16", 512, 256, 1024, None), ("f16", 512, 256, 1024, 7),
+                                                  ("f16", 256, 128, 1024, 5), ("f32", 256, 128, 512, None)])
+def test_skip_zero_a_mixes_mfma_and_exact_tiles(hip, dt_in, m, k, n, variant):
+    # Non-finite values of B only in columns 300-309: one 256-wide block of
+    # the f16 forms (one 64-wide group of the f32 form). The other tiles take
+    # the MFMA form, the flagged ones the exact kernel, in one run, with C
+    # accumulated from a non-zero start.
+    rng = np.random.default_rng(6)
+    A = rng.uniform(-1, 1, (m, k))
+    B = rng.uniform(-1, 1, (k, n))
+    B[5, 300:305] = np.inf
+    B[k - 2, 305:310] = np.nan
+    A[:, 5] = 0.0
+    A[:, k - 2] = 0.0
+    A[7, 5] = 0.25                               # row 7 reads the infinities
+    np_dt = {"f32": np.float32, "f16": np.float16}[dt_in]
+    A = A.astype(np_dt).astype(np.float64)
+    B = B.astype(np_dt).astype(np.float64)
+    C0 = rng.uniform(-1, 1, m * n)
+    call = fx.matmul_call_module(m, k, n, dt_in, "f32")
+    art = hip.build(call)
+    if variant is not None:
+        art.set_step_variant(0, variant)
+    ref = oracle.run(call, {0: A.reshape(-1), 1: B.reshape(-1)}, init={2: C0})[2]
+    got = art.run({0: A, 1: B, 2: C0})[2]
+    tol = 1e-5 * math.sqrt(k) if dt_in == "f32" else 1e-2
+    nonfinite = int((~np.isfinite(ref)).sum())
+    ok = same_class_close(got, ref, tol)
+    say(f"skip-zero-A mixed {dt_in} {m}x{k}x{n} form {variant}: {nonfinite} non-finite outputs, close: {ok}")
+    assert nonfinite == 5 and ok
 
 
 def test_fused_softmax_temps_read_by_a_later_root(hip):
@@ -183,6 +216,38 @@ def test_runs_on_two_streams_use_separate_scratch(hip):
         ref = oracle.run(km, {0: x})
         assert max_rel(b[ids[0]].to_numpy(), ref[ids[0]]) <= 1e-6
         assert np.array_equal(b[ids[1]].to_numpy().astype(np.float64), ref[ids[1]])
+    # Each stream's set is released before its stream is destroyed; a run
+    # after a release allocates a new set, with its temps cleared as ever.
     for s in streams:
+        art.release_stream_scratch(s)
+    art.run_device(bufs[1], stream=streams[0], sync=False)
+    assert lib.mlkhip_synchronize() == 0
+    ref = oracle.run(km, {0: xs[1]})
+    assert max_rel(bufs[1][ids[0]].to_numpy(), ref[ids[0]]) <= 1e-6
+    for s in streams:
+        art.release_stream_scratch(s)
         lib.mlkhip_stream_destroy(s)
-    say("two streams, separate scratch: both runs match the oracle")
+    art.release_stream_scratch(streams[0])          # not held: nothing to do
+    say("two streams, separate scratch: both runs match the oracle; sets released")
+
+
+def test_step_kernel_names_name_the_launched_kernels(hip):
+    # Profiles name kernels by these; bench.py reports them per config.
+    cases = [
+        (fx.config2_module(64, 4096, tier=1), ["softmaxWaveRowPair<16, true>"]),
+        (fx.config2_module(64, 1001, tier=1), ["softmaxBlockRow"]),
+        (fx.config4_module(256, 256, 256, "f16", tier=1), ["gemmF16Dma8<true>"]),
+        (fx.config4_module(256, 128, 256, "f32", tier=1), ["gemmF32Dma<true>"]),
+        (fx.config4_module(70, 33, 65, "f64", tier=1), ["gemmGeneral<double>"]),
+        (fx.score_softmax_module(1, 256, 128), ["scoreStatsQ+scoreStoreQ"]),
+    ]
+    for km, want in cases:
+        art = hip.build(km)
+        got = [art.step_kernel_name(i) for i in range(art.num_steps())]
+        say(f"{art.class_name}: {got}")
+        assert got == want, (art.class_name, got)
+    art = hip.build(fx.config4_module(256, 256, 256, "f16", tier=1))
+    art.set_step_variant(0, 7)
+    assert art.step_kernel_name(0) == "gemmF16Dma<true>"
+    art = hip.build(fx.config1_module(n=4096))
+    assert art.step_kernel_name(0).startswith("mlk_elementwise_")

@@ -201,3 +201,38 @@ def test_exact_pass_with_a_dynamic_bound(hip):
     d = ulp_distance_f32(got, ref)
     say(f"dynamic bound with declined arguments: max ULP {d.max()}, tail {d[4990:4996].tolist()}")
     assert d.max() <= 4.0 and d[4990:4996].max() == 0
+
+
+@pytest.mark.parametrize("lift", [False, True])
+def test_in_place_chains_with_declined_elements(hip, lift):
+    # y is x: the store goes back into the buffer the chain reads. A NaN or
+    # an out-of-range argument in a segment must not make that segment's
+    # other elements come out as f(f(x)); each element is the walker's f(x).
+    # The walker reads an element before it stores it (kernel_buffers.cpp:
+    # 342-402), so an in-place run equals the out-of-place one.
+    from test_host import in_place
+    n = 70001
+    rng = np.random.default_rng(16)
+    x = rng.uniform(-4, 4, n)
+    x[1000:1004] = [np.nan, 3000.0, -1e7, np.inf]       # declined sine arguments
+    x = x.astype(np.float32).astype(np.float64)
+    km = fx.config1_module(n=n)
+    if lift:
+        km = fx.lift_1d(km)
+    ref = oracle.run(km, {0: x})[1]
+    got = hip.build(in_place(km)).run({0: x})[0].astype(np.float32)
+    d = ulp_distance_f32(got, ref)
+    say(f"in-place sine lift={lift}: max ULP {d.max()}")
+    assert d.max() <= 4.0
+
+    a = exp_arguments(50000, rng)
+    b = rng.uniform(0.5, 2, a.size).astype(np.float32).astype(np.float64)
+    km = fx.lower_elementwise([("a", [a.size], "f32"), ("b", [a.size], "f32")], EXP_CASES[0][1], [a.size],
+                              out_dtype="f32")
+    if lift:
+        km = fx.lift_1d(km)
+    ref = oracle.run(km, {0: a, 1: b})[2]
+    got = hip.build(in_place(km)).run({0: a, 1: b})[0]
+    err = finite_max_rel(got, ref)
+    say(f"in-place exp*b lift={lift}: max rel {err:.3g}")
+    assert err <= 1e-6

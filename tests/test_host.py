@@ -323,3 +323,42 @@ def test_split_precision_sine_only_for_f32_outputs(lift):
         body = [line for line in src.splitlines() if "mlk_p7_sin" in line and "const double" in line]
         assert body, dtype
         assert ("mlk_p7_sin_f32out(" in body[0]) == split, (dtype, body[0])
+
+
+def in_place(km):
+    """The chain's store pointed back at its first input: y is x."""
+    root = km.nodes[km.roots()[0]]
+    while True:
+        kids = [km.nodes[c] for c in root.children]
+        store = next((n for n in kids if n.op == "store"), None)
+        if store is not None:
+            break
+        root = kids[0]
+    src = 0
+    km.buffers[src].is_output = True
+    store.out = src
+    return km
+
+
+IN_PLACE_CASES = [
+    ("sin", lambda: fx.config1_module(1 << 12)),
+    ("exp*b", lambda: fx.lower_elementwise([("a", [4096], "f32"), ("b", [4096], "f32")],
+                                           EXP_CASES[0][1], [4096], out_dtype="f32")),
+    ("c3", lambda: fx.config3_module(64, 1024, 2)),
+]
+
+
+@pytest.mark.parametrize("name,make", IN_PLACE_CASES, ids=[c[0] for c in IN_PLACE_CASES])
+@pytest.mark.parametrize("lift", [False, True])
+def test_in_place_chains_plan_the_exact_forms(name, make, lift):
+    # A chain that stores into the buffer it reads cannot take the forms
+    # whose declined elements are redone from re-read inputs: by then the
+    # inputs hold results. It plans the exact f64 forms, with no second pass.
+    km = make()
+    if lift and name != "c3":
+        km = fx.lift_1d(km)
+    fast, exact = chain_bodies(km)
+    assert exact != ""                   # out of place: a declining form
+    fast, exact = chain_bodies(in_place(km))
+    assert exact == "", fast
+    assert "f32acc" not in fast and "f32out" not in fast and "slow" not in fast.replace("(void)slow", "")

@@ -3,9 +3,9 @@
 Its scratch (materialized temps, score-softmax row statistics) comes from one
 file-scope device array. Each case runs twice in a row on that array, the
 second time on a smaller input, and must match mlkhip_run_device on the same
-buffers: bit for bit where both run the same kernels, and within the path's
-tolerance for Call(MatMul), which the allocation-free entry always runs on the
-exact skip-zero-A kernel (relative |got-ref|/max(|ref|,1) <= 1e-5*sqrt(K)).
+buffers bit for bit: both run the same kernels. Call(MatMul) keeps its
+skip-zero-A column flags in the array too, so the second, smaller run must not
+see the first run's flags.
 """
 import math
 import sys
@@ -79,16 +79,24 @@ def test_noalloc_score_softmax_statistics(hip, b, s):
     say(f"score-softmax {b}x{s}: bit-identical to run_device")
 
 
-@pytest.mark.parametrize("m,k,n", [(256, 64, 256), (128, 32, 128)])
-def test_noalloc_matmul_call(hip, m, k, n):
+@pytest.mark.parametrize("m,k,n,bad", [(256, 64, 512, True), (128, 32, 128, False)])
+def test_noalloc_matmul_call(hip, m, k, n, bad):
+    # The first run flags column group 6 of B (inf where A is zero, and a
+    # row that reads it); the second, smaller run has B finite and must take
+    # the MFMA form on every tile.
     km = fx.config4_module(m, k, n, "f32", tier=1)
     d = inputs.config_inputs("c4a", {"m": m, "k": k, "n": n})
+    A, B = d["A"].astype(np.float64).reshape(m, k), d["B"].astype(np.float64).reshape(k, n)
+    if bad:
+        B[3, 400:403] = np.inf
+        A[:, 3] = 0.0
+        A[11, 3] = 0.5
     c0 = inputs.uniform(9, m * n, -1, 1)
-    art, ref, got = _both(hip, km, {0: d["A"], 1: d["B"], 2: c0})
+    art, ref, got = _both(hip, km, {0: A, 1: B, 2: c0})
     for i in ref:
-        r = max_rel(got[i].astype(np.float64), ref[i].astype(np.float64))
-        assert r <= 1e-5 * math.sqrt(k), (m, k, n, r)
-    say(f"Call(MatMul) {m}x{k}x{n}: within {1e-5 * math.sqrt(k):g} of run_device")
+        assert np.array_equal(ref[i].view(np.uint32), got[i].view(np.uint32)), (m, k, n, i)
+        assert int(np.isinf(got[i]).sum()) == (3 if bad else 0)
+    say(f"Call(MatMul) {m}x{k}x{n} (non-finite B: {bad}): bit-identical to run_device")
 
 
 def test_noalloc_refusals(hip):
