@@ -286,6 +286,31 @@ def cpu_baseline_config(name: str) -> dict:
     return out
 
 
+def probe_mfma() -> dict:
+    """Settled f16 MFMA rates of register-only loops (no memory traffic in the
+    loop), one workgroup per CU: the ceiling the power limit leaves a GEMM
+    and the calibration of the MFMA-busy counters (rocprofv3 --pmc of this
+    command reads what those counters show at each measured rate)."""
+    import ctypes
+
+    from mlk2_amd.backend import lib
+
+    fn = lib().mlkd_probe_mfma_rate
+    fn.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_double, ctypes.c_int,
+                   ctypes.POINTER(ctypes.c_double), ctypes.c_void_p]
+    fn.restype = ctypes.c_int
+    out = {}
+    for shape, sname in ((0, "16x16x32"), (1, "32x32x16")):
+        for random in (1, 0):
+            for wps in (1, 2):
+                r = ctypes.c_double()
+                rc = fn(shape, random, wps, 100.0, 10, ctypes.byref(r), None)
+                key = f"{sname} {'random' if random else 'ones'} {wps}w/SIMD"
+                out[key] = None if rc != 0 else round(r.value / 1e12, 1)
+                print(f"[probe] {key}: {out[key]} TFLOP/s", file=sys.stderr, flush=True)
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -293,6 +318,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", default="")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--probe-mfma", action="store_true",
+                    help="only time the register-only f16 MFMA probes (TFLOP/s) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -308,6 +335,9 @@ def main() -> int:
     if not be.device_available():
         print("bench.py: no gfx950 device visible", file=sys.stderr)
         return 3
+    if args.probe_mfma:
+        print(json.dumps({"probe": "register-only f16 MFMA, TFLOP/s", "rates": probe_mfma()}), flush=True)
+        return 0
 
     # Headline: C2 softmax, K timed steps bracketed by device synchronization.
     m, k = 8192, 4096

@@ -1108,6 +1108,185 @@ __global__ __launch_bounds__(512, 1) void gemmF16Dma8(const _Float16* __restrict
     }
 }
 
+/// Direct load through a scalar base: lane bytes `voff` past `sbase` into LDS
+/// at M0 + 16 * lane. The K advance lives in `sbase` (scalar adds), so the
+/// per-lane address costs no vector instruction per step.
+__device__ __forceinline__ void dmaLoad16s(const void* sbase, uint32_t voff, uint32_t m0) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(m0) : "memory");
+}
+
+/// Variant 8 for K a multiple of 128: the same tiles, ring, swizzles and MFMA
+/// sequence as gemmF16Dma8 (results identical bit for bit), with no per-step
+/// vector address arithmetic and a fixed instruction order.
+/// * Vector instructions take issue cycles from the MFMAs of the wave sharing
+///   the SIMD (measured on gfx950: 32 v_add_u32 per 32 MFMAs cost 9% of the
+///   MFMA rate, 16 v_readfirstlane 18%). gemmF16Dma8 spends about 40 per K
+///   step on addresses: 64-bit adds, multiplies by ldb and a readfirstlane
+///   per direct load. Here the direct loads take a scalar base plus a fixed
+///   32-bit lane offset and M0 comes from scalar registers; the loop is
+///   unrolled over the 4 ring slots so that every LDS fragment read is a
+///   base register plus an immediate offset (two bases per operand, since
+///   DS offsets hold 16 bits).
+/// * The compiler does not keep the interleave that sched_group_barrier asks
+///   for across the unrolled steps: it hoists the next step's first MFMAs up
+///   to the reads that feed them and then waits for those reads every one or
+///   two MFMAs. Scheduling fences after each MFMA pin the order: the next
+///   m-tiles' A reads in the first MFMAs of group 1, the next step's
+///   fragments in the first MFMAs of group 2 in order of first use, and the
+///   direct loads after its second MFMA.
+/// Needs lda < 2^23 and ldb < 2^25 (32-bit lane offsets).
+template <bool ACC>
+__global__ __launch_bounds__(512, 1) void gemmF16Dma8s(const _Float16* __restrict__ A,
+                                                       const _Float16* __restrict__ B,
+                                                       float* __restrict__ C, int M, int N, int K,
+                                                       int64_t lda, int64_t ldb, int64_t ldc,
+                                                       const uint8_t* __restrict__ bad) {
+    extern __shared__ __align__(16) _Float16 lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int wm = wave >> 2, wn = wave & 3;
+    int tm, tn;
+    xcdTile(M / kBM, N / kBN, tm, tn);
+    const int64_t row0 = static_cast<int64_t>(tm) * kBM;
+    const int64_t col0 = static_cast<int64_t>(tn) * kBN;
+    if (skipTile(bad, col0, kBN)) return;  // columns the fix-up computes
+    const int steps = K / kDmaBK;
+
+    // Wave w's direct loads are A instructions 2w, 2w + 1 (16 rows each) and
+    // B instructions 2w, 2w + 1 (2 k-rows each) of every stage, as in
+    // gemmF16Dma8: lane byte offsets from the tile's A rows / B columns.
+    uint32_t gA[2], gB[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int q = (wave * 2 + j) * 64 + lane;
+        const int row = q >> 2;
+        const int c = (q & 3) ^ ((row >> 2) & 3);
+        gA[j] = static_cast<uint32_t>((row * lda + c * 8) * 2);
+        const int krow = q >> 5;
+        const int cb = (q & 31) ^ ((krow & 3) * 4);
+        gB[j] = static_cast<uint32_t>((krow * ldb + cb * 8) * 2);
+    }
+    const char* aTile = reinterpret_cast<const char*>(A + row0 * lda);
+    const char* bTile = reinterpret_cast<const char*>(B + col0);
+    const uint32_t ldsS = __builtin_amdgcn_readfirstlane(ldsOffset(lds));
+    const uint32_t m0Wave = ldsS + static_cast<uint32_t>(wave) * 2048u;
+    // Stage t (K step min(t, steps - 1)) into ring slot `slot` = t % 4.
+    auto issue = [&](int t, const int slot) {
+        const int64_t k0 = static_cast<int64_t>(min(t, steps - 1)) * kDmaBK;
+        const char* a = aTile + k0 * 2;
+        const char* b = bTile + k0 * ldb * 2;
+        const uint32_t m = m0Wave + static_cast<uint32_t>(slot) * (kDmaStage * 2u);
+        dmaLoad16s(a, gA[0], m);
+        dmaLoad16s(a, gA[1], m + 1024u);
+        dmaLoad16s(b, gB[0], m + kDmaA * 2u);
+        dmaLoad16s(b, gB[1], m + kDmaA * 2u + 1024u);
+    };
+
+    f32x4 acc[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    issue(0, 0);
+    issue(1, 1);
+    issue(2, 2);
+
+    // Fragment bases: slots 0 and 1 from vA0 / vB0, slots 2 and 3 from the
+    // bases 64 KiB up; the slot's remaining 0 or 32 KiB, the m-tile (1 KiB)
+    // and the second transposed half (4 k-rows, 2 KiB) are immediates.
+    const int l16 = lane & 15, g = lane >> 4;
+    uint32_t vA0;
+    {
+        const int row = wm * 128 + l16;
+        vA0 = ldsS + 2u * (row * kDmaBK + ((g ^ ((row >> 2) & 3)) * 8));
+    }
+    uint32_t vB0[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+        const int krow = 8 * g + (l16 >> 2);
+        const int col = wn * 64 + nt * 16 + 4 * (l16 & 3);
+        vB0[nt] = ldsS + 2u * (kDmaA + krow * 256 + (((col >> 3) ^ ((krow & 3) * 4)) * 8) + (col & 7));
+    }
+    const uint32_t vA2 = vA0 + 65536u;
+    uint32_t vB2[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) vB2[nt] = vB0[nt] + 65536u;
+    auto readA = [&](f16x8& f, const int slot, int mt) {
+        const uint32_t addr = (slot < 2 ? vA0 : vA2) + static_cast<uint32_t>((slot & 1) * kDmaStage * 2 + 1024 * mt);
+        f = *reinterpret_cast<const __attribute__((address_space(3))) f16x8*>(addr);
+    };
+    auto readB = [&](f16x8& f, const int slot, int nt) {
+        const uint32_t base = (slot < 2 ? vB0[nt] : vB2[nt]) + static_cast<uint32_t>((slot & 1) * kDmaStage * 2);
+        const fp16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+            reinterpret_cast<__attribute__((address_space(3))) fp16x4*>(base));
+        const fp16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+            reinterpret_cast<__attribute__((address_space(3))) fp16x4*>(base + 2048u));
+        f = __builtin_shufflevector(__builtin_bit_cast(f16x4, v0), __builtin_bit_cast(f16x4, v1), 0, 1, 2, 3, 4, 5,
+                                    6, 7);
+    };
+    f16x8 aLo[4], aHi[4], bX[4], bY[4];
+    // Stage 0 landed (stages 1 and 2, 4 direct loads each per wave, may be in
+    // flight).
+    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    asm volatile("s_barrier" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < 4; ++i) readA(aLo[i], 0, i);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) readB(bX[j], 0, j);
+    auto mfma = [&](const f16x8& a, const f16x8& b, f32x4& c) {
+        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(b, a, c, 0, 0, 0);
+    };
+    // K step s in ring slot q = s % 4.
+    auto step = [&](int s, const int q, f16x8 (&bCur)[4], f16x8 (&bNxt)[4]) {
+        const int qn = (q + 1) & 3;
+        // Group 1: m-tiles 0-3; the A fragments of m-tiles 4-7 are read
+        // behind its first four MFMAs.
+#pragma unroll
+        for (int idx = 0; idx < 16; ++idx) {
+            mfma(aLo[idx >> 2], bCur[idx & 3], acc[idx >> 2][idx & 3]);
+            if (idx < 4) readA(aHi[idx], q, 4 + idx);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // Stage s + 1 landed (one later stage may be in flight); after the
+        // barrier every wave is past step s - 1, so its slot can be refilled.
+        asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+        asm volatile("s_barrier" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        // Group 2: m-tiles 4-7; step s + 1's fragments read in order of first
+        // use, and stage s + 3 issued into slot (s - 1) % 4.
+#pragma unroll
+        for (int idx = 0; idx < 16; ++idx) {
+            mfma(aHi[idx >> 2], bCur[idx & 3], acc[4 + (idx >> 2)][idx & 3]);
+            if (idx == 0) readB(bNxt[0], qn, 0);
+            if (idx == 1) readA(aLo[0], qn, 0);
+            if (idx == 1) issue(s + kDmaStages - 1, (q + 3) & 3);
+            if (idx >= 2 && idx <= 4) readB(bNxt[idx - 1], qn, idx - 1);
+            if (idx >= 5 && idx <= 7) readA(aLo[idx - 4], qn, idx - 4);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    for (int s = 0; s < steps; s += 4) {
+        step(s, 0, bX, bY);
+        step(s + 1, 1, bY, bX);
+        step(s + 2, 2, bX, bY);
+        step(s + 3, 3, bY, bX);
+    }
+    // No direct load may still be writing LDS when the workgroup ends.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int64_t row = row0 + wm * 128 + i * 16 + l16;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            f32x4* dst = reinterpret_cast<f32x4*>(C + row * ldc + col0 + wn * 64 + j * 16 + 4 * g);
+            f32x4 v = acc[i][j];
+            if (ACC) v += *dst;
+            *dst = v;
+        }
+    }
+}
+
 // ---------------------------------------------------------------- f32 ----
 constexpr int kFM = 64, kFN = 64, kFK = 32;
 constexpr int kFDepth = 2;   // K steps of global loads in flight ahead of the MFMAs
@@ -1487,6 +1666,8 @@ int raiseLdsLimits() {
             {reinterpret_cast<const void*>(gemmF16Dma<false>), kLdsDma},
             {reinterpret_cast<const void*>(gemmF16Dma8<true>), kLdsDma},
             {reinterpret_cast<const void*>(gemmF16Dma8<false>), kLdsDma},
+            {reinterpret_cast<const void*>(gemmF16Dma8s<true>), kLdsDma},
+            {reinterpret_cast<const void*>(gemmF16Dma8s<false>), kLdsDma},
             {reinterpret_cast<const void*>(gemmF32Dma<true>), kLdsF32Dma},
             {reinterpret_cast<const void*>(gemmF32Dma<false>), kLdsF32Dma},
         };
@@ -1522,6 +1703,12 @@ int mfmaForm(const mlkd_gemm* p) {
     return -1;
 }
 
+/// Form 8 takes gemmF16Dma8s (K a multiple of 128, lane offsets within 32
+/// bits) and gemmF16Dma8 otherwise; the two give identical results.
+bool scalarAddressed8(const mlkd_gemm* p) {
+    return p->k % (4 * kDmaBK) == 0 && p->lda < (int64_t{1} << 23) && p->ldb < (int64_t{1} << 25);
+}
+
 /// Output columns per workgroup tile of an MFMA form.
 int formTileCols(int form) { return form >= 100 ? kFN : (form == 5 || form == 6 ? kBN2 : kBN); }
 
@@ -1537,8 +1724,13 @@ int launchMfma(const mlkd_gemm* p, int form, const uint8_t* bad, hipStream_t st)
     const size_t ldsDirect = (2 * kTileA + 2 * kTileHalves) * sizeof(_Float16);
     switch (form) {
         case 8:
-            hipLaunchKernelGGL((acc ? gemmF16Dma8<true> : gemmF16Dma8<false>), dim3(tiles), dim3(512), kLdsDma, st,
-                               a16, b16, c, m, n, k, p->lda, p->ldb, p->ldc, bad);
+            if (scalarAddressed8(p)) {
+                hipLaunchKernelGGL((acc ? gemmF16Dma8s<true> : gemmF16Dma8s<false>), dim3(tiles), dim3(512), kLdsDma,
+                                   st, a16, b16, c, m, n, k, p->lda, p->ldb, p->ldc, bad);
+            } else {
+                hipLaunchKernelGGL((acc ? gemmF16Dma8<true> : gemmF16Dma8<false>), dim3(tiles), dim3(512), kLdsDma,
+                                   st, a16, b16, c, m, n, k, p->lda, p->ldb, p->ldc, bad);
+            }
             break;
         case 7:
             hipLaunchKernelGGL((acc ? gemmF16Dma<true> : gemmF16Dma<false>), dim3(tiles), dim3(256), kLdsDma, st,
@@ -1606,7 +1798,9 @@ extern "C" int64_t mlkd_gemm_scratch_bytes(const mlkd_gemm* p) {
 extern "C" const char* mlkd_gemm_kernel_name(const mlkd_gemm* p) {
     const bool acc = p->accumulate != 0;
     switch (mfmaForm(p)) {
-        case 8: return acc ? "gemmF16Dma8<true>" : "gemmF16Dma8<false>";
+        case 8:
+            if (scalarAddressed8(p)) return acc ? "gemmF16Dma8s<true>" : "gemmF16Dma8s<false>";
+            return acc ? "gemmF16Dma8<true>" : "gemmF16Dma8<false>";
         case 7: return acc ? "gemmF16Dma<true>" : "gemmF16Dma<false>";
         case 6: return acc ? "gemmF16Mfma2cu<true, false>" : "gemmF16Mfma2cu<false, false>";
         case 5: return acc ? "gemmF16Mfma2cu<true, true>" : "gemmF16Mfma2cu<false, true>";

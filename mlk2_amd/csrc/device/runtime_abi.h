@@ -112,6 +112,11 @@ void mlkd_score_set_variant(int variant);
 /// throughput (register-only MFMAs, one wave per SIMD) of the current
 /// device, timed on `stream` (probe.hip).
 int mlkd_probe_environment(double* bytes_per_sec, double* f16_flops_per_sec, void* stream);
+/// Settled f16 MFMA rate of a register-only loop (probe.hip): shape 0 =
+/// 16x16x32, 1 = 32x32x16; random (1) or all-ones (0) operands; 1 or 2 waves
+/// per SIMD. Measurement only: calibrates the MFMA-busy counters.
+int mlkd_probe_mfma_rate(int shape, int random, int waves_per_simd, double settle_ms, int reps,
+                         double* flops_per_sec, void* stream);
 
 #ifdef __cplusplus
 }
