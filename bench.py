@@ -127,8 +127,8 @@ def bench_config(be, name: str, steps: int, warmup: int) -> dict:
     elif name == "c4b_call":
         # The Tier-1 Call(MatMul) form the reference's bench builds and times
         # first (tools/mlk-poly/poly_bench.cpp:123-160, :314-366): C += A*B
-        # with the executor's skip of A[i,p] == 0, here the device-side
-        # column flags of B, the MFMA form and the (empty) exact fix-up.
+        # with the executor's skip of A[i,p] == 0: one MFMA launch whose
+        # waves check their accumulators for non-finite values (none here).
         m = k = n = 4096
         km = fx.config4_module(m, k, n, "f16", tier=1)
         d = inputs.config_inputs("c4b")

@@ -114,7 +114,7 @@ void mlkhip_release(mlkhip_artifact* a);
 
 /* No counterpart in the reference (its artifact allocates per call): frees
  * the scratch set mlkhip_run_device keeps for `stream` (temps, row
- * statistics, column flags), after waiting for that stream. A caller that
+ * statistics), after waiting for that stream. A caller that
  * runs an artifact on many short-lived streams releases each one's set
  * before destroying the stream; the next run on a released stream
  * allocates a new set. Must not overlap a run of `a` on `stream` from
@@ -152,14 +152,14 @@ int mlkhip_kernel_1d(const mlkhip_artifact* a, double* const* ptrs, int n_ptrs, 
                      const double* scalars, int64_t n_scalars);
 
 /* Device-resident typed entry (the timing path): no copies, no allocation
- * except artifact-owned scratch (temps, the score-softmax row statistics, the
- * Call(MatMul) column flags), one set per stream; enqueued on `stream` (a
- * hipStream_t, NULL = default stream), asynchronous: no step reads anything
- * back to the host except a loop nest with run-time bounds checks, which
- * waits for its status word. A Call(MatMul) step decides its skip-zero-A
- * handling on the device (kernel_buffers.cpp:422): B's column groups with a
- * non-finite value are flagged, the MFMA form computes the other tiles and
- * the exact kernel the flagged ones. */
+ * except artifact-owned scratch (temps, the score-softmax row statistics),
+ * one set per stream; enqueued on `stream` (a hipStream_t, NULL = default
+ * stream), asynchronous: no step reads anything back to the host except a
+ * loop nest with run-time bounds checks, which waits for its status word. A
+ * Call(MatMul) step decides its skip-zero-A handling on the device
+ * (kernel_buffers.cpp:422) in one launch: the skip can change C only where B
+ * holds an infinity or a NaN, which makes the MFMA accumulators there
+ * non-finite, so a wave that finds one recomputes its block exactly. */
 int mlkhip_run_device(const mlkhip_artifact* a, const mlkhip_binding* binds, int n_binds,
                       const double* scalars, int64_t n_scalars, int64_t elements, void* stream);
 
@@ -173,9 +173,9 @@ int mlkhip_run_device(const mlkhip_artifact* a, const mlkhip_binding* binds, int
  * that each GPU holds until the process ends. A run that needs more is
  * refused (MLKHIP_REFUSED, see mlkhip_last_error) before anything is
  * launched, as is a step that needs a host read-back (a loop nest with
- * run-time bounds checks). A Call(MatMul) step keeps its skip-zero-A column
- * flags in the array and runs the same kernels as mlkhip_run_device. Calls
- * no hipMalloc or hipFree. Every call on one GPU shares that GPU's array,
+ * run-time bounds checks). A Call(MatMul) step runs the same single kernel
+ * as mlkhip_run_device and needs none of the array. The entry calls no
+ * hipMalloc or hipFree. Every call on one GPU shares that GPU's array,
  * which keeps the last call's contents: calls that overlap on one GPU (on
  * different streams, or from different threads) race. Enqueued on `stream`,
  * asynchronous. */

@@ -49,15 +49,70 @@ constexpr int kBM = 256, kBN = 256, kBK = 64;
 constexpr int kPadK = kBK + 8;           // halves per LDS row (16-byte pad)
 constexpr int kTileHalves = 256 * kPadK;  // one LDS tile (A or B)
 
-/// Skip-zero-A Call form: bad[g] is 1 when column group [64g, 64g + 64) of
-/// B holds an infinity or a NaN. A workgroup whose columns [col0, col0 +
-/// width) meet such a group leaves its tile untouched (C keeps its value
-/// going in), and the exact fix-up kernel computes it. nullptr: no check.
-__device__ __forceinline__ bool skipTile(const uint8_t* bad, int64_t col0, int width) {
-    if (bad == nullptr) return false;
-    uint32_t any = 0;
-    for (int g = 0; g < width / 64; ++g) any |= bad[col0 / 64 + g];
-    return any != 0;
+/// Skip-zero-A Call form (kernel_buffers.cpp:406-432 skips A[i,p] == 0):
+/// the skip changes a result beyond the sign of a zero sum only where B
+/// holds an infinity or a NaN, since 0 * inf and 0 * NaN are NaN, and then
+/// every accumulator of that column is non-finite (inf * a or 0 * inf; finite
+/// f16 products cannot overflow f32). So after the MFMA loop a wave checks
+/// its own accumulators for an infinity or a NaN. A wave that finds one
+/// recomputes its block exactly (exactWaveBlock); the
+/// others store the MFMA result. f32 operands can also overflow to inf from
+/// finite values; those blocks take the exact path too, which computes the
+/// same overflow.
+template <typename V, int I, int J>
+__device__ __forceinline__ bool waveNonFinite(const V (&acc)[I][J]) {
+    constexpr int E = sizeof(V) / sizeof(float);
+    // A class test per value into a lane mask: no vector registers beyond
+    // the accumulators, which the 4-wave forms hold in all 512.
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < I; ++i) {
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) bad |= !__builtin_isfinite(acc[i][j][e]);
+        }
+    }
+    return __builtin_amdgcn_ballot_w64(bad) != 0;
+}
+
+template <typename V>
+__device__ __forceinline__ bool waveNonFinite(const V& acc) {
+    const V one[1][1] = {{acc}};
+    return waveNonFinite(one);
+}
+
+/// The exact Call(MatMul) form over one wave's rows x cols block: C_in (when
+/// accumulating) plus A[i,p] * B[p,j] over p ascending, skipping A[i,p] ==
+/// 0, in f32 with separate multiply and add, as the general kernel computes
+/// it. Lane l takes column c0 + cb + l; rows go 4 at a time. Only a block
+/// whose MFMA accumulators met a non-finite value runs it.
+template <typename TA, typename TB>
+__device__ __forceinline__ void exactWaveBlock(const TA* __restrict__ A, const TB* __restrict__ B,
+                                               float* __restrict__ C, int64_t lda, int64_t ldb, int64_t ldc,
+                                               int K, int64_t r0, int64_t c0, int rows, int cols, bool acc) {
+    const int lane = threadIdx.x & 63;
+    for (int cb = 0; cb < cols; cb += 64) {
+        const bool on = cb + lane < cols;
+        const int64_t c = c0 + cb + lane;
+        for (int rb = 0; rb < rows; rb += 4) {
+            float s[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) s[r] = (acc && on) ? C[(r0 + rb + r) * ldc + c] : 0.0f;
+            for (int k = 0; k < K; ++k) {
+                const float b = on ? static_cast<float>(B[k * ldb + c]) : 0.0f;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float a = static_cast<float>(A[(r0 + rb + r) * lda + k]);
+                    if (a != 0.0f) s[r] = s[r] + a * b;
+                }
+            }
+            if (on) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) C[(r0 + rb + r) * ldc + c] = s[r];
+            }
+        }
+    }
 }
 
 __device__ __forceinline__ void xcdTile(int tilesM, int tilesN, int& tm, int& tn) {
@@ -87,7 +142,7 @@ __global__ __launch_bounds__(512) void gemmF16Mfma(const _Float16* __restrict__ 
                                                    const _Float16* __restrict__ B,
                                                    float* __restrict__ C, int M, int N, int K,
                                                    int64_t lda, int64_t ldb, int64_t ldc,
-                                                   int /*accumulate: template ACC*/, const uint8_t* __restrict__ bad) {
+                                                   int /*accumulate: template ACC*/, int skipZeroA) {
     extern __shared__ __align__(16) _Float16 lds[];
     _Float16* As = lds;                      // [2][256][kPadK]
     _Float16* Bs = lds + 2 * kTileHalves;    // [2][256][kPadK]
@@ -101,7 +156,6 @@ __global__ __launch_bounds__(512) void gemmF16Mfma(const _Float16* __restrict__ 
     xcdTile(M / kBM, N / kBN, tm, tn);
     const int64_t row0 = static_cast<int64_t>(tm) * kBM;
     const int64_t col0 = static_cast<int64_t>(tn) * kBN;
-    if (skipTile(bad, col0, kBN)) return;  // columns the fix-up computes
 
     // Loader roles: threads 0..255 load A (8 x 16 B each), 256..511 load a
     // 8 (k) x 8 (n) block of B each.
@@ -200,6 +254,10 @@ __global__ __launch_bounds__(512) void gemmF16Mfma(const _Float16* __restrict__ 
         __syncthreads();
     }
 
+    if (ACC && skipZeroA && waveNonFinite(acc)) {
+        exactWaveBlock<_Float16, _Float16>(A, B, C, lda, ldb, ldc, K, row0 + wm * 128, col0 + wn * 64, 128, 64, ACC);
+        return;
+    }
     // D layout of a 32x32 MFMA tile: lane l, register r holds
     // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
 #pragma unroll
@@ -245,7 +303,7 @@ template <bool ACC, bool AHEAD2>
 __global__ __launch_bounds__(256, 2) void gemmF16Mfma2cu(const _Float16* __restrict__ A,
                                                          const _Float16* __restrict__ B,
                                                          float* __restrict__ C, int M, int N, int K,
-                                                         int64_t lda, int64_t ldb, int64_t ldc, const uint8_t* __restrict__ bad) {
+                                                         int64_t lda, int64_t ldb, int64_t ldc, int skipZeroA) {
     extern __shared__ __align__(16) _Float16 lds[];
     _Float16* As = lds;                     // [2][128][40]
     _Float16* Bs = lds + 2 * kTileA2;       // [2][256][40]
@@ -256,7 +314,6 @@ __global__ __launch_bounds__(256, 2) void gemmF16Mfma2cu(const _Float16* __restr
     xcdTile2(M / kBM2, N / kBN2, tm, tn);
     const int64_t row0 = static_cast<int64_t>(tm) * kBM2;
     const int64_t col0 = static_cast<int64_t>(tn) * kBN2;
-    if (skipTile(bad, col0, kBN2)) return;  // columns the fix-up computes
     const int bk = t & 7;    // B block: k rows bk*4 .. +3
     const int bn = t >> 3;   // B block: n cols bn*8 .. +7
     u32x4 ra0[2], rb0[4], ra1[2], rb1[4];
@@ -348,6 +405,10 @@ __global__ __launch_bounds__(256, 2) void gemmF16Mfma2cu(const _Float16* __restr
             __syncthreads();
         }
     }
+    if (ACC && skipZeroA && waveNonFinite(acc)) {
+        exactWaveBlock<_Float16, _Float16>(A, B, C, lda, ldb, ldc, K, row0 + wm * 64, col0 + wn * 128, 64, 128, ACC);
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
 #pragma unroll
@@ -373,7 +434,7 @@ __global__ __launch_bounds__(256) void gemmF16Mfma4w(const _Float16* __restrict_
                                                      const _Float16* __restrict__ B,
                                                      float* __restrict__ C, int M, int N, int K,
                                                      int64_t lda, int64_t ldb, int64_t ldc,
-                                                     int /*accumulate: template ACC*/, const uint8_t* __restrict__ bad) {
+                                                     int /*accumulate: template ACC*/, int skipZeroA) {
     extern __shared__ __align__(16) _Float16 lds[];
     _Float16* As = lds;
     _Float16* Bs = lds + 2 * kTileHalves;
@@ -386,7 +447,6 @@ __global__ __launch_bounds__(256) void gemmF16Mfma4w(const _Float16* __restrict_
     xcdTile(M / kBM, N / kBN, tm, tn);
     const int64_t row0 = static_cast<int64_t>(tm) * kBM;
     const int64_t col0 = static_cast<int64_t>(tn) * kBN;
-    if (skipTile(bad, col0, kBN)) return;  // columns the fix-up computes
     const int bk = t & 7;
     const int bn = t >> 3;
     u32x4 ra[8], rb[8];
@@ -457,6 +517,10 @@ __global__ __launch_bounds__(256) void gemmF16Mfma4w(const _Float16* __restrict_
         if (s + 1 < steps) ldsStore(buf ^ 1);
         __syncthreads();
     }
+    if (ACC && skipZeroA && waveNonFinite(acc)) {
+        exactWaveBlock<_Float16, _Float16>(A, B, C, lda, ldb, ldc, K, row0 + wm * 128, col0 + wn * 128, 128, 128, ACC);
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -490,7 +554,7 @@ __global__ __launch_bounds__(256) void gemmF16Mfma4wDirect(const _Float16* __res
                                                            const _Float16* __restrict__ B,
                                                            float* __restrict__ C, int M, int N, int K,
                                                            int64_t lda, int64_t ldb, int64_t ldc,
-                                                           int /*accumulate: template ACC*/, const uint8_t* __restrict__ bad) {
+                                                           int /*accumulate: template ACC*/, int skipZeroA) {
     extern __shared__ __align__(16) _Float16 lds[];
     _Float16* As = lds;                    // [2][256][64] swizzled
     _Float16* Bs = lds + 2 * kTileA;       // [2][256][kPadK]
@@ -503,7 +567,6 @@ __global__ __launch_bounds__(256) void gemmF16Mfma4wDirect(const _Float16* __res
     xcdTile(M / kBM, N / kBN, tm, tn);
     const int64_t row0 = static_cast<int64_t>(tm) * kBM;
     const int64_t col0 = static_cast<int64_t>(tn) * kBN;
-    if (skipTile(bad, col0, kBN)) return;  // columns the fix-up computes
     const int bk = t & 7;
     const int bn = t >> 3;
     u32x4 rb[8];
@@ -587,6 +650,10 @@ __global__ __launch_bounds__(256) void gemmF16Mfma4wDirect(const _Float16* __res
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
     }
+    if (ACC && skipZeroA && waveNonFinite(acc)) {
+        exactWaveBlock<_Float16, _Float16>(A, B, C, lda, ldb, ldc, K, row0 + wm * 128, col0 + wn * 128, 128, 128, ACC);
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -614,7 +681,7 @@ template <bool ACC>
 __global__ __launch_bounds__(256) void gemmF16Mfma4wPipe(const _Float16* __restrict__ A,
                                                          const _Float16* __restrict__ B,
                                                          float* __restrict__ C, int M, int N, int K,
-                                                         int64_t lda, int64_t ldb, int64_t ldc, const uint8_t* __restrict__ bad) {
+                                                         int64_t lda, int64_t ldb, int64_t ldc, int skipZeroA) {
     extern __shared__ __align__(16) _Float16 lds[];
     _Float16* As = lds;
     _Float16* Bs = lds + 2 * kTileA;
@@ -627,7 +694,6 @@ __global__ __launch_bounds__(256) void gemmF16Mfma4wPipe(const _Float16* __restr
     xcdTile(M / kBM, N / kBN, tm, tn);
     const int64_t row0 = static_cast<int64_t>(tm) * kBM;
     const int64_t col0 = static_cast<int64_t>(tn) * kBN;
-    if (skipTile(bad, col0, kBN)) return;  // columns the fix-up computes
     const int bk = t & 7;
     const int bn = t >> 3;
     const int lrow = lane & 31;
@@ -744,6 +810,10 @@ __global__ __launch_bounds__(256) void gemmF16Mfma4wPipe(const _Float16* __restr
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
     }
+    if (ACC && skipZeroA && waveNonFinite(acc)) {
+        exactWaveBlock<_Float16, _Float16>(A, B, C, lda, ldb, ldc, K, row0 + wm * 128, col0 + wn * 128, 128, 128, ACC);
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -804,7 +874,7 @@ template <bool ACC>
 __global__ __launch_bounds__(256, 1) void gemmF16Dma(const _Float16* __restrict__ A,
                                                      const _Float16* __restrict__ B,
                                                      float* __restrict__ C, int M, int N, int K,
-                                                     int64_t lda, int64_t ldb, int64_t ldc, const uint8_t* __restrict__ bad) {
+                                                     int64_t lda, int64_t ldb, int64_t ldc, int skipZeroA) {
     extern __shared__ __align__(16) _Float16 lds[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave >> 1, wn = wave & 1;
@@ -812,7 +882,6 @@ __global__ __launch_bounds__(256, 1) void gemmF16Dma(const _Float16* __restrict_
     xcdTile(M / kBM, N / kBN, tm, tn);
     const int64_t row0 = static_cast<int64_t>(tm) * kBM;
     const int64_t col0 = static_cast<int64_t>(tn) * kBN;
-    if (skipTile(bad, col0, kBN)) return;  // columns the fix-up computes
     const int steps = K / kDmaBK;
 
     // Stage `slot` receives K step min(slot, steps - 1) in ring slot
@@ -927,6 +996,10 @@ __global__ __launch_bounds__(256, 1) void gemmF16Dma(const _Float16* __restrict_
     }
     // No direct load may still be writing LDS when the workgroup ends.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (ACC && skipZeroA && waveNonFinite(acc)) {
+        exactWaveBlock<_Float16, _Float16>(A, B, C, lda, ldb, ldc, K, row0 + wm * 128, col0 + wn * 128, 128, 128, ACC);
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -962,7 +1035,7 @@ template <bool ACC>
 __global__ __launch_bounds__(512, 1) void gemmF16Dma8(const _Float16* __restrict__ A,
                                                       const _Float16* __restrict__ B,
                                                       float* __restrict__ C, int M, int N, int K,
-                                                      int64_t lda, int64_t ldb, int64_t ldc, const uint8_t* __restrict__ bad) {
+                                                      int64_t lda, int64_t ldb, int64_t ldc, int skipZeroA) {
     extern __shared__ __align__(16) _Float16 lds[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave >> 2, wn = wave & 3;
@@ -970,7 +1043,6 @@ __global__ __launch_bounds__(512, 1) void gemmF16Dma8(const _Float16* __restrict
     xcdTile(M / kBM, N / kBN, tm, tn);
     const int64_t row0 = static_cast<int64_t>(tm) * kBM;
     const int64_t col0 = static_cast<int64_t>(tn) * kBN;
-    if (skipTile(bad, col0, kBN)) return;  // columns the fix-up computes
     const int steps = K / kDmaBK;
 
     // Stage `slot` receives K step min(slot, steps - 1) in ring slot
@@ -1095,6 +1167,10 @@ __global__ __launch_bounds__(512, 1) void gemmF16Dma8(const _Float16* __restrict
     }
     // No direct load may still be writing LDS when the workgroup ends.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (ACC && skipZeroA && waveNonFinite(acc)) {
+        exactWaveBlock<_Float16, _Float16>(A, B, C, lda, ldb, ldc, K, row0 + wm * 128, col0 + wn * 64, 128, 64, ACC);
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const int64_t row = row0 + wm * 128 + i * 16 + l16;
@@ -1140,7 +1216,7 @@ __global__ __launch_bounds__(512, 1) void gemmF16Dma8s(const _Float16* __restric
                                                        const _Float16* __restrict__ B,
                                                        float* __restrict__ C, int M, int N, int K,
                                                        int64_t lda, int64_t ldb, int64_t ldc,
-                                                       const uint8_t* __restrict__ bad) {
+                                                       int skipZeroA) {
     extern __shared__ __align__(16) _Float16 lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
@@ -1149,7 +1225,6 @@ __global__ __launch_bounds__(512, 1) void gemmF16Dma8s(const _Float16* __restric
     xcdTile(M / kBM, N / kBN, tm, tn);
     const int64_t row0 = static_cast<int64_t>(tm) * kBM;
     const int64_t col0 = static_cast<int64_t>(tn) * kBN;
-    if (skipTile(bad, col0, kBN)) return;  // columns the fix-up computes
     const int steps = K / kDmaBK;
 
     // Wave w's direct loads are A instructions 2w, 2w + 1 (16 rows each) and
@@ -1274,6 +1349,10 @@ __global__ __launch_bounds__(512, 1) void gemmF16Dma8s(const _Float16* __restric
     }
     // No direct load may still be writing LDS when the workgroup ends.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (ACC && skipZeroA && waveNonFinite(acc)) {
+        exactWaveBlock<_Float16, _Float16>(A, B, C, lda, ldb, ldc, K, row0 + wm * 128, col0 + wn * 64, 128, 64, ACC);
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const int64_t row = row0 + wm * 128 + i * 16 + l16;
@@ -1305,7 +1384,7 @@ __global__ __launch_bounds__(256) void gemmF32Mfma(const float* __restrict__ A,
                                                    const float* __restrict__ B,
                                                    float* __restrict__ C, int /*M: the grid covers it*/, int N,
                                                    int K, int64_t lda, int64_t ldb, int64_t ldc,
-                                                   int /*accumulate: template ACC*/, const uint8_t* __restrict__ bad) {
+                                                   int /*accumulate: template ACC*/, int skipZeroA) {
     __shared__ float At[2][kFK][kFM + 4];   // transposed: [k][m]
     __shared__ float Bs[2][kFK][kFN + 4];   // as loaded: [k][n]
     const int tid = threadIdx.x;
@@ -1315,7 +1394,6 @@ __global__ __launch_bounds__(256) void gemmF32Mfma(const float* __restrict__ A,
     const int tilesN = N / kFN;
     const int64_t row0 = static_cast<int64_t>(blockIdx.x / tilesN) * kFM;
     const int64_t col0 = static_cast<int64_t>(blockIdx.x % tilesN) * kFN;
-    if (skipTile(bad, col0, kFN)) return;  // columns the fix-up computes
 
     // A tile 64x32 floats = 512 float4 and B tile 32x64 = 512 float4: 2 of
     // each per thread. Item c of A: wave-slice q = c / 64 covers rows
@@ -1380,6 +1458,10 @@ __global__ __launch_bounds__(256) void gemmF32Mfma(const float* __restrict__ A,
             }
         }
     }
+    if (ACC && skipZeroA && waveNonFinite(acc)) {
+        exactWaveBlock<float, float>(A, B, C, lda, ldb, ldc, K, row0 + wm * 32, col0 + wn * 32, 32, 32, ACC);
+        return;
+    }
     const int64_t cBase = col0 + wn * 32 + (lane & 31);
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -1410,14 +1492,13 @@ constexpr size_t kLdsF32Dma = static_cast<size_t>(kQStages) * kQStage * sizeof(f
 template <bool ACC>
 __global__ __launch_bounds__(256, 1) void gemmF32Dma(const float* __restrict__ A, const float* __restrict__ B,
                                                      float* __restrict__ C, int N, int K, int64_t lda,
-                                                     int64_t ldb, int64_t ldc, const uint8_t* __restrict__ bad) {
+                                                     int64_t ldb, int64_t ldc, int skipZeroA) {
     extern __shared__ __align__(16) float ldsF[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int tilesN = N / kFN;
     const int64_t row0 = static_cast<int64_t>(blockIdx.x / tilesN) * kFM;
     const int64_t col0 = static_cast<int64_t>(blockIdx.x % tilesN) * kFN;
-    if (skipTile(bad, col0, kFN)) return;  // columns the fix-up computes
     const int steps = K / kQK;
     // Stage `slot` receives K step min(slot, steps - 1) in ring slot
     // slot % kQStages. A is 64 rows of 256 bytes and B 64 k-rows of 256
@@ -1484,6 +1565,10 @@ __global__ __launch_bounds__(256, 1) void gemmF32Dma(const float* __restrict__ A
     }
     // No direct load may still be writing LDS when the workgroup ends.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (ACC && skipZeroA && waveNonFinite(acc)) {
+        exactWaveBlock<float, float>(A, B, C, lda, ldb, ldc, K, row0 + wm * 32, col0 + wn * 32, 32, 32, ACC);
+        return;
+    }
     const int64_t cBase = col0 + wn * 32 + l32;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -1577,60 +1662,6 @@ __global__ __launch_bounds__(256) void gemmGeneral(mlkd_gemm p) {
 }
 
 /// Zeroes n 32-bit words.
-__global__ __launch_bounds__(256) void clearWords(uint32_t* __restrict__ p, int64_t n) {
-    const int64_t i = blockIdx.x * 256ll + threadIdx.x;
-    if (i < n) p[i] = 0u;
-}
-
-/// Column-group flags of B for the skip-zero-A Call form: bad[(c / 64)] = 1
-/// for every column c with an infinity or a NaN in any row. A product
-/// 0 * inf or 0 * NaN is the only one whose skip changes C beyond the sign
-/// of a zero sum, so only those columns need the exact kernel. Each thread
-/// checks 16-byte chunks of B's rows (a chunk lies inside one group: N and
-/// ldb are multiples of the chunk, B is 16-byte aligned); the flags start
-/// at zero and every writer stores 1.
-template <int DT>
-__global__ __launch_bounds__(256) void scanBadColumns(const void* __restrict__ B, int64_t K, int64_t N, int64_t ldb,
-                                                      uint8_t* __restrict__ bad) {
-    constexpr int per = DT == MLKD_F16 ? 8 : 4;  // elements per 16-byte chunk
-    const int64_t chunksRow = N / per;
-    const int64_t total = K * chunksRow;
-    for (int64_t c = blockIdx.x * 256ll + threadIdx.x; c < total; c += static_cast<int64_t>(gridDim.x) * 256) {
-        const int64_t k = c / chunksRow, col = (c - k * chunksRow) * per;
-        const u32x4 w = *reinterpret_cast<const u32x4*>(static_cast<const char*>(B) +
-                                                        (k * ldb + col) * (DT == MLKD_F16 ? 2 : 4));
-        bool nonFinite = false;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            if constexpr (DT == MLKD_F16) {
-                nonFinite = nonFinite || (w[i] & 0x7C00u) == 0x7C00u || (w[i] & 0x7C000000u) == 0x7C000000u;
-            } else {
-                nonFinite = nonFinite || (w[i] & 0x7F800000u) == 0x7F800000u;
-            }
-        }
-        if (nonFinite) bad[col / 64] = 1;
-    }
-}
-
-/// The exact fix-up of the skip-zero-A Call form: every 64x64 tile whose
-/// column group lies in a `blockCols`-wide block of the MFMA form's tiles
-/// that met a flagged group (those the MFMA form left untouched) is computed
-/// by generalTile with the skip; the other workgroups return at once.
-/// grid.x: column groups; grid.y: row-tile strides.
-template <typename T>
-__global__ __launch_bounds__(256) void gemmFixBadColumns(mlkd_gemm p, const uint8_t* __restrict__ bad, int blockCols) {
-    __shared__ T As[16][65];
-    __shared__ T Bs[16][65];
-    const int64_t g = blockIdx.x;
-    const int per = blockCols / 64;
-    const int64_t first = g - g % per;
-    uint32_t any = 0;
-    for (int i = 0; i < per; ++i) any |= bad[first + i];
-    if (any == 0) return;
-    const int64_t rowTiles = (p.m + 63) / 64;
-    for (int64_t r = blockIdx.y; r < rowTiles; r += gridDim.y) generalTile<T>(p, r * 64, g * 64, As, Bs);
-}
-
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Process default of the f16 GEMM launch form (a launch's own `variant`
@@ -1709,10 +1740,8 @@ bool scalarAddressed8(const mlkd_gemm* p) {
     return p->k % (4 * kDmaBK) == 0 && p->lda < (int64_t{1} << 23) && p->ldb < (int64_t{1} << 25);
 }
 
-/// Output columns per workgroup tile of an MFMA form.
-int formTileCols(int form) { return form >= 100 ? kFN : (form == 5 || form == 6 ? kBN2 : kBN); }
-
-int launchMfma(const mlkd_gemm* p, int form, const uint8_t* bad, hipStream_t st) {
+int launchMfma(const mlkd_gemm* p, int form, hipStream_t st) {
+    const int skip = p->skip_zero_a != 0 ? 1 : 0;
     if (raiseLdsLimits() != 0) return MLKD_RT_LAUNCH;
     const _Float16* a16 = static_cast<const _Float16*>(p->a);
     const _Float16* b16 = static_cast<const _Float16*>(p->b);
@@ -1726,15 +1755,15 @@ int launchMfma(const mlkd_gemm* p, int form, const uint8_t* bad, hipStream_t st)
         case 8:
             if (scalarAddressed8(p)) {
                 hipLaunchKernelGGL((acc ? gemmF16Dma8s<true> : gemmF16Dma8s<false>), dim3(tiles), dim3(512), kLdsDma,
-                                   st, a16, b16, c, m, n, k, p->lda, p->ldb, p->ldc, bad);
+                                   st, a16, b16, c, m, n, k, p->lda, p->ldb, p->ldc, skip);
             } else {
                 hipLaunchKernelGGL((acc ? gemmF16Dma8<true> : gemmF16Dma8<false>), dim3(tiles), dim3(512), kLdsDma,
-                                   st, a16, b16, c, m, n, k, p->lda, p->ldb, p->ldc, bad);
+                                   st, a16, b16, c, m, n, k, p->lda, p->ldb, p->ldc, skip);
             }
             break;
         case 7:
             hipLaunchKernelGGL((acc ? gemmF16Dma<true> : gemmF16Dma<false>), dim3(tiles), dim3(256), kLdsDma, st,
-                               a16, b16, c, m, n, k, p->lda, p->ldb, p->ldc, bad);
+                               a16, b16, c, m, n, k, p->lda, p->ldb, p->ldc, skip);
             break;
         case 5:
         case 6: {
@@ -1742,25 +1771,25 @@ int launchMfma(const mlkd_gemm* p, int form, const uint8_t* bad, hipStream_t st)
             auto kern = form == 5 ? (acc ? gemmF16Mfma2cu<true, true> : gemmF16Mfma2cu<false, true>)
                                   : (acc ? gemmF16Mfma2cu<true, false> : gemmF16Mfma2cu<false, false>);
             hipLaunchKernelGGL(kern, dim3(tiles2), dim3(256), kLdsGemm2, st, a16, b16, c, m, n, k, p->lda, p->ldb,
-                               p->ldc, bad);
+                               p->ldc, skip);
             break;
         }
         case 3:
             hipLaunchKernelGGL((acc ? gemmF16Mfma4wPipe<true> : gemmF16Mfma4wPipe<false>), dim3(tiles), dim3(256),
-                               ldsDirect, st, a16, b16, c, m, n, k, p->lda, p->ldb, p->ldc, bad);
+                               ldsDirect, st, a16, b16, c, m, n, k, p->lda, p->ldb, p->ldc, skip);
             break;
         case 2:
             hipLaunchKernelGGL((acc ? gemmF16Mfma4wDirect<true> : gemmF16Mfma4wDirect<false>), dim3(tiles),
                                dim3(256), ldsDirect, st, a16, b16, c, m, n, k, p->lda, p->ldb, p->ldc, p->accumulate,
-                               bad);
+                               skip);
             break;
         case 1:
             hipLaunchKernelGGL((acc ? gemmF16Mfma4w<true> : gemmF16Mfma4w<false>), dim3(tiles), dim3(256), ldsBytes,
-                               st, a16, b16, c, m, n, k, p->lda, p->ldb, p->ldc, p->accumulate, bad);
+                               st, a16, b16, c, m, n, k, p->lda, p->ldb, p->ldc, p->accumulate, skip);
             break;
         case 0:
             hipLaunchKernelGGL((acc ? gemmF16Mfma<true> : gemmF16Mfma<false>), dim3(tiles), dim3(512), ldsBytes, st,
-                               a16, b16, c, m, n, k, p->lda, p->ldb, p->ldc, p->accumulate, bad);
+                               a16, b16, c, m, n, k, p->lda, p->ldb, p->ldc, p->accumulate, skip);
             break;
         case 100:
         case 101: {
@@ -1769,10 +1798,10 @@ int launchMfma(const mlkd_gemm* p, int form, const uint8_t* bad, hipStream_t st)
             const float* b32 = static_cast<const float*>(p->b);
             if (form == 100) {
                 hipLaunchKernelGGL((acc ? gemmF32Dma<true> : gemmF32Dma<false>), dim3(ftiles), dim3(256), kLdsF32Dma,
-                                   st, a32, b32, c, n, k, p->lda, p->ldb, p->ldc, bad);
+                                   st, a32, b32, c, n, k, p->lda, p->ldb, p->ldc, skip);
             } else {
                 hipLaunchKernelGGL((acc ? gemmF32Mfma<true> : gemmF32Mfma<false>), dim3(ftiles), dim3(256), 0, st,
-                                   a32, b32, c, m, n, k, p->lda, p->ldb, p->ldc, p->accumulate, bad);
+                                   a32, b32, c, m, n, k, p->lda, p->ldb, p->ldc, p->accumulate, skip);
             }
             break;
         }
@@ -1782,22 +1811,13 @@ int launchMfma(const mlkd_gemm* p, int form, const uint8_t* bad, hipStream_t st)
     return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
 }
 
-/// Bytes of the column-group flags (one byte per 64 columns, whole 4-byte
-/// words for the fill kernel).
-int64_t flagBytes(int64_t n) { return (((n + 63) / 64) + 3) & ~int64_t{3}; }
-
 }  // namespace
 
 extern "C" void mlkd_gemm_set_variant(int variant) { gGemmF16Variant = variant; }
 
-extern "C" int64_t mlkd_gemm_scratch_bytes(const mlkd_gemm* p) {
-    if (p == nullptr || p->skip_zero_a == 0 || p->m <= 0 || p->n <= 0 || mfmaForm(p) < 0) return 0;
-    return (flagBytes(p->n) + 255) & ~int64_t{255};
-}
-
 extern "C" const char* mlkd_gemm_kernel_name(const mlkd_gemm* p) {
     const bool acc = p->accumulate != 0;
-    switch (mfmaForm(p)) {
+    switch (p->skip_zero_a != 0 && !acc ? -1 : mfmaForm(p)) {
         case 8:
             if (scalarAddressed8(p)) return acc ? "gemmF16Dma8s<true>" : "gemmF16Dma8s<false>";
             return acc ? "gemmF16Dma8<true>" : "gemmF16Dma8<false>";
@@ -1820,32 +1840,13 @@ extern "C" int mlkd_launch_gemm(const mlkd_gemm* p, void* stream) {
     if (p == nullptr || p->m < 0 || p->n < 0 || p->k < 0) return MLKD_RT_LAUNCH;
     if (p->m == 0 || p->n == 0) return 0;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const int form = mfmaForm(p);
-    if (form >= 0 && p->skip_zero_a == 0) return launchMfma(p, form, nullptr, st);
-    if (form >= 0 && p->scratch != nullptr && p->scratch_bytes >= flagBytes(p->n)) {
-        // The skip decided on the device, per column group: flags cleared by
-        // a kernel (no memset node under capture), B scanned, the MFMA form
-        // over every tile whose columns are all finite in B, then the exact
-        // kernel over the rest. No host read-back.
-        uint8_t* bad = static_cast<uint8_t*>(p->scratch);
-        const int64_t words = flagBytes(p->n) / 4;
-        hipLaunchKernelGGL(clearWords, dim3(static_cast<unsigned>((words + 255) / 256)), dim3(256), 0, st,
-                           reinterpret_cast<uint32_t*>(bad), words);
-        const int64_t chunks = p->k * (p->n / (p->b_dtype == MLKD_F16 ? 8 : 4));
-        const unsigned scanBlocks = static_cast<unsigned>(std::min<int64_t>((chunks + 1023) / 1024, 4096));
-        if (p->b_dtype == MLKD_F16) {
-            hipLaunchKernelGGL(scanBadColumns<MLKD_F16>, dim3(scanBlocks), dim3(256), 0, st, p->b, p->k, p->n, p->ldb,
-                               bad);
-        } else {
-            hipLaunchKernelGGL(scanBadColumns<MLKD_F32>, dim3(scanBlocks), dim3(256), 0, st, p->b, p->k, p->n, p->ldb,
-                               bad);
-        }
-        if (hipGetLastError() != hipSuccess) return MLKD_RT_LAUNCH;
-        if (const int rc = launchMfma(p, form, bad, st); rc != 0) return rc;
-        const int64_t rowTiles = (p->m + 63) / 64;
-        const dim3 grid(static_cast<unsigned>(p->n / 64), static_cast<unsigned>(std::min<int64_t>(rowTiles, 16)));
-        hipLaunchKernelGGL(gemmFixBadColumns<float>, grid, dim3(256), 0, st, *p, bad, formTileCols(form));
-        return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
+    // The MFMA forms take the skip-zero-A Call form themselves: a wave whose
+    // accumulators met an infinity or a NaN recomputes its block exactly. One
+    // launch, no scratch, no host read-back.
+    // Only the accumulating (Call) form skips; a non-accumulating launch that
+    // asks for the skip takes the general kernel.
+    if (const int form = mfmaForm(p); form >= 0 && (p->skip_zero_a == 0 || p->accumulate != 0)) {
+        return launchMfma(p, form, st);
     }
     const int64_t tiles = ((p->m + 63) / 64) * ((p->n + 63) / 64);
     if (tiles > 0x7FFFFFFF) return MLKD_RT_LAUNCH;

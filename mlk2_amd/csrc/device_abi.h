@@ -45,13 +45,10 @@ typedef struct mlkd_gemm {
     int32_t variant;      /* launch form; -1: the process default */
     /* 1: skip the products of A[i,p] == 0, the reference's gemmRowBlock
        (kernel_buffers.cpp:422), with C[i,j] = C_in + sum over p ascending.
-       With scratch of mlkd_gemm_scratch_bytes the MFMA form runs on the
-       column blocks where B is finite and the exact general kernel on the
-       rest, decided on the device; without it the general kernel runs on
-       everything. */
+       With `accumulate`, the MFMA forms run it: a wave whose accumulators
+       met an infinity or a NaN (only there can the skip change C) recomputes
+       its block exactly. Otherwise the general kernel runs everything. */
     int32_t skip_zero_a;
-    void* scratch;
-    int64_t scratch_bytes;
 } mlkd_gemm;
 
 /// S[b*seq + i, j] = softmax_j((Q[b,i,:] . K[b,j,:]) / div + bias[j]).

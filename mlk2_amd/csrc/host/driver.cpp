@@ -248,10 +248,6 @@ const char* HipLoadedKernel::stepKernelName(size_t si) const {
         } else if (st.kind == StepKind::Gemm) {
             mlkd_gemm p;
             fillGemmParams(st, ptr, p);
-            if (const int64_t need = mlkd_gemm_scratch_bytes(&p); need > 0) {
-                p.scratch = ptr[0];
-                p.scratch_bytes = need;
-            }
             name = mlkd_gemm_kernel_name(&p);
         } else if (st.kind == StepKind::ScoreSoftmax) {
             mlkd_score_softmax p;
@@ -283,8 +279,6 @@ void HipLoadedKernel::fillGemmParams(const Step& st, const std::vector<void*>& p
     p.lda = st.lda;
     p.ldb = st.ldb;
     p.ldc = st.ldc;
-    p.scratch = nullptr;
-    p.scratch_bytes = 0;
 }
 
 int HipLoadedKernel::arenaLayout(const DeviceBinding* binds, int64_t elements, const ScratchArena& arena,
@@ -325,10 +319,6 @@ int HipLoadedKernel::arenaLayout(const DeviceBinding* binds, int64_t elements, c
             mlkd_score_softmax p;
             fillScoreParams(st, ptr, p);
             need = mlkd_score_scratch_bytes(&p);
-        } else if (st.kind == StepKind::Gemm) {
-            mlkd_gemm p;
-            fillGemmParams(st, ptr, p);
-            need = mlkd_gemm_scratch_bytes(&p);
         }
         if (need > 0) {
             stepOff[si] = used;
@@ -473,26 +463,8 @@ int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* 
                 fillGemmParams(st, ptr, p);
                 // The skip-zero-A decision (0 * inf and 0 * NaN are the only
                 // products whose skip changes C beyond the sign of a zero
-                // sum) is taken on the device per column block of B, in the
-                // flags this scratch holds; no host read-back.
-                if (const int64_t need = mlkd_gemm_scratch_bytes(&p); need > 0 && arena != nullptr) {
-                    p.scratch = arena->base + stepOff[si];
-                    p.scratch_bytes = need;
-                } else if (need > 0) {
-                    std::lock_guard<std::mutex> g(scratchLock_);
-                    if (rs->step[si] == nullptr || rs->stepBytes[si] < need) {
-                        if (rs->step[si] != nullptr) mlkd_rt_free(rs->step[si]);
-                        rs->step[si] = nullptr;
-                        if (mlkd_rt_malloc(&rs->step[si], static_cast<size_t>(need)) != 0) {
-                            rs->step[si] = nullptr;
-                            why = "matmul flag scratch allocation failed";
-                            return MLKHIP_RUNTIME;
-                        }
-                        rs->stepBytes[si] = need;
-                    }
-                    p.scratch = rs->step[si];
-                    p.scratch_bytes = rs->stepBytes[si];
-                }
+                // sum) is taken inside the MFMA kernel, per wave: one launch,
+                // no scratch, no host read-back.
                 rc = mlkd_launch_gemm(&p, stream);
                 break;
             }

@@ -1,10 +1,11 @@
 """Executor semantics at the boundary, on the device, against the oracle.
 
 * Call(MatMul) skips A[i,p] == 0 (gemmRowBlock, runtime/src/execution/
-  kernel_buffers.cpp:422): 0 * inf or 0 * NaN in B must not reach C. The
-  backend flags, on the device, the column groups of B that hold non-finite
-  values; the MFMA form computes the other tiles and the exact skip kernel
-  the flagged ones.
+  kernel_buffers.cpp:422): 0 * inf or 0 * NaN in B must not reach C. Only
+  there can the skip change C, and there the MFMA accumulators of every row
+  of those columns come out non-finite; inside the one MFMA launch, a wave
+  whose block holds such a value recomputes it exactly with the skip, and
+  the other waves store the MFMA result.
 * A fused class keeps its temps on chip only when no other root reads them;
   a later root that reads the softmax row max, or the scaled scores, makes
   the nest run with the walker's materialized temps (kernel_buffers.cpp:
@@ -96,10 +97,9 @@ def test_skip_zero_a_with_nonfinite_b(hip, dt_in, dt_out, m, k, n):
 @pytest.mark.parametrize("dt_in,m,k,n,variant", [("f16", 512, 256, 1024, None), ("f16", 512, 256, 1024, 7),
                                                   ("f16", 256, 128, 1024, 5), ("f32", 256, 128, 512, None)])
 def test_skip_zero_a_mixes_mfma_and_exact_tiles(hip, dt_in, m, k, n, variant):
-    # Non-finite values of B only in columns 300-309: one 256-wide block of
-    # the f16 forms (one 64-wide group of the f32 form). The other tiles take
-    # the MFMA form, the flagged ones the exact kernel, in one run, with C
-    # accumulated from a non-zero start.
+    # Non-finite values of B only in columns 300-309. The waves whose blocks
+    # hold those columns recompute them exactly; every other wave stores its
+    # MFMA result, in one run, with C accumulated from a non-zero start.
     rng = np.random.default_rng(6)
     A = rng.uniform(-1, 1, (m, k))
     B = rng.uniform(-1, 1, (k, n))

@@ -3,9 +3,9 @@
 Its scratch (materialized temps, score-softmax row statistics) comes from one
 file-scope device array. Each case runs twice in a row on that array, the
 second time on a smaller input, and must match mlkhip_run_device on the same
-buffers bit for bit: both run the same kernels. Call(MatMul) keeps its
-skip-zero-A column flags in the array too, so the second, smaller run must not
-see the first run's flags.
+buffers bit for bit: both run the same kernels. Call(MatMul) takes its
+skip-zero-A decision inside its one kernel and needs none of the array; its
+case runs a B with infinities (exact blocks) and then a finite one.
 """
 import math
 import sys
@@ -81,9 +81,9 @@ def test_noalloc_score_softmax_statistics(hip, b, s):
 
 @pytest.mark.parametrize("m,k,n,bad", [(256, 64, 512, True), (128, 32, 128, False)])
 def test_noalloc_matmul_call(hip, m, k, n, bad):
-    # The first run flags column group 6 of B (inf where A is zero, and a
-    # row that reads it); the second, smaller run has B finite and must take
-    # the MFMA form on every tile.
+    # The first run has inf in B where A is zero, and a row that reads it:
+    # the waves over columns 400-402 recompute their blocks exactly. The
+    # second, smaller run has B finite and stores the MFMA result everywhere.
     km = fx.config4_module(m, k, n, "f32", tier=1)
     d = inputs.config_inputs("c4a", {"m": m, "k": k, "n": n})
     A, B = d["A"].astype(np.float64).reshape(m, k), d["B"].astype(np.float64).reshape(k, n)
