@@ -1191,7 +1191,7 @@ __device__ __forceinline__ void dmaLoad16s(const void* sbase, uint32_t voff, uin
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(m0) : "memory");
 }
 
-/// Variant 8 for K a multiple of 128: the same tiles, ring, swizzles and MFMA
+/// Variant 8 (K a multiple of 64): the same tiles, ring, swizzles and MFMA
 /// sequence as gemmF16Dma8 (results identical bit for bit), with no per-step
 /// vector address arithmetic and a fixed instruction order.
 /// * Vector instructions take issue cycles from the MFMAs of the wave sharing
@@ -1341,11 +1341,16 @@ __global__ __launch_bounds__(512, 1) void gemmF16Dma8s(const _Float16* __restric
             __builtin_amdgcn_sched_barrier(0);
         }
     };
-    for (int s = 0; s < steps; s += 4) {
+    int s = 0;
+    for (; s + 4 <= steps; s += 4) {
         step(s, 0, bX, bY);
         step(s + 1, 1, bY, bX);
         step(s + 2, 2, bX, bY);
         step(s + 3, 3, bY, bX);
+    }
+    if (s < steps) {   // K % 128 == 64: two more steps, in slots 0 and 1
+        step(s, 0, bX, bY);
+        step(s + 1, 1, bY, bX);
     }
     // No direct load may still be writing LDS when the workgroup ends.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -1734,10 +1739,10 @@ int mfmaForm(const mlkd_gemm* p) {
     return -1;
 }
 
-/// Form 8 takes gemmF16Dma8s (K a multiple of 128, lane offsets within 32
-/// bits) and gemmF16Dma8 otherwise; the two give identical results.
+/// Form 8 takes gemmF16Dma8s when its lane offsets fit 32 bits and
+/// gemmF16Dma8 otherwise; the two give identical results.
 bool scalarAddressed8(const mlkd_gemm* p) {
-    return p->k % (4 * kDmaBK) == 0 && p->lda < (int64_t{1} << 23) && p->ldb < (int64_t{1} << 25);
+    return p->lda < (int64_t{1} << 23) && p->ldb < (int64_t{1} << 25);
 }
 
 int launchMfma(const mlkd_gemm* p, int form, hipStream_t st) {

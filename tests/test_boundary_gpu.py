@@ -236,8 +236,8 @@ def test_step_kernel_names_name_the_launched_kernels(hip):
     cases = [
         (fx.config2_module(64, 4096, tier=1), ["softmaxWaveRowPair<16, true>"]),
         (fx.config2_module(64, 1001, tier=1), ["softmaxBlockRow"]),
-        (fx.config4_module(256, 256, 256, "f16", tier=1), ["gemmF16Dma8s<true>"]),   # K % 128 == 0
-        (fx.config4_module(256, 192, 256, "f16", tier=1), ["gemmF16Dma8<true>"]),
+        (fx.config4_module(256, 256, 256, "f16", tier=1), ["gemmF16Dma8s<true>"]),
+        (fx.config4_module(256, 192, 256, "f16", tier=1), ["gemmF16Dma8s<true>"]),   # K % 128 == 64
         (fx.config4_module(256, 256, 256, "f16", tier=2), ["gemmF16Dma8s<false>"]),
         (fx.config4_module(256, 128, 256, "f32", tier=1), ["gemmF32Dma<true>"]),
         (fx.config4_module(70, 33, 65, "f64", tier=1), ["gemmGeneral<double>"]),

@@ -312,10 +312,10 @@ def test_c4b_gemm_f16(hip, m, k, n):
 @pytest.mark.parametrize("m,k,n,tier", [(512, 4096, 256, 2), (256, 192, 512, 2), (512, 640, 256, 1),
                                         (256, 320, 256, 1)])
 def test_c4b_form8_kernels_match_form7_bitwise(hip, m, k, n, tier):
-    # Form 8 runs gemmF16Dma8s when K is a multiple of 128 and gemmF16Dma8
-    # otherwise; both take every output's products in form 7's k order, so
-    # all three agree bit for bit, for the nest (C = A*B) and for the Call
-    # form (C += A*B over a nonzero C).
+    # Form 8 runs gemmF16Dma8s (its loop unrolled over the 4 ring slots, with
+    # a two-step tail when K % 128 == 64); it takes every output's products
+    # in form 7's k order, so the two agree bit for bit, for the nest
+    # (C = A*B) and for the Call form (C += A*B over a nonzero C).
     say(f"c4b form 8 vs form 7 bitwise {m}x{k}x{n} tier {tier}")
     d = inputs.config_inputs("c4b", {"m": m, "k": k, "n": n})
     km = fx.config4_module(m, k, n, "f16", tier)
@@ -329,7 +329,7 @@ def test_c4b_form8_kernels_match_form7_bitwise(hip, m, k, n, tier):
             arrays[2] = c0
         outs[form] = art.run(arrays)[2]
     art.set_step_variant(0, -1)
-    assert art.step_kernel_name(0).startswith("gemmF16Dma8s" if k % 128 == 0 else "gemmF16Dma8<")
+    assert art.step_kernel_name(0).startswith("gemmF16Dma8s")
     bits = {f: o.astype(np.float32).view(np.uint32) for f, o in outs.items()}   # f32 results, carried in f64
     assert np.array_equal(bits[8], bits[7])
     ref = _gemm_ref(d["A"].astype(np.float64), d["B"].astype(np.float64)).reshape(-1)
