@@ -82,8 +82,8 @@ typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 //   keys of the same query, and the pair is combined once at the end into
 //   scratch[row][key half].
 //   Pass 2 (scoreStoreQ) computes D = Q K^T per panel and writes
-//   exp(v - max) / sum for the panel at once: each 32-lane half-wave stores
-//   one 128-byte line, while the other workgroup on the CU computes.
+//   exp2(v - (max + log2 sum)) for the panel at once: each 32-lane half-wave
+//   stores one 128-byte line, while the other workgroup on the CU computes.
 // Both passes work in base 2 with log2(e) folded into 1/div and the bias, so
 // a score costs one fused multiply-add and one v_exp_f32. Pass 2 is bound by
 // its stores (256 MiB in the MFMA output layout); pass 1 by its MFMAs and
@@ -208,10 +208,13 @@ __device__ __forceinline__ float2 statsRangeQ(const _Float16* __restrict__ Q, co
 }
 
 /// Row statistics of the 16 rows this lane's pass-2 accumulators hold,
-/// merged from NP key-range partials part[row * NP + i] (base 2).
+/// merged from NP key-range partials part[row * NP + i] (base 2), as one
+/// log-normalizer per row: rlm = max + log2(sum(exp2(v - max))), so pass 2
+/// writes exp2(v - rlm) = exp2(v - max) / sum with no multiply. A row whose
+/// scores are all -inf gets rlm = -inf (max -inf, sum 0): exp2(-inf - -inf)
+/// writes NaN, as the reference does.
 template <int NP>
-__device__ __forceinline__ void mergeStatsQ(const float2* __restrict__ part, int64_t r0, float (&rmx)[16],
-                                            float (&rinv)[16]) {
+__device__ __forceinline__ void mergeStatsQ(const float2* __restrict__ part, int64_t r0, float (&rlm)[16]) {
     const int hl = (threadIdx.x & 63) >> 5;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -226,8 +229,7 @@ __device__ __forceinline__ void mergeStatsQ(const float2* __restrict__ part, int
         float lt = 0.0f;
 #pragma unroll
         for (int i = 0; i < NP; ++i) lt += pp[i].y * __builtin_amdgcn_exp2f(pp[i].x - ms);
-        rmx[r] = mx;  // -inf for a row of -inf scores: exp2(-inf - -inf) writes NaN, as the reference does
-        rinv[r] = lt != 0.0f ? 1.0f / lt : 0.0f;
+        rlm[r] = mx + __builtin_amdgcn_logf(lt);   // v_log_f32: log2
     }
 }
 
@@ -237,7 +239,7 @@ __device__ __forceinline__ void mergeStatsQ(const float2* __restrict__ part, int
 __device__ __forceinline__ void storeRangeQ(const _Float16* __restrict__ Q, const _Float16* __restrict__ K,
                                             const float* __restrict__ bias, float* __restrict__ S, int seq,
                                             float c2, int64_t b, int64_t r0, int k0, int keys,
-                                            const float (&rmx)[16], const float (&rinv)[16], _Float16* ldsQ) {
+                                            const float (&rlm)[16], _Float16* ldsQ) {
     const int tid = threadIdx.x;
     const int lane = tid & 63, l32 = lane & 31, hl = lane >> 5;
     const int np = keys / kPanelQ;
@@ -247,6 +249,13 @@ __device__ __forceinline__ void storeRangeQ(const _Float16* __restrict__ Q, cons
         aq[ks] = *reinterpret_cast<const f16x8*>(Q + (r0 + l32) * kD2 + ks * 16 + hl * 8);
     }
     const _Float16* kb = K + (b * seq + k0) * kD2;
+    // Stores: a scalar base per panel (row r0, key kc) plus a fixed lane
+    // offset per accumulator register r, the key sub-block j as an immediate.
+    uint32_t soff[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        soff[r] = static_cast<uint32_t>(((8 * (r >> 2) + 4 * hl + (r & 3)) * seq + l32) * sizeof(float));
+    }
     u32x4v v[8];
     loadPanelQ(kb, tid, v);
     storePanelQ(ldsQ, tid, v);
@@ -272,12 +281,13 @@ __device__ __forceinline__ void storeRangeQ(const _Float16* __restrict__ Q, cons
         float bj[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) bj[j] = bias[kc + j * 32 + l32] * kLog2e;
+        char* sb = reinterpret_cast<char*>(S + r0 * static_cast<int64_t>(seq) + kc);
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            float* dst = S + (r0 + 8 * (r >> 2) + 4 * hl + (r & 3)) * static_cast<int64_t>(seq) + kc + l32;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                dst[j * 32] = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[j][r], c2, bj[j]) - rmx[r]) * rinv[r];
+                *reinterpret_cast<float*>(sb + soff[r] + j * 32 * sizeof(float)) =
+                    __builtin_amdgcn_exp2f(__builtin_fmaf(acc[j][r], c2, bj[j]) - rlm[r]);
             }
         }
         if (p + 1 < np) storePanelQ(ldsQ + ((p + 1) & 1) * kPanelHalvesQ, tid, v);
@@ -307,10 +317,11 @@ __global__ __launch_bounds__(256, 2) void scoreStoreQ(const _Float16* __restrict
     int64_t b;
     int rb, kh;
     blockOfQ(seq / 128, b, rb, kh);
-    const int64_t r0 = b * seq + static_cast<int64_t>(rb) * 128 + (threadIdx.x >> 6) * 32;
-    float rmx[16], rinv[16];
-    mergeStatsQ<2>(part, r0, rmx, rinv);
-    storeRangeQ(Q, K, bias, S, seq, c2, b, r0, kh * (seq / 2), seq / 2, rmx, rinv, ldsQ);
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int64_t r0 = b * seq + static_cast<int64_t>(rb) * 128 + wave * 32;   // wave-uniform
+    float rlm[16];
+    mergeStatsQ<2>(part, r0, rlm);
+    storeRangeQ(Q, K, bias, S, seq, c2, b, r0, kh * (seq / 2), seq / 2, rlm, ldsQ);
 }
 
 int launchQ(const mlkd_score_softmax* p, hipStream_t st) {
