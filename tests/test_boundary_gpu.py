@@ -125,6 +125,66 @@ def test_skip_zero_a_mixes_mfma_and_exact_tiles(hip, dt_in, m, k, n, variant):
     assert nonfinite == 5 and ok
 
 
+@pytest.mark.parametrize("dt_in,m,k,n", [("f16", 512, 256, 512), ("f32", 128, 128, 128)])
+def test_skip_zero_a_every_declared_form(hip, dt_in, m, k, n):
+    # Every launch form of the Call(MatMul) step takes the skip inside its
+    # own kernel: the waves whose blocks hold columns 300-302 (f16) or 70-72
+    # (f32) of B, where inf meets A[i,p] == 0, recompute exactly; the rest
+    # store their MFMA result. Each form is held to the oracle.
+    rng = np.random.default_rng(8)
+    A = rng.uniform(-1, 1, (m, k))
+    B = rng.uniform(-1, 1, (k, n))
+    c0 = 300 if n > 300 else 70
+    B[9, c0:c0 + 3] = np.inf
+    B[k - 3, c0 + 1] = np.nan
+    A[:, 9] = 0.0
+    A[:, k - 3] = 0.0
+    A[5, 9] = -0.75                              # row 5 reads the infinities
+    np_dt = {"f32": np.float32, "f16": np.float16}[dt_in]
+    A = A.astype(np_dt).astype(np.float64)
+    B = B.astype(np_dt).astype(np.float64)
+    C0 = rng.uniform(-1, 1, m * n)
+    call = fx.matmul_call_module(m, k, n, dt_in, "f32")
+    ref = oracle.run(call, {0: A.reshape(-1), 1: B.reshape(-1)}, init={2: C0})[2]
+    art = hip.build(call)
+    forms = art.step_variants(0)
+    assert forms, "the Call(MatMul) step declares its launch forms"
+    tol = 1e-5 * math.sqrt(k) if dt_in == "f32" else 1e-2
+    for form in forms:
+        art.set_step_variant(0, form)
+        got = art.run({0: A, 1: B, 2: C0})[2]
+        ok = same_class_close(got, ref, tol)
+        say(f"skip-zero-A {dt_in} {m}x{k}x{n} form {form}: {int((~np.isfinite(got)).sum())} non-finite, close: {ok}")
+        assert ok, form
+    art.set_step_variant(0, -1)
+    assert int((~np.isfinite(ref)).sum()) == 3
+
+
+def test_skip_zero_a_f32_overflow_takes_the_exact_path(hip):
+    # Finite f32 operands whose products overflow make non-finite
+    # accumulators with B finite; those blocks take the exact path, which
+    # computes the same overflow the reference does.
+    m = k = n = 128
+    rng = np.random.default_rng(9)
+    A = rng.uniform(-1, 1, (m, k)).astype(np.float32).astype(np.float64)
+    B = rng.uniform(-1, 1, (k, n)).astype(np.float32).astype(np.float64)
+    A[3, 0] = 3e38
+    B[0, 7] = 2.0                                # 6e38: +inf in f32
+    A[4, 1] = -3e38
+    B[1, 8] = 4.0                                # -inf
+    C0 = np.zeros(m * n)
+    call = fx.matmul_call_module(m, k, n, "f32", "f32")
+    ref = oracle.run(call, {0: A.reshape(-1), 1: B.reshape(-1)}, init={2: C0})[2]
+    got = hip.build(call).run({0: A, 1: B, 2: C0})[2]
+    # The oracle accumulates in f64, where these sums stay finite; the f32
+    # output rounds them to inf. Compare in f32.
+    ref32 = ref.astype(np.float32).astype(np.float64)
+    assert np.isposinf(got.reshape(m, n)[3, 7]) and np.isneginf(got.reshape(m, n)[4, 8])
+    ok = same_class_close(got, ref32, 1e-5 * math.sqrt(k))
+    say(f"f32 overflow: {int(np.isinf(got).sum())} infinities, finite ones close: {ok}")
+    assert ok
+
+
 def test_fused_softmax_temps_read_by_a_later_root(hip):
     km = fx.softmax_rowmax_reader_module(32, 256)
     x = inputs.config_inputs("c2", {"m": 32, "k": 256})["x"]
