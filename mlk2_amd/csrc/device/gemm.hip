@@ -4,7 +4,8 @@
 // poly.synth.cpp:58-147, C = 0 then +=).
 //
 // f16 x f16 -> f32 (tensor_f16_gpu), 256x256 workgroup tiles, launch forms 0-8.
-// The default, form 8 (gemmF16Dma8), moves both operands global -> LDS by
+// The default, form 8 (gemmF16Dma8s, or gemmF16Dma8 when a lane offset
+// needs more than 32 bits), moves both operands global -> LDS by
 // the direct path into a 4-deep ring of K steps and runs 8 waves of
 // v_mfma_f32_16x16x32_f16 tiles; form 7 (gemmF16Dma) is the same data path
 // with 4 waves of 32x32x16 tiles. Form 0, the first: v_mfma_f32_32x32x16_f16,
