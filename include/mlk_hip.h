@@ -228,7 +228,7 @@ int mlkhip_plan_variants(const char* module_json, size_t len, int step, int* out
  * source hash>; a generic loop nest: mlk_nest), or the precompiled kernel
  * the step's launcher picks for its shape, dtypes and pinned form on
  * 256-byte aligned buffers, with template arguments and without parameters
- * (gemmF16Dma8<true>, softmaxWaveRowPair<16, true>; a two-kernel launch
+ * (gemmF16Dma8s<true>, softmaxWaveRowPair<16, true>; a two-kernel launch
  * joins them with '+': scoreStatsQ+scoreStoreQ). The text lives as long as
  * the artifact. */
 const char* mlkhip_step_kernel_name(const mlkhip_artifact* a, int step);
