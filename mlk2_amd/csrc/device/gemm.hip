@@ -1503,8 +1503,13 @@ __global__ __launch_bounds__(256, 1) void gemmF32Dma(const float* __restrict__ A
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int tilesN = N / kFN;
-    const int64_t row0 = static_cast<int64_t>(blockIdx.x / tilesN) * kFM;
-    const int64_t col0 = static_cast<int64_t>(blockIdx.x % tilesN) * kFN;
+    // XCD-blocked map: at 1024^2 each XCD's 32 tiles form a 4 x 8 block, so
+    // its L2 holds 4 A and 8 B panels (3 MiB) instead of 16 A panels; the
+    // bytes fetched per launch drop by a third (18.5 -> 12.3 MB, FETCH_SIZE).
+    int tm, tn;
+    xcdTile(static_cast<int>(gridDim.x) / tilesN, tilesN, tm, tn);
+    const int64_t row0 = static_cast<int64_t>(tm) * kFM;
+    const int64_t col0 = static_cast<int64_t>(tn) * kFN;
     const int steps = K / kQK;
     // Stage `slot` receives K step min(slot, steps - 1) in ring slot
     // slot % kQStages. A is 64 rows of 256 bytes and B 64 k-rows of 256

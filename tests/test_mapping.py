@@ -152,6 +152,7 @@ def test_gemm_expected_values_match_oracle():
                                          # row-major (3 x 5) and in XCD groups of 4 x 8
                                          # (8 x 32 and 32 x 8 tiles)
                                          (192, 256, 320, "f32"), (2048, 128, 512, "f32"),
+                                         (512, 128, 2048, "f32"),
                                          (768, 1024, 1280, "f16"), (2048, 2048, 8192, "f16"),
                                          (8192, 256, 2048, "f16")])
 def test_gemm_full_shape_mapping_every_form(hip, m, k, n, dtype):
