@@ -1505,7 +1505,7 @@ __global__ __launch_bounds__(256, 1) void gemmF32Dma(const float* __restrict__ A
     const int tilesN = N / kFN;
     // XCD-blocked map: at 1024^2 each XCD's 32 tiles form a 4 x 8 block, so
     // its L2 holds 4 A and 8 B panels (3 MiB) instead of 16 A panels; the
-    // bytes fetched per launch drop by a third (18.5 -> 12.3 MB, FETCH_SIZE).
+    // bytes fetched per launch drop by a third (FETCH_SIZE 18470 -> 12330 KiB).
     int tm, tn;
     xcdTile(static_cast<int>(gridDim.x) / tilesN, tilesN, tm, tn);
     const int64_t row0 = static_cast<int64_t>(tm) * kFM;
