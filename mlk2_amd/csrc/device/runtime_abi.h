@@ -83,8 +83,8 @@ int mlkd_launch_softmax(const mlkd_softmax* p, void* stream);
 void mlkd_softmax_set_variant(int variant, int64_t waves);
 int mlkd_launch_gemm(const mlkd_gemm* p, void* stream);
 /// The symbol of the kernel mlkd_launch_gemm runs for `p` (the MFMA form, or
-/// the general kernel; a skip-zero-A launch adds the column scan and the
-/// fix-up around the form), as profilers print it without the parameters.
+/// the general kernel), as profilers print it without the parameters. A
+/// skip-zero-A launch is the same single kernel.
 const char* mlkd_gemm_kernel_name(const mlkd_gemm* p);
 /// Likewise for the softmax launch (valid until this thread's next call).
 const char* mlkd_softmax_kernel_name(const mlkd_softmax* p);

@@ -51,10 +51,9 @@ public:
     const std::vector<uint32_t>& bindables() const { return bindables_; }
 
     /// Device-resident run on `stream`; returns an ABI status code and sets
-    /// `why` on failure. With `arena`, every scratch buffer (temps, launcher
-    /// scratch, the Call(MatMul) column flags) is carved out of it and
-    /// nothing is allocated; steps that need a host read-back are refused
-    /// (checked loop nests).
+    /// `why` on failure. With `arena`, every scratch buffer (temps and
+    /// launcher scratch) is carved out of it and nothing is allocated; steps
+    /// that need a host read-back are refused (checked loop nests).
     int runDevice(const DeviceBinding* binds, int n, const double* scalars, int64_t nScalars,
                   int64_t elements, void* stream, std::string& why, const ScratchArena* arena = nullptr) const;
 
@@ -104,11 +103,11 @@ private:
     // Artifact-owned device scratch of the runs on one stream: temps (zeroed
     // on every run like the reference's fresh temp storage), the status word
     // of loop-nest steps with run-time bounds checks, and per-step scratch a
-    // launcher asks for (score-softmax row statistics, the Call(MatMul)
-    // column flags). Allocated on first use and kept until the artifact or
-    // the stream's set is released (releaseStreamScratch). Each stream gets
-    // its own set, so runs on different streams never share device memory;
-    // runs on one stream are ordered by it.
+    // launcher asks for (score-softmax row statistics). Allocated on first
+    // use and kept until the artifact or the stream's set is released
+    // (releaseStreamScratch). Each stream gets its own set, so runs on
+    // different streams never share device memory; runs on one stream are
+    // ordered by it.
     struct RunScratch {
         std::vector<void*> temp;
         std::vector<int64_t> tempElems;
