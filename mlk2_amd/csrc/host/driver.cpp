@@ -1,9 +1,15 @@
 // HIP backend driver and the C ABI of include/mlk_hip.h.
 #include "driver.h"
 
+#include <pthread.h>
+#include <unistd.h>
+
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <memory>
+#include <new>
 #include <unordered_map>
 
 #include "../device/runtime_abi.h"
@@ -36,6 +42,49 @@ double fromHalfBits(uint16_t bits) {
     _Float16 h;
     std::memcpy(&h, &bits, sizeof(h));
     return static_cast<double>(h);
+}
+
+struct RangeJob {
+    const void* fn;
+    void (*call)(const void*, int64_t, int64_t);
+    int64_t begin, end;
+};
+
+void* rangeThread(void* p) {
+    const RangeJob* j = static_cast<const RangeJob*>(p);
+    j->call(j->fn, j->begin, j->end);
+    return nullptr;
+}
+
+/// Runs fn(begin, end) over [0, n) split across up to 16 host threads, each
+/// taking at least 2^18 elements; below 2^20 elements, or for a thread that
+/// cannot be started, the calling thread runs the range itself. The host
+/// ABI's dtype conversions are element-wise, so the split changes no result.
+template <typename F>
+void parallelRange(int64_t n, const F& fn) {
+    constexpr int kMaxThreads = 16;
+    const long cpus = sysconf(_SC_NPROCESSORS_ONLN);
+    int64_t t = std::min<int64_t>({kMaxThreads, cpus > 0 ? cpus : 1, n >> 18});
+    if (n < (int64_t{1} << 20) || t < 2) {
+        fn(int64_t{0}, n);
+        return;
+    }
+    RangeJob jobs[kMaxThreads];
+    pthread_t threads[kMaxThreads];
+    bool started[kMaxThreads] = {};
+    for (int64_t i = 0; i < t; ++i) {
+        jobs[i] = {&fn, [](const void* f, int64_t b, int64_t e) { (*static_cast<const F*>(f))(b, e); }, n * i / t,
+                   n * (i + 1) / t};
+    }
+    for (int64_t i = 1; i < t; ++i) started[i] = pthread_create(&threads[i], nullptr, rangeThread, &jobs[i]) == 0;
+    fn(jobs[0].begin, jobs[0].end);
+    for (int64_t i = 1; i < t; ++i) {
+        if (started[i]) {
+            pthread_join(threads[i], nullptr);
+        } else {
+            fn(jobs[i].begin, jobs[i].end);
+        }
+    }
 }
 
 }  // namespace
@@ -603,18 +652,30 @@ int HipLoadedKernel::runHost(double* const* ptrs, int n, const double* scalars, 
         }
         owned.push_back(d);
         binds[i].ptr = d;
-        std::vector<unsigned char> stage(bytes);
         const double* src = ptrs[i];
-        if (kb.dtype == Dtype::F64) {
-            std::memcpy(stage.data(), src, bytes);
-        } else if (kb.dtype == Dtype::F32) {
-            float* f = reinterpret_cast<float*>(stage.data());
-            for (int64_t e = 0; e < cnt; ++e) f[e] = static_cast<float>(src[e]);
-        } else {
-            uint16_t* h = reinterpret_cast<uint16_t*>(stage.data());
-            for (int64_t e = 0; e < cnt; ++e) h[e] = toHalfBits(src[e]);
+        const void* up = src;   // f64 buffers upload from the caller's array
+        std::unique_ptr<unsigned char[]> stage;
+        if (kb.dtype != Dtype::F64) {
+            stage.reset(new (std::nothrow) unsigned char[bytes]);
+            if (!stage) {
+                why = "host staging allocation failed";
+                cleanup();
+                return MLKHIP_RUNTIME;
+            }
+            if (kb.dtype == Dtype::F32) {
+                float* f = reinterpret_cast<float*>(stage.get());
+                parallelRange(cnt, [&](int64_t b, int64_t e) {
+                    for (int64_t x = b; x < e; ++x) f[x] = static_cast<float>(src[x]);
+                });
+            } else {
+                uint16_t* h = reinterpret_cast<uint16_t*>(stage.get());
+                parallelRange(cnt, [&](int64_t b, int64_t e) {
+                    for (int64_t x = b; x < e; ++x) h[x] = toHalfBits(src[x]);
+                });
+            }
+            up = stage.get();
         }
-        if (mlkd_rt_h2d(d, stage.data(), bytes, nullptr) != 0 || mlkd_rt_sync(nullptr) != 0) {
+        if (mlkd_rt_h2d(d, up, bytes, nullptr) != 0 || mlkd_rt_sync(nullptr) != 0) {
             why = "host-to-device copy failed";
             cleanup();
             return MLKHIP_RUNTIME;
@@ -632,21 +693,36 @@ int HipLoadedKernel::runHost(double* const* ptrs, int n, const double* scalars, 
             if (kb.isTemp || !written[b] || binds[i].elements == 0) continue;
             const int64_t cnt = binds[i].elements;
             const size_t bytes = static_cast<size_t>(cnt) * dtypeBytes(kb.dtype);
-            std::vector<unsigned char> stage(bytes);
-            if (mlkd_rt_d2h(stage.data(), binds[i].ptr, bytes, nullptr) != 0 || mlkd_rt_sync(nullptr) != 0) {
+            double* dst = ptrs[i];
+            if (kb.dtype == Dtype::F64) {   // straight into the caller's array
+                if (mlkd_rt_d2h(dst, binds[i].ptr, bytes, nullptr) != 0 || mlkd_rt_sync(nullptr) != 0) {
+                    why = "device-to-host copy failed";
+                    rc = MLKHIP_RUNTIME;
+                    break;
+                }
+                continue;
+            }
+            std::unique_ptr<unsigned char[]> stage(new (std::nothrow) unsigned char[bytes]);
+            if (!stage) {
+                why = "host staging allocation failed";
+                rc = MLKHIP_RUNTIME;
+                break;
+            }
+            if (mlkd_rt_d2h(stage.get(), binds[i].ptr, bytes, nullptr) != 0 || mlkd_rt_sync(nullptr) != 0) {
                 why = "device-to-host copy failed";
                 rc = MLKHIP_RUNTIME;
                 break;
             }
-            double* dst = ptrs[i];
-            if (kb.dtype == Dtype::F64) {
-                std::memcpy(dst, stage.data(), bytes);
-            } else if (kb.dtype == Dtype::F32) {
-                const float* f = reinterpret_cast<const float*>(stage.data());
-                for (int64_t e = 0; e < cnt; ++e) dst[e] = static_cast<double>(f[e]);
+            if (kb.dtype == Dtype::F32) {
+                const float* f = reinterpret_cast<const float*>(stage.get());
+                parallelRange(cnt, [&](int64_t b, int64_t e) {
+                    for (int64_t x = b; x < e; ++x) dst[x] = static_cast<double>(f[x]);
+                });
             } else {
-                const uint16_t* h = reinterpret_cast<const uint16_t*>(stage.data());
-                for (int64_t e = 0; e < cnt; ++e) dst[e] = fromHalfBits(h[e]);
+                const uint16_t* h = reinterpret_cast<const uint16_t*>(stage.get());
+                parallelRange(cnt, [&](int64_t b, int64_t e) {
+                    for (int64_t x = b; x < e; ++x) dst[x] = fromHalfBits(h[x]);
+                });
             }
         }
     }
