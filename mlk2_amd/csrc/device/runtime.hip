@@ -93,6 +93,17 @@ int mlkd_rt_free(void* p) {
     return mapErr(hipFree(p), MLKD_RT_ALLOC);
 }
 
+int mlkd_rt_host_alloc(void** p, size_t bytes) {
+    *p = nullptr;
+    if (bytes == 0) bytes = 256;
+    return mapErr(hipHostMalloc(p, bytes, hipHostMallocDefault), MLKD_RT_ALLOC);
+}
+
+int mlkd_rt_host_free(void* p) {
+    if (p == nullptr) return 0;
+    return mapErr(hipHostFree(p), MLKD_RT_ALLOC);
+}
+
 int mlkd_rt_h2d(void* dst, const void* src, size_t bytes, void* stream) {
     if (bytes == 0) return 0;
     return mapErr(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice,

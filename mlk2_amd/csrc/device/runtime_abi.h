@@ -27,6 +27,10 @@ int mlkd_rt_device_info(int dev, int* cu_count, int64_t* max_grid_x, int* max_bl
                         int64_t* global_mem);
 int mlkd_rt_malloc(void** p, size_t bytes);
 int mlkd_rt_free(void* p);
+/// Page-locked host memory (hipHostMalloc): copies between it and the device
+/// run at DMA rate. Released by mlkd_rt_host_free.
+int mlkd_rt_host_alloc(void** p, size_t bytes);
+int mlkd_rt_host_free(void* p);
 int mlkd_rt_h2d(void* dst, const void* src, size_t bytes, void* stream);
 int mlkd_rt_d2h(void* dst, const void* src, size_t bytes, void* stream);
 int mlkd_rt_d2d(void* dst, const void* src, size_t bytes, void* stream);

@@ -87,6 +87,49 @@ void parallelRange(int64_t n, const F& fn) {
     }
 }
 
+/// The caller's f64 values [0, cnt) as `dt` elements at `out` (one rounding
+/// to nearest even for f32 and f16).
+void narrowTo(void* out, const double* src, int64_t cnt, Dtype dt) {
+    if (dt == Dtype::F64) {
+        double* o = static_cast<double*>(out);
+        parallelRange(cnt, [&](int64_t b, int64_t e) {
+            std::memcpy(o + b, src + b, static_cast<size_t>(e - b) * sizeof(double));
+        });
+    } else if (dt == Dtype::F32) {
+        float* o = static_cast<float*>(out);
+        parallelRange(cnt, [&](int64_t b, int64_t e) {
+            for (int64_t x = b; x < e; ++x) o[x] = static_cast<float>(src[x]);
+        });
+    } else {
+        uint16_t* o = static_cast<uint16_t*>(out);
+        parallelRange(cnt, [&](int64_t b, int64_t e) {
+            for (int64_t x = b; x < e; ++x) o[x] = toHalfBits(src[x]);
+        });
+    }
+}
+
+/// `dt` elements [0, cnt) at `in`, widened exactly into the caller's f64s.
+void widenFrom(double* dst, const void* in, int64_t cnt, Dtype dt) {
+    if (dt == Dtype::F64) {
+        const double* s = static_cast<const double*>(in);
+        parallelRange(cnt, [&](int64_t b, int64_t e) {
+            std::memcpy(dst + b, s + b, static_cast<size_t>(e - b) * sizeof(double));
+        });
+    } else if (dt == Dtype::F32) {
+        const float* s = static_cast<const float*>(in);
+        parallelRange(cnt, [&](int64_t b, int64_t e) {
+            for (int64_t x = b; x < e; ++x) dst[x] = static_cast<double>(s[x]);
+        });
+    } else {
+        const uint16_t* s = static_cast<const uint16_t*>(in);
+        parallelRange(cnt, [&](int64_t b, int64_t e) {
+            for (int64_t x = b; x < e; ++x) dst[x] = fromHalfBits(s[x]);
+        });
+    }
+}
+
+constexpr size_t kHostStageBytes = size_t{64} << 20;
+
 }  // namespace
 
 bool validArch(const std::string& arch) {
@@ -195,6 +238,7 @@ HipLoadedKernel::~HipLoadedKernel() {
         (void)stream;
         freeScratch(*rs);
     }
+    mlkd_rt_host_free(hostStage_);
 }
 
 int HipLoadedKernel::releaseStreamScratch(void* stream, std::string& why) {
@@ -608,6 +652,70 @@ int HipLoadedKernel::runHost(double* const* ptrs, int n, const double* scalars, 
         why = "expected " + std::to_string(bindables_.size()) + " bindables, got " + std::to_string(n);
         return MLKHIP_BAD_BINDING;
     }
+    // Host-buffer runs of this artifact share its page-locked staging.
+    std::lock_guard<std::mutex> hostGuard(hostLock_);
+    size_t maxBytes = 0;
+    for (const uint32_t b : bindables_) {
+        const KernelBuffer& kb = km_.buffers[b];
+        const int64_t cnt = bufferElements(kb, elements);
+        if (!kb.isTemp && cnt > 0) maxBytes = std::max(maxBytes, static_cast<size_t>(cnt) * dtypeBytes(kb.dtype));
+    }
+    if (const size_t want = std::min(maxBytes, kHostStageBytes); want > hostStageBytes_) {
+        // Grown to the largest buffer seen, up to 64 MiB; without page-locked
+        // memory the copies go through an ordinary heap buffer instead.
+        void* p = nullptr;
+        if (mlkd_rt_host_alloc(&p, want) == 0) {
+            mlkd_rt_host_free(hostStage_);
+            hostStage_ = p;
+            hostStageBytes_ = want;
+        }
+    }
+    // Caller's f64s -> `dt` on the device, chunk by chunk through the staging.
+    auto copyIn = [&](void* d, const double* src, int64_t cnt, Dtype dt) -> bool {
+        const size_t es = dtypeBytes(dt);
+        if (hostStage_ == nullptr) {
+            std::unique_ptr<unsigned char[]> heap(new (std::nothrow) unsigned char[static_cast<size_t>(cnt) * es]);
+            if (!heap) return false;
+            narrowTo(heap.get(), src, cnt, dt);
+            return mlkd_rt_h2d(d, heap.get(), static_cast<size_t>(cnt) * es, nullptr) == 0 &&
+                   mlkd_rt_sync(nullptr) == 0;
+        }
+        const int64_t per = static_cast<int64_t>(hostStageBytes_ / es);
+        for (int64_t c0 = 0; c0 < cnt; c0 += per) {
+            const int64_t m = std::min(per, cnt - c0);
+            narrowTo(hostStage_, src + c0, m, dt);
+            if (mlkd_rt_h2d(static_cast<char*>(d) + c0 * static_cast<int64_t>(es), hostStage_,
+                            static_cast<size_t>(m) * es, nullptr) != 0 ||
+                mlkd_rt_sync(nullptr) != 0) {
+                return false;
+            }
+        }
+        return true;
+    };
+    // Device `dt` values -> the caller's f64s, the same way back.
+    auto copyOut = [&](double* dst, const void* d, int64_t cnt, Dtype dt) -> bool {
+        const size_t es = dtypeBytes(dt);
+        if (hostStage_ == nullptr) {
+            std::unique_ptr<unsigned char[]> heap(new (std::nothrow) unsigned char[static_cast<size_t>(cnt) * es]);
+            if (!heap) return false;
+            if (mlkd_rt_d2h(heap.get(), d, static_cast<size_t>(cnt) * es, nullptr) != 0 || mlkd_rt_sync(nullptr) != 0) {
+                return false;
+            }
+            widenFrom(dst, heap.get(), cnt, dt);
+            return true;
+        }
+        const int64_t per = static_cast<int64_t>(hostStageBytes_ / es);
+        for (int64_t c0 = 0; c0 < cnt; c0 += per) {
+            const int64_t m = std::min(per, cnt - c0);
+            if (mlkd_rt_d2h(hostStage_, static_cast<const char*>(d) + c0 * static_cast<int64_t>(es),
+                            static_cast<size_t>(m) * es, nullptr) != 0 ||
+                mlkd_rt_sync(nullptr) != 0) {
+                return false;
+            }
+            widenFrom(dst + c0, hostStage_, m, dt);
+        }
+        return true;
+    };
     // Buffers written by some step are copied back (outputs, and any input
     // a Store targets, as the reference writes through the caller's array).
     std::vector<bool> written(km_.buffers.size(), false);
@@ -652,30 +760,7 @@ int HipLoadedKernel::runHost(double* const* ptrs, int n, const double* scalars, 
         }
         owned.push_back(d);
         binds[i].ptr = d;
-        const double* src = ptrs[i];
-        const void* up = src;   // f64 buffers upload from the caller's array
-        std::unique_ptr<unsigned char[]> stage;
-        if (kb.dtype != Dtype::F64) {
-            stage.reset(new (std::nothrow) unsigned char[bytes]);
-            if (!stage) {
-                why = "host staging allocation failed";
-                cleanup();
-                return MLKHIP_RUNTIME;
-            }
-            if (kb.dtype == Dtype::F32) {
-                float* f = reinterpret_cast<float*>(stage.get());
-                parallelRange(cnt, [&](int64_t b, int64_t e) {
-                    for (int64_t x = b; x < e; ++x) f[x] = static_cast<float>(src[x]);
-                });
-            } else {
-                uint16_t* h = reinterpret_cast<uint16_t*>(stage.get());
-                parallelRange(cnt, [&](int64_t b, int64_t e) {
-                    for (int64_t x = b; x < e; ++x) h[x] = toHalfBits(src[x]);
-                });
-            }
-            up = stage.get();
-        }
-        if (mlkd_rt_h2d(d, up, bytes, nullptr) != 0 || mlkd_rt_sync(nullptr) != 0) {
+        if (!copyIn(d, ptrs[i], cnt, kb.dtype)) {
             why = "host-to-device copy failed";
             cleanup();
             return MLKHIP_RUNTIME;
@@ -692,37 +777,10 @@ int HipLoadedKernel::runHost(double* const* ptrs, int n, const double* scalars, 
             const KernelBuffer& kb = km_.buffers[b];
             if (kb.isTemp || !written[b] || binds[i].elements == 0) continue;
             const int64_t cnt = binds[i].elements;
-            const size_t bytes = static_cast<size_t>(cnt) * dtypeBytes(kb.dtype);
-            double* dst = ptrs[i];
-            if (kb.dtype == Dtype::F64) {   // straight into the caller's array
-                if (mlkd_rt_d2h(dst, binds[i].ptr, bytes, nullptr) != 0 || mlkd_rt_sync(nullptr) != 0) {
-                    why = "device-to-host copy failed";
-                    rc = MLKHIP_RUNTIME;
-                    break;
-                }
-                continue;
-            }
-            std::unique_ptr<unsigned char[]> stage(new (std::nothrow) unsigned char[bytes]);
-            if (!stage) {
-                why = "host staging allocation failed";
-                rc = MLKHIP_RUNTIME;
-                break;
-            }
-            if (mlkd_rt_d2h(stage.get(), binds[i].ptr, bytes, nullptr) != 0 || mlkd_rt_sync(nullptr) != 0) {
+            if (!copyOut(ptrs[i], binds[i].ptr, cnt, kb.dtype)) {
                 why = "device-to-host copy failed";
                 rc = MLKHIP_RUNTIME;
                 break;
-            }
-            if (kb.dtype == Dtype::F32) {
-                const float* f = reinterpret_cast<const float*>(stage.get());
-                parallelRange(cnt, [&](int64_t b, int64_t e) {
-                    for (int64_t x = b; x < e; ++x) dst[x] = static_cast<double>(f[x]);
-                });
-            } else {
-                const uint16_t* h = reinterpret_cast<const uint16_t*>(stage.get());
-                parallelRange(cnt, [&](int64_t b, int64_t e) {
-                    for (int64_t x = b; x < e; ++x) dst[x] = fromHalfBits(h[x]);
-                });
             }
         }
     }

@@ -313,3 +313,23 @@ def test_step_kernel_names_name_the_launched_kernels(hip):
     assert art.step_kernel_name(0) == "gemmF16Dma<true>"
     art = hip.build(fx.config1_module(n=4096))
     assert art.step_kernel_name(0).startswith("mlk_elementwise_")
+
+
+@pytest.mark.parametrize("dt_in,dt_out,n", [("f32", "f32", (1 << 24) + 3),    # 64 MiB + 12 B on the device
+                                            ("f16", "f32", (1 << 25) + 5),    # f16 input: 64 MiB + 10 B
+                                            ("f64", "f64", (1 << 23) + 7)])   # f64 both ways, 64 MiB + 56 B
+def test_host_abi_stages_large_buffers_in_chunks(hip, dt_in, dt_out, n):
+    # The host-buffer ABI (mlk_kernel's f64 arrays) converts and copies each
+    # buffer through at most 64 MiB of page-locked staging, chunk by chunk;
+    # these buffers need a second, short chunk both ways. y = x + 0 returns
+    # x rounded once to the input dtype, widened exactly: a misplaced or
+    # stale chunk shows as a mismatch.
+    from mlk2_amd.kernel_ir import KernelExpr, const, elem_a
+    say(f"host abi chunks {dt_in}->{dt_out} n={n}")
+    km = fx.lower_elementwise([("x", [n], dt_in)], [KernelExpr("add", elem_a(), const(0.0))], [n], dt_out)
+    art = hip.build(km)
+    x = inputs.normal(77, n, 0.0, 3.0, "f64")
+    got = art.run({0: x})[km.output_ids()[0]]
+    want = {"f32": x.astype(np.float32), "f16": x.astype(np.float16), "f64": x}[dt_in].astype(np.float64)
+    assert np.array_equal(got, want)
+    say(f"host abi chunks {dt_in}->{dt_out}: every element exact")
