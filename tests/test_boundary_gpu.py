@@ -15,6 +15,8 @@
   lossless document, all-(-inf) softmax rows included.
 * Each stream gets its own artifact scratch, so runs of one artifact on two
   streams at once do not share temps.
+* The host-buffer ABI moves buffers through the artifact's page-locked
+  staging chunk by chunk, one call at a time per artifact.
 """
 import math
 import sys
@@ -333,3 +335,30 @@ def test_host_abi_stages_large_buffers_in_chunks(hip, dt_in, dt_out, n):
     want = {"f32": x.astype(np.float32), "f16": x.astype(np.float16), "f64": x}[dt_in].astype(np.float64)
     assert np.array_equal(got, want)
     say(f"host abi chunks {dt_in}->{dt_out}: every element exact")
+
+
+def test_host_abi_calls_from_two_threads(hip):
+    # Two host threads call the host-buffer ABI of one artifact at once (ctypes
+    # releases the GIL during the call); the calls share the artifact's
+    # page-locked staging one at a time, so each gets its own result.
+    import threading
+    from mlk2_amd.kernel_ir import KernelExpr, const, elem_a
+    n = (1 << 22) + 9
+    km = fx.lower_elementwise([("x", [n], "f32")], [KernelExpr("mul", elem_a(), const(2.0))], [n], "f32")
+    art = hip.build(km)
+    out_id = km.output_ids()[0]
+    xs = [inputs.normal(80 + t, n, 0.0, 1.0, "f64") for t in range(2)]
+    got = [None, None]
+
+    def work(t):
+        for _ in range(3):
+            got[t] = art.run({0: xs[t]})[out_id]
+
+    threads = [threading.Thread(target=work, args=(t,)) for t in range(2)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    for t in range(2):
+        assert np.array_equal(got[t], xs[t].astype(np.float32).astype(np.float64) * 2.0)
+    say("host abi from two threads: both results exact")
