@@ -313,7 +313,9 @@ class LoadedKernel:
         """Host f64 artifact ABI (mlk_kernel multi-dim form, or the legacy 1-D
         form with ``legacy``). ``arrays`` maps buffer ids (inputs, and
         outputs to seed += / max stores) to arrays; every non-temp bindable
-        gets an f64 array, outputs come back by buffer id."""
+        gets an f64 array. Outputs come back by buffer id, and so does every
+        input, as the call left it: a Store may target an input, and the
+        reference then writes through the caller's array."""
         ids = self.bindables()
         host: List[Optional[np.ndarray]] = []
         for bid in ids:
@@ -337,8 +339,7 @@ class LoadedKernel:
             rc = lib().mlkhip_kernel(self._h, ptrs, dims, len(ids), sc.ctypes.data_as(_PD), nsc,
                                      int(elements))
         _check(rc)
-        return {bid: h for bid, h in zip(ids, host)
-                if h is not None and self.module.buffers[bid].is_output}
+        return {bid: h for bid, h in zip(ids, host) if h is not None}
 
     def _bindings(self, bufs: Dict[int, DeviceBuffer]):
         ids = self.bindables()

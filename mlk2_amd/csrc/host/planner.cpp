@@ -453,6 +453,26 @@ Result<Step> elementwiseNest(const KernelModule& km, const NestInfo& ni) {
 
 /// Tier-1 Loop: each Compute child with the first Store child
 /// (kernel_buffers.cpp:921-1000, runElementwiseRange :342-402).
+/// Buffer id the reference's 1-D executor reaches for `bid` (resolveInput /
+/// resolveOutput in runtime/src/execution/kernel_buffers.cpp): its bindings
+/// hold the input buffers, then the output buffers, each in id order, and it
+/// indexes them by the id itself. kInvalidId where that index has no binding.
+uint32_t resolve1d(const KernelModule& km, uint32_t bid, bool store) {
+    if (bid == kInvalidId || bid >= km.buffers.size()) return kInvalidId;
+    std::vector<uint32_t> ins, outs;
+    for (uint32_t b = 0; b < km.buffers.size(); ++b) {
+        if (km.buffers[b].isInput) ins.push_back(b);
+        if (km.buffers[b].isOutput) outs.push_back(b);
+    }
+    const bool viaOutputs = store ? km.buffers[bid].isOutput : !km.buffers[bid].isInput;
+    if (viaOutputs) {
+        if (bid < ins.size()) return kInvalidId;
+        const size_t o = bid - ins.size();
+        return o < outs.size() ? outs[o] : kInvalidId;
+    }
+    return bid < ins.size() ? ins[bid] : kInvalidId;
+}
+
 Result<std::vector<Step>> tier1Loop(const KernelModule& km, const KernelNode& loop) {
     std::vector<Step> out;
     const KernelNode* store = nullptr;
@@ -476,9 +496,17 @@ Result<std::vector<Step>> tier1Loop(const KernelModule& km, const KernelNode& lo
                 needsB = needsB || o->kind == K::ElemB;
             }
         }
-        auto valid = [&](uint32_t bid) { return bid != kInvalidId && bid < km.buffers.size(); };
-        // Unbound operands or output: the reference skips the pair.
-        if (!valid(so.bufferOut) || (needsA && !valid(c.bufferA)) || (needsB && !valid(c.bufferB))) continue;
+        // The 1-D path resolves buffer ids by position, as the reference's
+        // executor does (kernel_buffers.cpp resolveInput / resolveOutput): an
+        // input id indexes the inputs, any other operand id the outputs after
+        // them; an output id indexes the outputs after the inputs, any other
+        // store id the inputs. For modules laid out inputs first, outputs
+        // after (lower.to_kernel_ir's), that is the id itself.
+        const uint32_t bufA = resolve1d(km, c.bufferA, false);
+        const uint32_t bufB = resolve1d(km, c.bufferB, false);
+        const uint32_t bufOut = resolve1d(km, so.bufferOut, true);
+        // Unresolved operands or output: the reference skips the pair.
+        if (bufOut == kInvalidId || (needsA && bufA == kInvalidId) || (needsB && bufB == kInvalidId)) continue;
         Step st;
         st.kind = StepKind::Elementwise;
         st.what = "elementwise-1d";
@@ -511,38 +539,38 @@ Result<std::vector<Step>> tier1Loop(const KernelModule& km, const KernelNode& lo
         auto streamOf = [&](const KernelOperand& o) -> int {
             if (o.kind == K::ElemA) {
                 if (slotA < 0) {
-                    st.inputs.push_back(ref(c.bufferA));
+                    st.inputs.push_back(ref(bufA));
                     slotA = static_cast<int>(st.inputs.size() - 1);
                 }
                 return slotA;
             }
             if (o.kind == K::ElemB) {
                 if (slotB < 0) {
-                    st.inputs.push_back(ref(c.bufferB));
+                    st.inputs.push_back(ref(bufB));
                     slotB = static_cast<int>(st.inputs.size() - 1);
                 }
                 return slotB;
             }
             return -1;  // ElemIdx is a multi-dim operand
         };
-        const Dtype od = km.buffers[so.bufferOut].dtype;
+        const Dtype od = km.buffers[bufOut].dtype;
         // Split-precision sin for f32 outputs only, as in the n-D path.
         auto bits = [&](const KernelOperand& o) {
-            return o.kind == K::ElemA ? streamBits(km, c.bufferA == kInvalidId ? -1 : static_cast<int64_t>(c.bufferA))
-                                      : (o.kind == K::ElemB ? streamBits(km, c.bufferB == kInvalidId ? -1 : static_cast<int64_t>(c.bufferB)) : 99);
+            return o.kind == K::ElemA ? streamBits(km, bufA == kInvalidId ? -1 : static_cast<int64_t>(bufA))
+                                      : (o.kind == K::ElemB ? streamBits(km, bufB == kInvalidId ? -1 : static_cast<int64_t>(bufB)) : 99);
         };
         auto exact = chainCode(exprs, c.family == "poly7", false, streamCode(streamOf), "return ", bits);
         if (!exact.has_value()) return err(exact.error().code, exact.error().message);
         // In place: exact forms throughout, as in the n-D path (the fast
         // forms' exact pass would re-read stored results).
         bool inPlace = false;
-        for (const StreamRef& s : st.inputs) inPlace = inPlace || s.buffer == so.bufferOut;
+        for (const StreamRef& s : st.inputs) inPlace = inPlace || s.buffer == bufOut;
         auto body = inPlace ? exact
                             : chainCode(exprs, c.family == "poly7", od == Dtype::F32, streamCode(streamOf), "return ", bits);
         if (!body.has_value()) return err(body.error().code, body.error().message);
         st.chainBody = *body;
         if (*exact != *body) st.chainExact = *exact;
-        st.out = ref(so.bufferOut);
+        st.out = ref(bufOut);
         if (!st.dynamicExtent) {
             if (st.extent[0] == 0) continue;
             if (begin < 0) return err(ErrorCode::InvalidGraph, "1-D loop begins below element 0");
@@ -558,6 +586,25 @@ Result<std::vector<Step>> tier1Loop(const KernelModule& km, const KernelNode& lo
 
 Result<Step> callStep(const KernelModule& km, const KernelNode& top, bool walker) {
     Step st;
+    if (!walker) {
+        // The Tier-1 call executors take their data through the same
+        // position-based lookup as the 1-D path (kernel_buffers.cpp
+        // resolveInput / resolveOutput) and their shapes from the ids'
+        // buffers. A lookup that finds no binding is the reference's
+        // InvalidArgument; one that lands on another buffer than the id is
+        // refused rather than run on mismatched shapes.
+        const bool mm = top.math == MathOp::MatMul;
+        const uint32_t ids[3] = {top.bufferA, mm ? top.bufferB : kInvalidId, top.bufferOut};
+        for (int i = 0; i < 3; ++i) {
+            if (ids[i] == kInvalidId || ids[i] >= km.buffers.size()) continue;   // checked below
+            const uint32_t r = resolve1d(km, ids[i], i == 2);
+            if (r == kInvalidId) return err(ErrorCode::InvalidArgument, "call buffers not bound by the caller");
+            if (r != ids[i]) {
+                return err(ErrorCode::UnsupportedCapability,
+                           "call buffer resolves by position to another buffer than its id");
+            }
+        }
+    }
     if (top.math == MathOp::MatMul) {
         if (top.bufferA >= km.buffers.size() || top.bufferB >= km.buffers.size() ||
             top.bufferOut >= km.buffers.size()) {

@@ -362,3 +362,41 @@ def test_host_abi_calls_from_two_threads(hip):
     for t in range(2):
         assert np.array_equal(got[t], xs[t].astype(np.float32).astype(np.float64) * 2.0)
     say("host abi from two threads: both results exact")
+
+
+def test_1d_roots_resolve_buffers_by_position(hip):
+    # The 1-D executor path indexes its bindings (the inputs, then the
+    # outputs) by buffer id (kernel_buffers.cpp resolveInput/resolveOutput).
+    # With a temp between the input and the output, a store to the temp (not
+    # an output) and a store to y (output 1 of 1) both resolve to no binding,
+    # so neither root runs and y stays as given. With the output right after
+    # the input, x -> y and y -> y run, and a root reading the temp after
+    # them (output 1 of 1 again) is skipped.
+    from mlk2_amd.kernel_ir import KernelModule, KernelBuffer, KernelNode, KernelExpr, const, elem_a
+
+    def module(order, roots):
+        km = KernelModule()
+        ids = {}
+        for name in order:
+            kind = {"x": dict(is_input=True), "t": dict(is_temp=True), "y": dict(is_output=True)}[name]
+            ids[name] = km.add_buffer(KernelBuffer(name=name, dtype="f32", elements=4096, dims=[4096], **kind))
+        for src, dst, op, c in roots:
+            cid = km.add_node(KernelNode(op="compute", math=op, exprs=[KernelExpr(op, elem_a(), const(c))],
+                                         a=ids[src], b=0xFFFFFFFF))
+            sid = km.add_node(KernelNode(op="store", out=ids[dst]))
+            km.add_node(KernelNode(op="loop", var="i", begin=0, end=4096, children=[cid, sid]))
+        return km, ids
+
+    x = inputs.uniform(6, 4096, -4.0, 4.0)
+    y0 = inputs.uniform(7, 4096, -1.0, 1.0)
+    cases = [(("x", "t", "y"), (("x", "t", "mul", 2.0), ("t", "y", "add", 1.0)), False),
+             (("x", "y", "t"), (("x", "y", "mul", 2.0), ("y", "y", "add", 1.0), ("t", "y", "mul", 5.0)), True)]
+    for order, roots, runs in cases:
+        km, ids = module(order, roots)
+        got = hip.build(km).run({ids["x"]: x, ids["y"]: y0})[ids["y"]].astype(np.float32)
+        ref = oracle.run(km, {ids["x"]: x}, init={ids["y"]: y0})[ids["y"]].astype(np.float32)
+        assert np.array_equal(got, ref), order
+        want = (x.astype(np.float32).astype(np.float64) * 2.0 + 1.0).astype(np.float32) if runs else \
+            y0.astype(np.float32)
+        assert np.array_equal(got, want), order
+        say(f"1-D position resolution {order}: same as the executor")

@@ -326,7 +326,9 @@ def test_split_precision_sine_only_for_f32_outputs(lift):
 
 
 def in_place(km):
-    """The chain's store pointed back at its first input: y is x."""
+    """The chain's store pointed back at its first input: y is x. The input
+    stays an input only, so the reference's executor, which looks buffers up
+    by position (kernel_buffers.cpp resolveOutput), writes through it."""
     root = km.nodes[km.roots()[0]]
     while True:
         kids = [km.nodes[c] for c in root.children]
@@ -335,7 +337,6 @@ def in_place(km):
             break
         root = kids[0]
     src = 0
-    km.buffers[src].is_output = True
     store.out = src
     return km
 
@@ -362,3 +363,44 @@ def test_in_place_chains_plan_the_exact_forms(name, make, lift):
     fast, exact = chain_bodies(in_place(km))
     assert exact == "", fast
     assert "f32acc" not in fast and "f32out" not in fast and "slow" not in fast.replace("(void)slow", "")
+
+
+def _roots_module(order, roots):
+    km = KernelModule()
+    ids = {}
+    for name in order:
+        kind = {"x": dict(is_input=True), "t": dict(is_temp=True), "y": dict(is_output=True)}[name]
+        ids[name] = km.add_buffer(KernelBuffer(name=name, dtype="f32", elements=64, dims=[64], **kind))
+    for src, dst in roots:
+        cid = km.add_node(KernelNode(op="compute", math="mul", exprs=[KernelExpr("mul", elem_a(), const(2.0))],
+                                     a=ids[src], b=INVALID_ID))
+        sid = km.add_node(KernelNode(op="store", out=ids[dst]))
+        km.add_node(KernelNode(op="loop", var="i", begin=0, end=64, children=[cid, sid]))
+    return km
+
+
+def test_1d_path_resolves_buffers_by_position():
+    # kernel_buffers.cpp resolveInput/resolveOutput: the 1-D executor looks
+    # an input up as inputs[id], anything else it reads as outputs[id -
+    # #inputs], an output it stores as outputs[id - #inputs], anything else
+    # as inputs[id]. A temp between x and y leaves both roots without a
+    # binding (the reference skips them); with y right after x both run.
+    assert be.plan(_roots_module(("x", "t", "y"), (("x", "t"), ("t", "y"))))[2] == 0
+    assert be.plan(_roots_module(("x", "y", "t"), (("x", "y"), ("y", "y"))))[2] == 2
+    # A store into the input writes through the caller's array: it runs.
+    assert be.plan(_roots_module(("x", "y"), (("x", "x"),)))[2] == 1
+
+
+def test_call_buffers_resolved_by_position():
+    # The Tier-1 call executors use the same lookup for their data: a
+    # binding it cannot find is the reference's InvalidArgument; one that
+    # lands on another buffer than the id is refused, not run on mismatched
+    # shapes.
+    km = KernelModule()
+    a = km.add_buffer(KernelBuffer("A", "f32", is_input=True, elements=8 * 4, dims=[8, 4]))
+    km.add_buffer(KernelBuffer("T", "f32", is_temp=True, elements=8, dims=[8]))   # between A and Y
+    y = km.add_buffer(KernelBuffer("Y", "f32", is_output=True, elements=8 * 4, dims=[8, 4]))
+    km.add_node(KernelNode(op="call", math="softmax", a=a, b=INVALID_ID, out=y))
+    with pytest.raises(be.MlkHipError) as ei:
+        be.plan(km)
+    assert "not bound" in ei.value.message
