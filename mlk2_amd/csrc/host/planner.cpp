@@ -473,6 +473,65 @@ uint32_t resolve1d(const KernelModule& km, uint32_t bid, bool store) {
     return bid < ins.size() ? ins[bid] : kInvalidId;
 }
 
+/// The multi-dim walker reaches every non-temp buffer through the same
+/// position lookup (kernel_buffers.cpp elemPtr :85-103, the store target in
+/// execPair :730-737, the call executors :784-812 and their softmax /
+/// reducesum twins), and temps by id. The multi-dim steps bind buffers by
+/// id; for the tables the lowering emits (inputs, then outputs, then temps,
+/// each in id order) the two agree. A module where a lookup lands on another
+/// buffer than its id, or where an operand finds no binding (the walker
+/// would read zeros), is declined. A store or call target that finds no
+/// binding is the walker's InvalidArgument, raised here at plan time.
+Result<void> walkerPositions(const KernelModule& km) {
+    // One entry per lookup the walker makes: buffer id, store role, temps by
+    // id, and the error an unbound lookup raises (nullptr: the walker reads
+    // zeros instead).
+    struct Lookup {
+        uint32_t bid;
+        bool store, tempById;
+        const char* unbound;
+    };
+    std::vector<Lookup> looks;
+    for (const KernelNode& n : km.nodes) {
+        if (n.op == KernelOp::Store) {
+            looks.push_back({n.bufferOut, true, true, "walker: output buffer not bound"});
+        } else if (n.op == KernelOp::Call &&
+                   (n.math == MathOp::MatMul || n.math == MathOp::Softmax || n.math == MathOp::ReduceSum)) {
+            const char* msg = n.math == MathOp::MatMul    ? "matmul buffers not bound by the caller"
+                              : n.math == MathOp::Softmax ? "softmax buffers not bound by the caller"
+                                                          : "reducesum buffers not bound by the caller";
+            looks.push_back({n.bufferA, false, false, msg});
+            if (n.math == MathOp::MatMul) looks.push_back({n.bufferB, false, false, msg});
+            looks.push_back({n.bufferOut, true, false, msg});
+        } else if (n.op == KernelOp::Compute) {
+            for (const KernelExpr& e : n.exprs) {
+                for (const KernelOperand* o : {&e.a, &e.b}) {
+                    if (o->kind == K::ElemIdx && o->index >= 0) {
+                        looks.push_back({static_cast<uint32_t>(o->index), false, true, nullptr});
+                    }
+                }
+            }
+        }
+    }
+    auto resolved = [&km](const Lookup& l) {
+        if (l.bid >= km.buffers.size()) return l.bid;  // range errors come from the step builders
+        if (l.tempById && km.buffers[l.bid].isTemp) return l.bid;
+        return resolve1d(km, l.bid, l.store);
+    };
+    // Errors before declines: an unbound target ends the walker's run
+    // whatever the other roots would have read.
+    for (const Lookup& l : looks) {
+        if (l.unbound != nullptr && resolved(l) == kInvalidId) return err(ErrorCode::InvalidArgument, l.unbound);
+    }
+    for (const Lookup& l : looks) {
+        if (resolved(l) != l.bid) {
+            return err(ErrorCode::UnsupportedCapability,
+                       "buffer '" + km.buffers[l.bid].name + "' resolves by position to another binding than its id");
+        }
+    }
+    return {};
+}
+
 Result<std::vector<Step>> tier1Loop(const KernelModule& km, const KernelNode& loop) {
     std::vector<Step> out;
     const KernelNode* store = nullptr;
@@ -1224,6 +1283,7 @@ Result<Plan> planModule(const KernelModule& input) {
             }
         }
     } else {
+        MLK_TRYV(walkerPositions(input));
         const std::vector<uint32_t> roots = forestRoots(km);
         for (size_t i = 0; i < roots.size(); ++i) {
             const KernelNode& r = km.nodes[roots[i]];

@@ -14,9 +14,10 @@ from mlk2_amd import backend as be
 from mlk2_amd import fixtures as fx
 import test_nest as tn
 import numpy as np
+import oracle
 
 from mlk2_amd.kernel_ir import (INVALID_ID, KernelBuffer, KernelExpr, KernelModule, KernelNode, const,
-                                elem_a, elem_b, temp)
+                                elem_a, elem_b, elem_idx, temp)
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
@@ -404,3 +405,42 @@ def test_call_buffers_resolved_by_position():
     with pytest.raises(be.MlkHipError) as ei:
         be.plan(km)
     assert "not bound" in ei.value.message
+
+
+def _nd_module(order, dst, reads=("x",)):
+    # y[i] = sum of the read buffers at i, over a multi-dim (elem_idx) nest.
+    km = KernelModule()
+    ids = {}
+    for name in order:
+        kind = {"x": dict(is_input=True), "t": dict(is_temp=True)}.get(name, dict(is_output=True))
+        ids[name] = km.add_buffer(KernelBuffer(name=name, dtype="f32", elements=64, dims=[64], **kind))
+    ops = [elem_idx(ids[r], [1]) for r in reads] + [const(0.0)] * (2 - len(reads))
+    cid = km.add_node(KernelNode(op="compute", exprs=[KernelExpr("add", ops[0], ops[1])]))
+    sid = km.add_node(KernelNode(op="store", out=ids[dst], out_index_coeffs=[1]))
+    km.add_node(KernelNode(op="loop", var="i", begin=0, end=64, children=[cid, sid]))
+    return km
+
+
+def test_multi_dim_path_checks_buffer_positions():
+    # The walker looks non-temp buffers up by position as the 1-D executor
+    # does (kernel_buffers.cpp elemPtr :85-103, execPair :730-737) and temps
+    # by id. The lowering's tables (inputs, outputs, temps) resolve to the
+    # ids themselves and plan as usual.
+    assert be.plan(_nd_module(("x", "y", "t"), "y"))[2] == 1
+    assert be.plan(_nd_module(("x", "y", "t"), "t"))[2] == 1
+    # A temp between x and y leaves y's store without a binding: the
+    # walker's InvalidArgument.
+    for order, dst in ((("x", "t", "y"), "y"), (("x", "t", "y", "z"), "z")):
+        km = _nd_module(order, dst)
+        with pytest.raises(be.MlkHipError) as ei:
+            be.plan(km)
+        assert "walker: output buffer not bound" in ei.value.message
+        with pytest.raises(RuntimeError, match="walker: output buffer not bound"):
+            oracle.run(km, {0: np.zeros(64)})
+    # With a second output after it, y's position reaches z's binding: the
+    # module is declined rather than run on the wrong array.
+    with pytest.raises(be.MlkHipError) as ei:
+        be.plan(_nd_module(("x", "t", "y", "z"), "y"))
+    assert "resolves by position" in ei.value.message
+    # Stores into temps go by id wherever the temp sits.
+    assert be.plan(_nd_module(("x", "t", "y"), "t"))[2] == 1
