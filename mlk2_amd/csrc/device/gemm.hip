@@ -1488,29 +1488,34 @@ __global__ __launch_bounds__(256) void gemmF32Mfma(const float* __restrict__ A,
 
 /// f32 form 0: both 64x64 tiles move global -> LDS by the direct path
 /// (global_load_lds_dwordx4, no register staging and no LDS writes) into a
-/// 4-deep ring of K steps of 64 (32 KiB per stage). 4 waves (2 x 2) each own
-/// a 32x32 tile on v_mfma_f32_32x32x2_f32, with the k order permuted within
-/// a step: MFMA t takes k = t from lanes 0-31 and k = 32 + t from lanes
-/// 32-63, so the A operand of 4 consecutive MFMAs is one 16-byte read of a
-/// row of A (16-byte chunk c of row m sits at c ^ (m & 15): the 16 rows a
-/// quarter-wave reads hit 16 distinct slots), and the B operand is a 4-byte
-/// read of 32 consecutive columns. One barrier per K step; every step issues
-/// exactly one stage (past the end a harmless reload into a slot nothing
-/// reads), so the wait before the barrier is a constant vmcnt. Needs K a
-/// multiple of 64. Each output's sum runs over k in a different order from
-/// form 1's k ascending, within the f32 tolerance.
+/// 4-deep ring of K steps of 64 (32 KiB per stage). 8 waves: waves q and
+/// q + 4 own the same 32x32 tile (2 x 2 quadrants) on v_mfma_f32_32x32x2_f32
+/// and take the two halves of every K step, so each SIMD runs two
+/// independent accumulator chains. Within a step the k order is permuted:
+/// MFMA t takes k = t from lanes 0-31 and k = 32 + t from lanes 32-63; wave
+/// half h takes t = 16h .. 16h + 15. The A operand of 4 consecutive MFMAs is
+/// then one 16-byte read of a row of A (16-byte chunk c of row m sits at
+/// c ^ (m & 15): the 16 rows a quarter-wave reads hit 16 distinct slots),
+/// and the B operand a 4-byte read of 32 consecutive columns. One barrier
+/// per K step; every step issues exactly one stage (past the end a harmless
+/// reload into a slot nothing reads), so the wait before the barrier is a
+/// constant vmcnt. At the end the second half's sums reach the first half's
+/// waves through LDS and each output is half 0 + half 1, in that order.
+/// Needs K a multiple of 64. Each output's sum runs over k in a different
+/// order from form 1's k ascending, within the f32 tolerance.
 constexpr int kQK = 64, kQStages = 4;
 constexpr int kQA = kFM * kQK;                        // floats per A stage (64 rows x 64 k)
 constexpr int kQStage = 2 * kQA;                      // A, then B (64 k x 64 n)
 constexpr size_t kLdsF32Dma = static_cast<size_t>(kQStages) * kQStage * sizeof(float);   // 128 KiB
 
 template <bool ACC>
-__global__ __launch_bounds__(256, 1) void gemmF32Dma(const float* __restrict__ A, const float* __restrict__ B,
+__global__ __launch_bounds__(512, 1) void gemmF32Dma(const float* __restrict__ A, const float* __restrict__ B,
                                                      float* __restrict__ C, int N, int K, int64_t lda,
                                                      int64_t ldb, int64_t ldc, int skipZeroA) {
     extern __shared__ __align__(16) float ldsF[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int quad = wave & 3, h = wave >> 2;   // output quadrant, K-step half
+    const int wm = quad >> 1, wn = quad & 1;
     const int tilesN = N / kFN;
     // XCD-blocked map: at 1024^2 each XCD's 32 tiles form a 4 x 8 block, so
     // its L2 holds 4 A and 8 B panels (3 MiB) instead of 16 A panels; the
@@ -1523,21 +1528,21 @@ __global__ __launch_bounds__(256, 1) void gemmF32Dma(const float* __restrict__ A
     // Stage `slot` receives K step min(slot, steps - 1) in ring slot
     // slot % kQStages. A is 64 rows of 256 bytes and B 64 k-rows of 256
     // bytes, 16 direct loads of 4 rows each: wave w issues instructions
-    // 4w .. 4w + 3 of each.
+    // 2w and 2w + 1 of each.
     auto issue = [&](int slot) {
         const int k0 = min(slot, steps - 1) * kQK;
         const float* st = ldsF + (slot % kQStages) * kQStage;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int ins = wave * 4 + j;
+        for (int j = 0; j < 2; ++j) {
+            const int ins = wave * 2 + j;
             const int row = ins * 4 + (lane >> 4);
             const int c = (lane & 15) ^ (row & 15);
             dmaLoad16(reinterpret_cast<const _Float16*>(A + (row0 + row) * lda + k0 + c * 4),
                       reinterpret_cast<const _Float16*>(st + ins * 256));
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int ins = wave * 4 + j;
+        for (int j = 0; j < 2; ++j) {
+            const int ins = wave * 2 + j;
             const int krow = ins * 4 + (lane >> 4);
             dmaLoad16(reinterpret_cast<const _Float16*>(B + static_cast<int64_t>(k0 + krow) * ldb + col0 +
                                                         (lane & 15) * 4),
@@ -1551,40 +1556,52 @@ __global__ __launch_bounds__(256, 1) void gemmF32Dma(const float* __restrict__ A
     for (int s = 0; s < kQStages - 1; ++s) issue(s);
     const int l32 = lane & 31, hl = lane >> 5;
     const int m = wm * 32 + l32;
-    // A: row m, chunks 8 hl .. 8 hl + 7 (k 32 hl .. + 31) at their slots.
-    uint32_t offA[8];
+    // A: row m, chunks 8 hl + 4 h .. + 3 (k 32 hl + 16 h .. + 15) at their
+    // slots.
+    uint32_t offA[4];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) offA[q] = 4u * static_cast<uint32_t>(m * kQK + (((8 * hl + q) ^ (m & 15)) * 4));
-    // B: k-row 32 hl + t, column wn * 32 + l32.
-    const uint32_t offB = 4u * static_cast<uint32_t>(kQA + 32 * hl * kFN + wn * 32 + l32);
+    for (int i = 0; i < 4; ++i) {
+        const int q = 4 * h + i;
+        offA[i] = 4u * static_cast<uint32_t>(m * kQK + (((8 * hl + q) ^ (m & 15)) * 4));
+    }
+    // B: k-row 32 hl + 16 h + t, column wn * 32 + l32.
+    const uint32_t offB = 4u * static_cast<uint32_t>(kQA + (32 * hl + 16 * h) * kFN + wn * 32 + l32);
     const uint32_t ldsBase = ldsOffset(ldsF);
-    // Stage 0 landed (stages 1 and 2, 8 direct loads each per wave, may be
+    // Stage 0 landed (stages 1 and 2, 4 direct loads each per wave, may be
     // in flight).
-    asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
     asm volatile("s_barrier" ::: "memory");
     for (int s = 0; s < steps; ++s) {
         const uint32_t cb = ldsBase + 4u * static_cast<uint32_t>((s % kQStages) * kQStage);
-        f32x4 a[8];
-        float b[32];
+        f32x4 a[4];
+        float b[16];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            a[q] = *reinterpret_cast<const __attribute__((address_space(3))) f32x4*>(cb + offA[q]);
-        }
+        for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const __attribute__((address_space(3))) f32x4*>(cb + offA[i]);
 #pragma unroll
-        for (int t = 0; t < 32; ++t) {
+        for (int t = 0; t < 16; ++t) {
             b[t] = *reinterpret_cast<const __attribute__((address_space(3))) float*>(cb + offB + 4u * kFN * t);
         }
 #pragma unroll
-        for (int t = 0; t < 32; ++t) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t >> 2][t & 3], b[t], acc, 0, 0, 0);
+        for (int t = 0; t < 16; ++t) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t >> 2][t & 3], b[t], acc, 0, 0, 0);
         // Stage s + 1 landed (one later stage may be in flight); after the
         // barrier every wave is past step s, so slot (s + 3) % 4, which held
         // step s - 1, can be refilled.
-        asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
         asm volatile("s_barrier" ::: "memory");
         issue(s + kQStages - 1);
     }
-    // No direct load may still be writing LDS when the workgroup ends.
+    // No direct load may still be writing LDS when the halves meet there.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    float* red = ldsF + quad * (64 * 16);
+    if (h == 1) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) red[r * 64 + lane] = acc[r];
+    }
+    __syncthreads();
+    if (h == 1) return;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] += red[r * 64 + lane];
     if (ACC && skipZeroA && waveNonFinite(acc)) {
         exactWaveBlock<float, float>(A, B, C, lda, ldb, ldc, K, row0 + wm * 32, col0 + wn * 32, 32, 32, ACC);
         return;
@@ -1817,7 +1834,7 @@ int launchMfma(const mlkd_gemm* p, int form, hipStream_t st) {
             const float* a32 = static_cast<const float*>(p->a);
             const float* b32 = static_cast<const float*>(p->b);
             if (form == 100) {
-                hipLaunchKernelGGL((acc ? gemmF32Dma<true> : gemmF32Dma<false>), dim3(ftiles), dim3(256), kLdsF32Dma,
+                hipLaunchKernelGGL((acc ? gemmF32Dma<true> : gemmF32Dma<false>), dim3(ftiles), dim3(512), kLdsF32Dma,
                                    st, a32, b32, c, n, k, p->lda, p->ldb, p->ldc, skip);
             } else {
                 hipLaunchKernelGGL((acc ? gemmF32Mfma<true> : gemmF32Mfma<false>), dim3(ftiles), dim3(256), 0, st,
