@@ -52,16 +52,21 @@ def build(src: str) -> str:
     exe = os.path.join(CACHE, f"nest_{h}")
     if os.path.exists(exe):
         return exe
-    path = os.path.join(CACHE, f"nest_{h}.hip.inc")
+    # Per-process file names, then an atomic rename: test workers running in
+    # parallel may build the same kernel at once.
+    tag = f"{os.getpid()}"
+    path = os.path.join(CACHE, f"nest_{h}.{tag}.hip.inc")
     with open(path, "w") as f:
         f.write(src)
+    tmp = f"{exe}.{tag}.tmp"
     cmd = [CLANG, "-std=c++17", "-O1", "-g", "-fno-omit-frame-pointer", "-ffp-contract=off",
            "-fsanitize=address,undefined", "-fno-sanitize-recover=undefined",
-           "-include", SHIM, f'-DMLK_NEST_SRC="{path}"', HARNESS, "-o", exe + ".tmp"]
+           "-include", SHIM, f'-DMLK_NEST_SRC="{path}"', HARNESS, "-o", tmp]
     r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    os.remove(path)
     if r.returncode != 0:
         raise RuntimeError("host build of the nest kernel failed:\n" + r.stdout[-4000:])
-    os.replace(exe + ".tmp", exe)
+    os.replace(tmp, exe)
     return exe
 
 
