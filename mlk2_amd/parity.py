@@ -5,7 +5,11 @@
 * ``ulp_distance_f32`` is the same over f32 bit patterns: the GPU value
   against the f64 reference rounded to f32.
 * ``max_rel`` restates ``bench/math/math_bench.cpp:172-181``:
-  ``|got - ref| / max(|ref|, 1)``.
+  ``|got - ref| / max(|ref|, 1)``. There a NaN error never raises the
+  maximum, so equal infinities (inf - inf) count as no error; they do here
+  too. A NaN on one side only is also skipped there; here it counts as an
+  infinite error, so a gate cannot pass over a NaN the reference does not
+  produce.
 * ``bit_exact`` restates the Rule-43 element gate
   (``tools/mlk-poly/poly_bench.cpp:211-224``): no element differs under
   ``!=``, so a NaN never matches, not even a NaN.
@@ -57,9 +61,10 @@ def max_rel(got: np.ndarray, ref: np.ndarray) -> float:
     if g.size == 0:
         return 0.0
     denom = np.maximum(np.abs(r), 1.0)
-    e = np.abs(g - r) / denom
+    with np.errstate(invalid="ignore"):
+        e = np.abs(g - r) / denom
     both_nan = np.isnan(g) & np.isnan(r)
-    e = np.where(both_nan, 0.0, e)
+    e = np.where(both_nan | (g == r), 0.0, e)
     e = np.where(np.isnan(e), np.inf, e)
     return float(e.max())
 

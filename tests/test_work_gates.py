@@ -12,7 +12,7 @@ import numpy as np
 from mlk2_amd import backend as be
 from mlk2_amd import fixtures as fx
 from mlk2_amd.kernel_ir import KernelExpr, const, elem_a
-from mlk2_amd.parity import bit_exact, policy_gate, ulp_distance_f32, ulp_distance_f64
+from mlk2_amd.parity import bit_exact, max_rel, policy_gate, ulp_distance_f32, ulp_distance_f64
 
 
 # ---- work model (fastkernel essentialWorkModel / rooflineLowerBound) ----
@@ -75,6 +75,20 @@ def test_bit_exact_nan_never_matches():
     assert bit_exact(np.array([1.0, -0.0]), np.array([1.0, 0.0])) == (True, -1)
     assert bit_exact(np.array([1.0, np.nan]), np.array([1.0, np.nan])) == (False, 1)
     assert bit_exact(np.array([1.0, 2.0]), np.array([1.0, np.nextafter(2.0, 3.0)])) == (False, 1)
+
+
+def test_max_rel_special_values():
+    # math_bench.cpp:172-181: |got - ref| / max(|ref|, 1), where a NaN error
+    # (inf - inf, or a NaN operand) never raises the maximum.
+    inf, nan = np.inf, np.nan
+    assert max_rel(np.array([3.0, -0.5]), np.array([2.0, -0.25])) == 0.5     # 1/2 and 0.25/1
+    assert max_rel(np.array([inf, -inf, 1.0]), np.array([inf, -inf, 1.0])) == 0.0   # equal infinities
+    assert max_rel(np.array([nan, 1.0]), np.array([nan, 1.0])) == 0.0
+    assert max_rel(np.array([inf]), np.array([-inf])) == inf
+    assert max_rel(np.array([inf]), np.array([1e300])) == inf
+    # Stricter than the reference: a NaN on one side only fails.
+    assert max_rel(np.array([nan]), np.array([1.0])) == inf
+    assert max_rel(np.array([1.0]), np.array([nan])) == inf
 
 
 def test_policy_gates():
