@@ -143,7 +143,8 @@ int mlkhip_bindable_info(const mlkhip_artifact* a, int i, int32_t* dtype, int64_
  * module dtypes (RNE) on upload, back to f64 on download; outputs are
  * uploaded too, since += and max stores read them. Synchronous. The copies
  * go through up to 64 MiB of page-locked staging that the artifact keeps
- * until it is released; host-buffer calls on one artifact run one at a
+ * until it is released, in two halves so that converting one chunk overlaps
+ * copying the previous one; host-buffer calls on one artifact run one at a
  * time. */
 int mlkhip_kernel(const mlkhip_artifact* a, double* const* ptrs, const int64_t* const* dims,
                   int n_bindables, const double* scalars, int64_t n_scalars, int64_t elements);

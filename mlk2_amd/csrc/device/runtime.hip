@@ -173,6 +173,10 @@ int mlkd_rt_event_record(void* e, void* stream) {
                   MLKD_RT_LAUNCH);
 }
 
+int mlkd_rt_event_sync(void* e) {
+    return mapErr(hipEventSynchronize(static_cast<hipEvent_t>(e)), MLKD_RT_LAUNCH);
+}
+
 int mlkd_rt_event_elapsed_ms(void* start, void* stop, float* ms) {
     if (hipEventSynchronize(static_cast<hipEvent_t>(stop)) != hipSuccess) return MLKD_RT_LAUNCH;
     return mapErr(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start),

@@ -46,6 +46,8 @@ int mlkd_rt_stream_destroy(void* s);
 int mlkd_rt_event_create(void** e);
 int mlkd_rt_event_destroy(void* e);
 int mlkd_rt_event_record(void* e, void* stream);
+/* Waits on the host until the work before the event's record has finished. */
+int mlkd_rt_event_sync(void* e);
 int mlkd_rt_event_elapsed_ms(void* start, void* stop, float* ms);
 const char* mlkd_rt_last_error(void);
 

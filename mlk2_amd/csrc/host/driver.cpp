@@ -238,6 +238,8 @@ HipLoadedKernel::~HipLoadedKernel() {
         (void)stream;
         freeScratch(*rs);
     }
+    mlkd_rt_event_destroy(hostEvent_[0]);
+    mlkd_rt_event_destroy(hostEvent_[1]);
     mlkd_rt_host_free(hostStage_);
 }
 
@@ -660,9 +662,11 @@ int HipLoadedKernel::runHost(double* const* ptrs, int n, const double* scalars, 
         const int64_t cnt = bufferElements(kb, elements);
         if (!kb.isTemp && cnt > 0) maxBytes = std::max(maxBytes, static_cast<size_t>(cnt) * dtypeBytes(kb.dtype));
     }
-    if (const size_t want = std::min(maxBytes, kHostStageBytes); want > hostStageBytes_) {
-        // Grown to the largest buffer seen, up to 64 MiB; without page-locked
-        // memory the copies go through an ordinary heap buffer instead.
+    // Two halves, each holding the largest buffer seen (rounded up to 256
+    // bytes, so a half always holds an element), up to 32 MiB each; without
+    // page-locked memory the copies go through an ordinary heap buffer.
+    const size_t twoHalves = 2 * ((maxBytes + 255) & ~size_t{255});
+    if (const size_t want = std::min(twoHalves, kHostStageBytes); want > hostStageBytes_) {
         void* p = nullptr;
         if (mlkd_rt_host_alloc(&p, want) == 0) {
             mlkd_rt_host_free(hostStage_);
@@ -670,32 +674,47 @@ int HipLoadedKernel::runHost(double* const* ptrs, int n, const double* scalars, 
             hostStageBytes_ = want;
         }
     }
-    // Caller's f64s -> `dt` on the device, chunk by chunk through the staging.
+    if (hostStage_ != nullptr && hostEvent_[0] == nullptr) {
+        if (mlkd_rt_event_create(&hostEvent_[0]) != 0 || mlkd_rt_event_create(&hostEvent_[1]) != 0) {
+            mlkd_rt_event_destroy(hostEvent_[0]);
+            hostEvent_[0] = hostEvent_[1] = nullptr;
+        }
+    }
+    // Two halves of the staging: chunk i goes through half i % 2, and an
+    // event recorded after its copy tells when that half is free again.
+    const bool piped = hostStage_ != nullptr && hostEvent_[0] != nullptr;
+    const size_t half = hostStageBytes_ / 2;
+    auto halfPtr = [&](int64_t i) { return static_cast<unsigned char*>(hostStage_) + (i & 1) * half; };
+    // Caller's f64s -> `dt` on the device, chunk by chunk through the
+    // staging; converting chunk i overlaps the copy of chunk i - 1.
     auto copyIn = [&](void* d, const double* src, int64_t cnt, Dtype dt) -> bool {
         const size_t es = dtypeBytes(dt);
-        if (hostStage_ == nullptr) {
+        if (!piped) {
             std::unique_ptr<unsigned char[]> heap(new (std::nothrow) unsigned char[static_cast<size_t>(cnt) * es]);
             if (!heap) return false;
             narrowTo(heap.get(), src, cnt, dt);
             return mlkd_rt_h2d(d, heap.get(), static_cast<size_t>(cnt) * es, nullptr) == 0 &&
                    mlkd_rt_sync(nullptr) == 0;
         }
-        const int64_t per = static_cast<int64_t>(hostStageBytes_ / es);
-        for (int64_t c0 = 0; c0 < cnt; c0 += per) {
+        const int64_t per = static_cast<int64_t>(half / es);
+        int64_t i = 0;
+        for (int64_t c0 = 0; c0 < cnt; c0 += per, ++i) {
             const int64_t m = std::min(per, cnt - c0);
-            narrowTo(hostStage_, src + c0, m, dt);
-            if (mlkd_rt_h2d(static_cast<char*>(d) + c0 * static_cast<int64_t>(es), hostStage_,
+            if (i >= 2 && mlkd_rt_event_sync(hostEvent_[i & 1]) != 0) return false;   // chunk i - 2 sent
+            narrowTo(halfPtr(i), src + c0, m, dt);
+            if (mlkd_rt_h2d(static_cast<char*>(d) + c0 * static_cast<int64_t>(es), halfPtr(i),
                             static_cast<size_t>(m) * es, nullptr) != 0 ||
-                mlkd_rt_sync(nullptr) != 0) {
+                mlkd_rt_event_record(hostEvent_[i & 1], nullptr) != 0) {
                 return false;
             }
         }
-        return true;
+        return mlkd_rt_sync(nullptr) == 0;
     };
-    // Device `dt` values -> the caller's f64s, the same way back.
+    // Device `dt` values -> the caller's f64s: chunk i + 1 is in flight
+    // while chunk i is widened.
     auto copyOut = [&](double* dst, const void* d, int64_t cnt, Dtype dt) -> bool {
         const size_t es = dtypeBytes(dt);
-        if (hostStage_ == nullptr) {
+        if (!piped) {
             std::unique_ptr<unsigned char[]> heap(new (std::nothrow) unsigned char[static_cast<size_t>(cnt) * es]);
             if (!heap) return false;
             if (mlkd_rt_d2h(heap.get(), d, static_cast<size_t>(cnt) * es, nullptr) != 0 || mlkd_rt_sync(nullptr) != 0) {
@@ -704,15 +723,21 @@ int HipLoadedKernel::runHost(double* const* ptrs, int n, const double* scalars, 
             widenFrom(dst, heap.get(), cnt, dt);
             return true;
         }
-        const int64_t per = static_cast<int64_t>(hostStageBytes_ / es);
-        for (int64_t c0 = 0; c0 < cnt; c0 += per) {
-            const int64_t m = std::min(per, cnt - c0);
-            if (mlkd_rt_d2h(hostStage_, static_cast<const char*>(d) + c0 * static_cast<int64_t>(es),
-                            static_cast<size_t>(m) * es, nullptr) != 0 ||
-                mlkd_rt_sync(nullptr) != 0) {
-                return false;
-            }
-            widenFrom(dst + c0, hostStage_, m, dt);
+        const int64_t per = static_cast<int64_t>(half / es);
+        const int64_t chunks = (cnt + per - 1) / per;
+        auto fetch = [&](int64_t i) {
+            const int64_t c0 = i * per, m = std::min(per, cnt - c0);
+            return mlkd_rt_d2h(halfPtr(i), static_cast<const char*>(d) + c0 * static_cast<int64_t>(es),
+                               static_cast<size_t>(m) * es, nullptr) == 0 &&
+                   mlkd_rt_event_record(hostEvent_[i & 1], nullptr) == 0;
+        };
+        if (chunks > 0 && !fetch(0)) return false;
+        for (int64_t i = 0; i < chunks; ++i) {
+            // Half (i + 1) % 2 last held chunk i - 1, widened in the previous pass.
+            if (i + 1 < chunks && !fetch(i + 1)) return false;
+            if (mlkd_rt_event_sync(hostEvent_[i & 1]) != 0) return false;
+            const int64_t c0 = i * per;
+            widenFrom(dst + c0, halfPtr(i), std::min(per, cnt - c0), dt);
         }
         return true;
     };

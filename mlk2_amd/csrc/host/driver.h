@@ -130,14 +130,16 @@ private:
     int ensureNestForm(size_t si, int form, void*& fn, std::string& why) const;
     mutable std::mutex scratchLock_;
     mutable std::vector<std::pair<void*, std::unique_ptr<RunScratch>>> scratchByStream_;
-    // Page-locked staging of the host-buffer run (runHost), at most 64 MiB:
-    // each buffer is converted into it and copied chunk by chunk. Allocated
-    // on the first host-buffer run and kept until the artifact is released.
+    // Page-locked staging of the host-buffer run (runHost), at most 64 MiB,
+    // used as two halves: each buffer is converted into one half while the
+    // other half's chunk is in flight over PCIe. Allocated on the first
+    // host-buffer run and kept until the artifact is released.
     // Host-buffer runs of one artifact hold hostLock_ for the whole call, so
     // they run one at a time.
     mutable std::mutex hostLock_;
     mutable void* hostStage_{nullptr};
     mutable size_t hostStageBytes_{0};
+    mutable void* hostEvent_[2]{nullptr, nullptr};   // one per staging half
     // Loop-nest launch forms 1-4 (no LDS slabs; 512 and 64 threads per
     // workgroup; one fewer collapsed loop), each compiled on first use; form
     // 0 is the step's own.
