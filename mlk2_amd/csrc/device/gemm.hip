@@ -860,10 +860,14 @@ __device__ __forceinline__ uint32_t ldsOffset(const void* p) {
 }
 
 /// 16 bytes per lane from `src` to LDS `dst` + 16 * lane; `dst` is the same
-/// for the whole wave and goes through M0.
+/// for the whole wave and goes through M0. M0 is a reserved register: naming
+/// it as a clobber only draws a warning that reserved registers are not
+/// preserved, so it is left out. The asm sets M0 itself right before the
+/// load, and in the kernels that use these loads every M0 write comes from
+/// these asm statements (the compiled code holds no other value in M0).
 __device__ __forceinline__ void dmaLoad16(const _Float16* src, const _Float16* dst) {
     const uint32_t m0 = __builtin_amdgcn_readfirstlane(ldsOffset(dst));
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory");
 }
 
 struct DmaFrag {
@@ -1188,11 +1192,7 @@ __global__ __launch_bounds__(512, 1) void gemmF16Dma8(const _Float16* __restrict
 /// Direct load through a scalar base: lane bytes `voff` past `sbase` into LDS
 /// at M0 + 16 * lane. The K advance lives in `sbase` (scalar adds), so the
 /// per-lane address costs no vector instruction per step.
-/// M0 is a reserved register: naming it as a clobber (as dmaLoad16 does)
-/// only draws a warning that reserved registers are not preserved, so it is
-/// left out here. The asm sets M0 itself right before the load, and in the
-/// kernels that use these loads every M0 write comes from these asm
-/// statements (the compiled code holds no other value in M0).
+/// M0 is handled as in dmaLoad16.
 __device__ __forceinline__ void dmaLoad16s(const void* sbase, uint32_t voff, uint32_t m0) {
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(m0) : "memory");
 }
