@@ -1859,11 +1859,190 @@ int launchMfma(const mlkd_gemm* p, int form, hipStream_t st) {
     return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
 }
 
+/// dst[r, c] = src[r * lds + c] for r < rows, c < cols, and 0 on the rest
+/// of the drows x dcols block (row-major, stride dcols). Element bits are
+/// copied as they are (T is a 16- or 32-bit integer type).
+template <typename T>
+__global__ __launch_bounds__(256) void padBlock(const T* __restrict__ src, int64_t rows, int64_t cols,
+                                                int64_t lds, T* __restrict__ dst, int64_t drows, int64_t dcols) {
+    for (int64_t r = blockIdx.y; r < drows; r += gridDim.y) {
+        for (int64_t c = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; c < dcols;
+             c += static_cast<int64_t>(gridDim.x) * 256) {
+            dst[r * dcols + c] = (r < rows && c < cols) ? src[r * lds + c] : T(0);
+        }
+    }
+}
+
+/// dst[r * ldd + c] = src[r * scols + c] for r < rows, c < cols.
+template <typename T>
+__global__ __launch_bounds__(256) void unpadBlock(const T* __restrict__ src, int64_t scols, T* __restrict__ dst,
+                                                  int64_t rows, int64_t cols, int64_t ldd) {
+    for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+        for (int64_t c = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; c < cols;
+             c += static_cast<int64_t>(gridDim.x) * 256) {
+            dst[r * ldd + c] = src[r * scols + c];
+        }
+    }
+}
+
+/// The zero-padded shape a GEMM the MFMA forms do not tile runs at: f16
+/// operands with an f32 C on 256 x 256 tiles, or all-f32 on 64 x 64 tiles,
+/// K rounded up to 64. Padding adds only products 0 * 0 to the sums (and
+/// the skip-zero-A test skips them), so each output keeps its value. Below
+/// 2^30 flop the copies cost more than the general kernel takes.
+struct PadShape {
+    int64_t m, n, k;
+    size_t es;   // operand element bytes
+};
+
+bool padShape(const mlkd_gemm* p, PadShape& ps) {
+    const bool f16 = p->a_dtype == MLKD_F16 && p->b_dtype == MLKD_F16 && p->c_dtype == MLKD_F32;
+    const bool f32 = p->a_dtype == MLKD_F32 && p->b_dtype == MLKD_F32 && p->c_dtype == MLKD_F32;
+    if (!(f16 || f32) || p->m <= 0 || p->n <= 0 || p->k <= 0) return false;
+    if (p->skip_zero_a != 0 && p->accumulate == 0) return false;   // that launch takes the general kernel
+    if (mfmaForm(p) >= 0) return false;                             // already tiled
+    if (2.0 * static_cast<double>(p->m) * static_cast<double>(p->n) * static_cast<double>(p->k) <
+        static_cast<double>(int64_t{1} << 30)) {
+        return false;
+    }
+    const int64_t tm = f16 ? kBM : kFM, tn = f16 ? kBN : kFN, tk = 64;
+    ps.m = (p->m + tm - 1) / tm * tm;
+    ps.n = (p->n + tn - 1) / tn * tn;
+    ps.k = (p->k + tk - 1) / tk * tk;
+    ps.es = f16 ? 2 : 4;
+    return ps.m < (int64_t{1} << 31) && ps.n < (int64_t{1} << 31) && ps.k < (int64_t{1} << 31);
+}
+
+size_t align256g(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
+
+size_t padBytes(const PadShape& ps) {
+    return align256g(static_cast<size_t>(ps.m * ps.k) * ps.es) + align256g(static_cast<size_t>(ps.k * ps.n) * ps.es) +
+           align256g(static_cast<size_t>(ps.m * ps.n) * sizeof(float));
+}
+
+/// The padded launch's MFMA parameters, with A', B', C' carved from the
+/// workspace; false when the workspace is missing or too small.
+bool paddedParams(const mlkd_gemm* p, mlkd_gemm& q, PadShape& ps) {
+    if (p->work == nullptr || !padShape(p, ps) || p->work_bytes < static_cast<int64_t>(padBytes(ps))) return false;
+    unsigned char* w = static_cast<unsigned char*>(p->work);
+    q = *p;
+    q.a = w;
+    q.b = w + align256g(static_cast<size_t>(ps.m * ps.k) * ps.es);
+    q.c = static_cast<unsigned char*>(const_cast<void*>(q.b)) + align256g(static_cast<size_t>(ps.k * ps.n) * ps.es);
+    q.m = ps.m;
+    q.n = ps.n;
+    q.k = ps.k;
+    q.lda = ps.k;
+    q.ldb = ps.n;
+    q.ldc = ps.n;
+    q.work = nullptr;
+    q.work_bytes = 0;
+    return mfmaForm(&q) >= 0;
+}
+
+/// padBlock in 16-byte pieces, for source rows that start 16-byte aligned
+/// (src and lds * sizeof(T) multiples of 16; dcols a multiple of 16 /
+/// sizeof(T)). A piece that straddles `cols` is copied element by element.
+template <typename T>
+__global__ __launch_bounds__(256) void padBlock16(const T* __restrict__ src, int64_t rows, int64_t cols,
+                                                  int64_t lds, T* __restrict__ dst, int64_t drows, int64_t dcols) {
+    constexpr int V = 16 / sizeof(T);
+    const int64_t pieces = dcols / V;
+    for (int64_t r = blockIdx.y; r < drows; r += gridDim.y) {
+        for (int64_t j = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; j < pieces;
+             j += static_cast<int64_t>(gridDim.x) * 256) {
+            const int64_t c0 = j * V;
+            u32x4 v = {0u, 0u, 0u, 0u};
+            if (r < rows && c0 + V <= cols) {
+                v = *reinterpret_cast<const u32x4*>(src + r * lds + c0);
+            } else if (r < rows && c0 < cols) {
+                T e[V];
+#pragma unroll
+                for (int i = 0; i < V; ++i) e[i] = c0 + i < cols ? src[r * lds + c0 + i] : T(0);
+                v = __builtin_bit_cast(u32x4, e);
+            }
+            *reinterpret_cast<u32x4*>(dst + r * dcols + c0) = v;
+        }
+    }
+}
+
+/// unpadBlock in 16-byte pieces (dst and ldd * 4 multiples of 16 bytes); a
+/// piece that straddles `cols` is copied element by element.
+__global__ __launch_bounds__(256) void unpadBlock16(const uint32_t* __restrict__ src, int64_t scols,
+                                                    uint32_t* __restrict__ dst, int64_t rows, int64_t cols,
+                                                    int64_t ldd) {
+    const int64_t pieces = (cols + 3) / 4;
+    for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+        for (int64_t j = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; j < pieces;
+             j += static_cast<int64_t>(gridDim.x) * 256) {
+            const int64_t c0 = j * 4;
+            if (c0 + 4 <= cols) {
+                *reinterpret_cast<u32x4*>(dst + r * ldd + c0) = *reinterpret_cast<const u32x4*>(src + r * scols + c0);
+            } else {
+                for (int64_t c = c0; c < cols; ++c) dst[r * ldd + c] = src[r * scols + c];
+            }
+        }
+    }
+}
+
+template <typename T>
+void launchPad(const void* src, int64_t rows, int64_t cols, int64_t lds, void* dst, int64_t drows, int64_t dcols,
+               hipStream_t st) {
+    constexpr int V = 16 / sizeof(T);
+    const unsigned gy = static_cast<unsigned>(std::min<int64_t>(drows, 4096));
+    if ((reinterpret_cast<uintptr_t>(src) & 15) == 0 && (lds * static_cast<int64_t>(sizeof(T))) % 16 == 0 &&
+        dcols % V == 0) {
+        const unsigned gx = static_cast<unsigned>(std::min<int64_t>((dcols / V + 255) / 256, 64));
+        hipLaunchKernelGGL(padBlock16<T>, dim3(gx, gy), dim3(256), 0, st, static_cast<const T*>(src), rows, cols, lds,
+                           static_cast<T*>(dst), drows, dcols);
+        return;
+    }
+    const unsigned gx = static_cast<unsigned>(std::min<int64_t>((dcols + 255) / 256, 64));
+    hipLaunchKernelGGL(padBlock<T>, dim3(gx, gy), dim3(256), 0, st, static_cast<const T*>(src), rows, cols, lds,
+                       static_cast<T*>(dst), drows, dcols);
+}
+
+int launchPadded(const mlkd_gemm* p, const mlkd_gemm& q, const PadShape& ps, hipStream_t st) {
+    if (ps.es == 2) {
+        launchPad<uint16_t>(p->a, p->m, p->k, p->lda, const_cast<void*>(q.a), ps.m, ps.k, st);
+        launchPad<uint16_t>(p->b, p->k, p->n, p->ldb, const_cast<void*>(q.b), ps.k, ps.n, st);
+    } else {
+        launchPad<uint32_t>(p->a, p->m, p->k, p->lda, const_cast<void*>(q.a), ps.m, ps.k, st);
+        launchPad<uint32_t>(p->b, p->k, p->n, p->ldb, const_cast<void*>(q.b), ps.k, ps.n, st);
+    }
+    // C += A*B reads C: its padded copy starts from C (and zeros).
+    if (p->accumulate != 0) launchPad<uint32_t>(p->c, p->m, p->n, p->ldc, q.c, ps.m, ps.n, st);
+    if (hipGetLastError() != hipSuccess) return MLKD_RT_LAUNCH;
+    if (const int rc = launchMfma(&q, mfmaForm(&q), st); rc != 0) return rc;
+    const unsigned gy = static_cast<unsigned>(std::min<int64_t>(p->m, 4096));
+    if ((reinterpret_cast<uintptr_t>(p->c) & 15) == 0 && p->ldc % 4 == 0) {
+        const unsigned gx = static_cast<unsigned>(std::min<int64_t>(((p->n + 3) / 4 + 255) / 256, 64));
+        hipLaunchKernelGGL(unpadBlock16, dim3(gx, gy), dim3(256), 0, st, static_cast<const uint32_t*>(q.c), ps.n,
+                           static_cast<uint32_t*>(p->c), p->m, p->n, p->ldc);
+    } else {
+        const unsigned gx = static_cast<unsigned>(std::min<int64_t>((p->n + 255) / 256, 64));
+        hipLaunchKernelGGL(unpadBlock<uint32_t>, dim3(gx, gy), dim3(256), 0, st, static_cast<const uint32_t*>(q.c),
+                           ps.n, static_cast<uint32_t*>(p->c), p->m, p->n, p->ldc);
+    }
+    return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
+}
+
 }  // namespace
 
 extern "C" void mlkd_gemm_set_variant(int variant) { gGemmF16Variant = variant; }
 
+extern "C" int64_t mlkd_gemm_pad_bytes(const mlkd_gemm* p) {
+    PadShape ps;
+    return p != nullptr && padShape(p, ps) ? static_cast<int64_t>(padBytes(ps)) : 0;
+}
+
 extern "C" const char* mlkd_gemm_kernel_name(const mlkd_gemm* p) {
+    {
+        // A padded launch is named by the MFMA form it runs.
+        mlkd_gemm q;
+        PadShape ps;
+        if (paddedParams(p, q, ps)) return mlkd_gemm_kernel_name(&q);
+    }
     const bool acc = p->accumulate != 0;
     switch (p->skip_zero_a != 0 && !acc ? -1 : mfmaForm(p)) {
         case 8:
@@ -1895,6 +2074,14 @@ extern "C" int mlkd_launch_gemm(const mlkd_gemm* p, void* stream) {
     // asks for the skip takes the general kernel.
     if (const int form = mfmaForm(p); form >= 0 && (p->skip_zero_a == 0 || p->accumulate != 0)) {
         return launchMfma(p, form, st);
+    }
+    {
+        mlkd_gemm q;
+        PadShape ps;
+        if (paddedParams(p, q, ps)) {
+            if (raiseLdsLimits() != 0) return MLKD_RT_LAUNCH;
+            return launchPadded(p, q, ps, st);
+        }
     }
     const int64_t tiles = ((p->m + 63) / 64) * ((p->n + 63) / 64);
     if (tiles > 0x7FFFFFFF) return MLKD_RT_LAUNCH;

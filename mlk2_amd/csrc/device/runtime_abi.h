@@ -88,6 +88,11 @@ int mlkd_launch_softmax(const mlkd_softmax* p, void* stream);
 /// with plain stores; waves <= 0 keeps the default grid).
 void mlkd_softmax_set_variant(int variant, int64_t waves);
 int mlkd_launch_gemm(const mlkd_gemm* p, void* stream);
+/// Bytes of workspace that let mlkd_launch_gemm run `p` on an MFMA form
+/// through zero-padded copies of A, B and C; 0 when the shape needs none
+/// (already tiled, another dtype combination, or too small to pay for the
+/// copies).
+int64_t mlkd_gemm_pad_bytes(const mlkd_gemm* p);
 /// The symbol of the kernel mlkd_launch_gemm runs for `p` (the MFMA form, or
 /// the general kernel), as profilers print it without the parameters. A
 /// skip-zero-A launch is the same single kernel.

@@ -49,6 +49,13 @@ typedef struct mlkd_gemm {
        met an infinity or a NaN (only there can the skip change C) recomputes
        its block exactly. Otherwise the general kernel runs everything. */
     int32_t skip_zero_a;
+    int32_t pad_;
+    /* Device workspace for shapes the MFMA forms do not tile
+       (mlkd_gemm_pad_bytes): the operands are copied into zero-padded
+       blocks there, the MFMA form runs on them and C is copied back. NULL
+       (or too small) keeps such shapes on the general kernel. */
+    void* work;
+    int64_t work_bytes;
 } mlkd_gemm;
 
 /// S[b*seq + i, j] = softmax_j((Q[b,i,:] . K[b,j,:]) / div + bias[j]).

@@ -343,6 +343,10 @@ const char* HipLoadedKernel::stepKernelName(size_t si) const {
         } else if (st.kind == StepKind::Gemm) {
             mlkd_gemm p;
             fillGemmParams(st, ptr, p);
+            if (const int64_t need = mlkd_gemm_pad_bytes(&p); need > 0) {
+                p.work = ptr[0];   // runDevice gives such a step its padding workspace
+                p.work_bytes = need;
+            }
             name = mlkd_gemm_kernel_name(&p);
         } else if (st.kind == StepKind::ScoreSoftmax) {
             mlkd_score_softmax p;
@@ -374,6 +378,9 @@ void HipLoadedKernel::fillGemmParams(const Step& st, const std::vector<void*>& p
     p.lda = st.lda;
     p.ldb = st.ldb;
     p.ldc = st.ldc;
+    p.pad_ = 0;
+    p.work = nullptr;
+    p.work_bytes = 0;
 }
 
 int HipLoadedKernel::arenaLayout(const DeviceBinding* binds, int64_t elements, const ScratchArena& arena,
@@ -559,7 +566,24 @@ int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* 
                 // The skip-zero-A decision (0 * inf and 0 * NaN are the only
                 // products whose skip changes C beyond the sign of a zero
                 // sum) is taken inside the MFMA kernel, per wave: one launch,
-                // no scratch, no host read-back.
+                // no host read-back.
+                // A shape the MFMA forms do not tile runs on zero-padded
+                // copies in a per-stream workspace. The allocation-free entry
+                // has no room for them and keeps such shapes on the general
+                // kernel.
+                if (const int64_t need = mlkd_gemm_pad_bytes(&p); need > 0 && arena == nullptr) {
+                    std::lock_guard<std::mutex> g(scratchLock_);
+                    if (rs->step[si] == nullptr || rs->stepBytes[si] < need) {
+                        if (rs->step[si] != nullptr) mlkd_rt_free(rs->step[si]);
+                        rs->step[si] = nullptr;
+                        rs->stepBytes[si] = 0;
+                        if (mlkd_rt_malloc(&rs->step[si], static_cast<size_t>(need)) != 0) rs->step[si] = nullptr;
+                        else rs->stepBytes[si] = need;
+                    }
+                    // Without the workspace the general kernel runs the step.
+                    p.work = rs->step[si];
+                    p.work_bytes = rs->stepBytes[si];
+                }
                 rc = mlkd_launch_gemm(&p, stream);
                 break;
             }

@@ -313,6 +313,11 @@ def test_step_kernel_names_name_the_launched_kernels(hip):
     art = hip.build(fx.config4_module(256, 256, 256, "f16", tier=1))
     art.set_step_variant(0, 7)
     assert art.step_kernel_name(0) == "gemmF16Dma<true>"
+    # Shapes the MFMA forms do not tile run on zero-padded copies (named by
+    # the MFMA form); small ones stay on the general kernel.
+    assert hip.build(fx.config4_module(1000, 600, 1000, "f16", tier=2)).step_kernel_name(0) == "gemmF16Dma8s<false>"
+    assert hip.build(fx.config4_module(700, 1000, 900, "f32", tier=1)).step_kernel_name(0) == "gemmF32Dma<true>"
+    assert hip.build(fx.config4_module(300, 50, 70, "f16", tier=2)).step_kernel_name(0) == "gemmGeneral<float>"
     art = hip.build(fx.config1_module(n=4096))
     assert art.step_kernel_name(0).startswith("mlk_elementwise_")
 
@@ -400,3 +405,34 @@ def test_1d_roots_resolve_buffers_by_position(hip):
             y0.astype(np.float32)
         assert np.array_equal(got, want), order
         say(f"1-D position resolution {order}: same as the executor")
+
+
+@pytest.mark.parametrize("m,k,n,dt,tier", [(1000, 600, 1000, "f16", 2), (1000, 600, 1000, "f16", 1),
+                                           (700, 1000, 900, "f32", 2), (700, 1000, 900, "f32", 1),
+                                           (4000, 4000, 4000, "f16", 2)])
+def test_ragged_gemm_runs_padded(hip, m, k, n, dt, tier):
+    # M, N or K off the MFMA tiles: A, B (and C for the Call form) are copied
+    # into zero-padded blocks, the MFMA form runs there, and C is copied
+    # back. The extra products are 0 * 0, so each output is the product's.
+    # The Call form accumulates into a non-zero C.
+    rng = np.random.default_rng(21)
+    A = rng.uniform(-1, 1, (m, k))
+    B = rng.uniform(-1, 1, (k, n))
+    np_dt = {"f32": np.float32, "f16": np.float16}[dt]
+    A = A.astype(np_dt).astype(np.float64)
+    B = B.astype(np_dt).astype(np.float64)
+    km = fx.config4_module(m, k, n, dt, tier)
+    art = hip.build(km)
+    name = art.step_kernel_name(0)
+    assert name.startswith("gemmF16Dma8s" if dt == "f16" else "gemmF32Dma"), name
+    rows = slice(0, m) if m <= 1000 else slice(0, m, 97)       # the oracle on sampled rows at 4000^3
+    C0 = rng.uniform(-1, 1, m * n) if tier == 1 else np.zeros(m * n)
+    got = (art.run({0: A, 1: B, 2: C0}) if tier == 1 else art.run({0: A, 1: B}))[2].reshape(m, n)
+    Ar = np.ascontiguousarray(A[rows])
+    ref = oracle.run(fx.matmul_call_module(Ar.shape[0], k, n, "f64", "f64"), {0: Ar.reshape(-1), 1: B.reshape(-1)},
+                     init={2: np.ascontiguousarray(C0.reshape(m, n)[rows]).reshape(-1)},
+                     hw_threads=8)[2].reshape(-1, n)
+    tol = 1e-2 if dt == "f16" else 1e-5 * math.sqrt(k)
+    e = max_rel(got[rows], ref)
+    say(f"ragged gemm {dt} {m}x{k}x{n} tier {tier} on {name}: max_rel {e:.3e}")
+    assert e <= tol
