@@ -102,6 +102,9 @@ const char* mlkd_softmax_kernel_name(const mlkd_softmax* p);
 /// Likewise for score-softmax: its kernels joined by '+' (valid until this
 /// thread's next call).
 const char* mlkd_score_kernel_names(const mlkd_score_softmax* p);
+/// Workspace bytes that let mlkd_launch_score_softmax run a sequence length
+/// off the two-pass form's blocks on zero-padded copies; 0 when none applies.
+int64_t mlkd_score_pad_bytes(const mlkd_score_softmax* p);
 /// Process default of the f16 GEMM launch form (8: direct-to-LDS ring with 8
 /// waves of 16x16x32 tiles, the default; 7: the same ring with 4 waves of
 /// 32x32x16; 0: 8 waves x 128x64; 1: 4 waves x 128x128; 2: A direct to LDS;

@@ -235,11 +235,16 @@ __device__ __forceinline__ void mergeStatsQ(const float2* __restrict__ part, int
 
 /// Pass 2 over keys [k0, k0 + keys) of this wave's 32 rows r0..r0+31 of
 /// batch b: D = Q K^T per panel, written as exp2(v - max) / sum at once;
-/// each 32-lane half-wave stores one 128-byte line.
+/// each 32-lane half-wave stores one 128-byte line. RAGGED: Q, K and the
+/// bias are zero-padded copies of length seq of a sequence of length sseq;
+/// S is [batch][sseq][sseq] and only rows and keys below sseq are stored.
+template <bool RAGGED>
 __device__ __forceinline__ void storeRangeQ(const _Float16* __restrict__ Q, const _Float16* __restrict__ K,
                                             const float* __restrict__ bias, float* __restrict__ S, int seq,
-                                            float c2, int64_t b, int64_t r0, int k0, int keys,
+                                            int sseq, float c2, int64_t b, int64_t r0, int k0, int keys,
                                             const float (&rlm)[16], _Float16* ldsQ) {
+    const int ld = RAGGED ? sseq : seq;           // S row length
+    const int i0 = static_cast<int>(r0 - b * seq);   // first row within the batch
     const int tid = threadIdx.x;
     const int lane = tid & 63, l32 = lane & 31, hl = lane >> 5;
     const int np = keys / kPanelQ;
@@ -254,7 +259,7 @@ __device__ __forceinline__ void storeRangeQ(const _Float16* __restrict__ Q, cons
     uint32_t soff[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-        soff[r] = static_cast<uint32_t>(((8 * (r >> 2) + 4 * hl + (r & 3)) * seq + l32) * sizeof(float));
+        soff[r] = static_cast<uint32_t>(((8 * (r >> 2) + 4 * hl + (r & 3)) * ld + l32) * sizeof(float));
     }
     u32x4v v[8];
     loadPanelQ(kb, tid, v);
@@ -281,11 +286,12 @@ __device__ __forceinline__ void storeRangeQ(const _Float16* __restrict__ Q, cons
         float bj[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) bj[j] = bias[kc + j * 32 + l32] * kLog2e;
-        char* sb = reinterpret_cast<char*>(S + r0 * static_cast<int64_t>(seq) + kc);
+        char* sb = reinterpret_cast<char*>(S + (b * ld + i0) * static_cast<int64_t>(ld) + kc);
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
+                if (RAGGED && (i0 + 8 * (r >> 2) + 4 * hl + (r & 3) >= sseq || kc + j * 32 + l32 >= sseq)) continue;
                 *reinterpret_cast<float*>(sb + soff[r] + j * 32 * sizeof(float)) =
                     __builtin_amdgcn_exp2f(__builtin_fmaf(acc[j][r], c2, bj[j]) - rlm[r]);
             }
@@ -308,11 +314,12 @@ __global__ __launch_bounds__(256, 2) void scoreStatsQ(const _Float16* __restrict
     if (((threadIdx.x & 63) >> 5) == 0) part[qrow * 2 + kh] = st;
 }
 
+template <bool RAGGED>
 __global__ __launch_bounds__(256, 2) void scoreStoreQ(const _Float16* __restrict__ Q,
                                                       const _Float16* __restrict__ K,
                                                       const float* __restrict__ bias,
                                                       const float2* __restrict__ part, float* __restrict__ S,
-                                                      int seq, float c2) {
+                                                      int seq, int sseq, float c2) {
     extern __shared__ __align__(16) _Float16 ldsQ[];
     int64_t b;
     int rb, kh;
@@ -321,18 +328,22 @@ __global__ __launch_bounds__(256, 2) void scoreStoreQ(const _Float16* __restrict
     const int64_t r0 = b * seq + static_cast<int64_t>(rb) * 128 + wave * 32;   // wave-uniform
     float rlm[16];
     mergeStatsQ<2>(part, r0, rlm);
-    storeRangeQ(Q, K, bias, S, seq, c2, b, r0, kh * (seq / 2), seq / 2, rlm, ldsQ);
+    storeRangeQ<RAGGED>(Q, K, bias, S, seq, sseq, c2, b, r0, kh * (seq / 2), seq / 2, rlm, ldsQ);
 }
 
-int launchQ(const mlkd_score_softmax* p, hipStream_t st) {
+/// Both passes over p's (padded) Q, K and bias; `ragged` > 0 stores only
+/// rows and keys below it into p->s laid out [batch][ragged][ragged].
+int launchQ(const mlkd_score_softmax* p, hipStream_t st, int64_t ragged = 0) {
     const size_t ldsStats = kLdsStoreQ + static_cast<size_t>(p->seq / 2) * sizeof(float);
     // Once per process; a function-local static initializes thread-safely.
     static const bool attrs = [] {
         const size_t maxStats = kLdsStoreQ + static_cast<size_t>(kMaxSeqQ / 2) * sizeof(float);
         return hipFuncSetAttribute(reinterpret_cast<const void*>(scoreStatsQ), hipFuncAttributeMaxDynamicSharedMemorySize,
                                    static_cast<int>(maxStats)) == hipSuccess &&
-               hipFuncSetAttribute(reinterpret_cast<const void*>(scoreStoreQ), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                   static_cast<int>(kLdsStoreQ)) == hipSuccess;
+               hipFuncSetAttribute(reinterpret_cast<const void*>(scoreStoreQ<false>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLdsStoreQ)) == hipSuccess &&
+               hipFuncSetAttribute(reinterpret_cast<const void*>(scoreStoreQ<true>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLdsStoreQ)) == hipSuccess;
     }();
     if (!attrs) return MLKD_RT_LAUNCH;
     const unsigned blocks = static_cast<unsigned>(p->batch * (p->seq / 128) * 2);
@@ -342,10 +353,11 @@ int launchQ(const mlkd_score_softmax* p, hipStream_t st) {
     hipLaunchKernelGGL(scoreStatsQ, dim3(blocks), dim3(256), ldsStats, st, static_cast<const _Float16*>(p->q),
                        static_cast<const _Float16*>(p->k), static_cast<const float*>(p->bias),
                        static_cast<float2*>(p->scratch), static_cast<int>(p->seq), c2);
-    hipLaunchKernelGGL(scoreStoreQ, dim3(blocks), dim3(256), kLdsStoreQ, st, static_cast<const _Float16*>(p->q),
-                       static_cast<const _Float16*>(p->k), static_cast<const float*>(p->bias),
-                       static_cast<const float2*>(p->scratch), static_cast<float*>(p->s), static_cast<int>(p->seq),
-                       c2);
+    hipLaunchKernelGGL(ragged > 0 ? scoreStoreQ<true> : scoreStoreQ<false>, dim3(blocks), dim3(256), kLdsStoreQ, st,
+                       static_cast<const _Float16*>(p->q), static_cast<const _Float16*>(p->k),
+                       static_cast<const float*>(p->bias), static_cast<const float2*>(p->scratch),
+                       static_cast<float*>(p->s), static_cast<int>(p->seq),
+                       static_cast<int>(ragged > 0 ? ragged : p->seq), c2);
     return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
 }
 
@@ -391,6 +403,66 @@ __global__ __launch_bounds__(256) void scoresGeneral(mlkd_score_softmax p) {
     }
 }
 
+/// [batch][rows][128] f16 -> [batch][drows][128], zero rows past `rows`, in
+/// 16-byte pieces (16 per row).
+__global__ __launch_bounds__(256) void padQK(const u32x4v* __restrict__ src, int64_t batch, int64_t rows,
+                                             u32x4v* __restrict__ dst, int64_t drows) {
+    const int64_t total = batch * drows * 16;
+    for (int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; t < total;
+         t += static_cast<int64_t>(gridDim.x) * 256) {
+        const int64_t piece = t & 15, r = t >> 4;
+        const int64_t b = r / drows, i = r % drows;
+        dst[t] = i < rows ? src[(b * rows + i) * 16 + piece] : u32x4v{0u, 0u, 0u, 0u};
+    }
+}
+
+/// bias' = bias on [0, seq), -inf on [seq, dseq): padded keys take no share.
+__global__ __launch_bounds__(256) void padBias(const float* __restrict__ src, int64_t seq, float* __restrict__ dst,
+                                               int64_t dseq) {
+    for (int64_t j = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; j < dseq;
+         j += static_cast<int64_t>(gridDim.x) * 256) {
+        dst[j] = j < seq ? src[j] : -INFINITY;
+    }
+}
+
+/// The padded two-pass launch: sequence length rounded up to 256 (at most
+/// kMaxSeqQ), for shapes the two passes would take but for the length.
+/// Q, K and the bias are copied into the workspace (q.s stays the caller's
+/// S: pass 2 stores only its rows and keys). Below 2^20 scores the general
+/// kernels take less than the copies.
+bool padScore(const mlkd_score_softmax* p, mlkd_score_softmax& q) {
+    if (p->work == nullptr || p->seq % 256 == 0) return false;
+    q = *p;
+    q.seq = (p->seq + 255) / 256 * 256;
+    if (q.seq > kMaxSeqQ || p->batch * p->seq * p->seq < (int64_t{1} << 20)) return false;
+    unsigned char* w = static_cast<unsigned char*>(p->work);
+    const size_t qk = static_cast<size_t>(p->batch * q.seq * kD2) * sizeof(_Float16);
+    q.q = w;
+    q.k = w + qk;
+    q.bias = w + 2 * qk;
+    q.scratch = w + 2 * qk + static_cast<size_t>(q.seq) * sizeof(float);
+    q.scratch_bytes = scratch2(&q);
+    q.work = nullptr;
+    q.work_bytes = 0;
+    const int64_t need = static_cast<int64_t>(2 * qk + static_cast<size_t>(q.seq) * sizeof(float)) + q.scratch_bytes;
+    return twoPassApplies(&q) && p->work_bytes >= need && (reinterpret_cast<uintptr_t>(p->q) & 15u) == 0 &&
+           (reinterpret_cast<uintptr_t>(p->k) & 15u) == 0;
+}
+
+int launchPaddedQ(const mlkd_score_softmax* p, const mlkd_score_softmax& q, hipStream_t st) {
+    const int64_t pieces = p->batch * q.seq * 16;
+    const unsigned g = static_cast<unsigned>(std::min<int64_t>((pieces + 255) / 256, 16384));
+    hipLaunchKernelGGL(padQK, dim3(g), dim3(256), 0, st, static_cast<const u32x4v*>(p->q), p->batch, p->seq,
+                       static_cast<u32x4v*>(const_cast<void*>(q.q)), q.seq);
+    hipLaunchKernelGGL(padQK, dim3(g), dim3(256), 0, st, static_cast<const u32x4v*>(p->k), p->batch, p->seq,
+                       static_cast<u32x4v*>(const_cast<void*>(q.k)), q.seq);
+    hipLaunchKernelGGL(padBias, dim3(static_cast<unsigned>((q.seq + 255) / 256)), dim3(256), 0, st,
+                       static_cast<const float*>(p->bias), p->seq, static_cast<float*>(const_cast<void*>(q.bias)),
+                       q.seq);
+    if (hipGetLastError() != hipSuccess) return MLKD_RT_LAUNCH;
+    return launchQ(&q, st, p->seq);
+}
+
 // 0: the best form for the shape (the two-pass query-stationary form where
 // it applies); 1: scores, then the softmax kernel in place over S.
 int gScoreVariant = 0;
@@ -403,9 +475,21 @@ extern "C" int64_t mlkd_score_scratch_bytes(const mlkd_score_softmax* p) {
     return p != nullptr && twoPassApplies(p) ? scratch2(p) : 0;
 }
 
+extern "C" int64_t mlkd_score_pad_bytes(const mlkd_score_softmax* p) {
+    if (p == nullptr) return 0;
+    mlkd_score_softmax probe = *p;
+    probe.work = reinterpret_cast<void*>(uintptr_t{1} << 12);
+    probe.work_bytes = INT64_MAX;
+    mlkd_score_softmax q;
+    if (!padScore(&probe, q)) return 0;
+    const int64_t qk = p->batch * q.seq * kD2 * static_cast<int64_t>(sizeof(_Float16));
+    return 2 * qk + q.seq * static_cast<int64_t>(sizeof(float)) + scratch2(&q);
+}
+
 extern "C" const char* mlkd_score_kernel_names(const mlkd_score_softmax* p) {
     static thread_local char name[160];
     const int variant = p->variant >= 0 ? p->variant : gScoreVariant;
+    if (mlkd_score_softmax q; variant != 1 && padScore(p, q)) return "scoreStatsQ+scoreStoreQ";
     if (variant != 1 && twoPassApplies(p) && p->scratch != nullptr &&
         (reinterpret_cast<uintptr_t>(p->scratch) & 7u) == 0 && p->scratch_bytes >= scratch2(p)) {
         return "scoreStatsQ+scoreStoreQ";
@@ -438,6 +522,7 @@ extern "C" int mlkd_launch_score_softmax(const mlkd_score_softmax* p, void* stre
         (reinterpret_cast<uintptr_t>(p->scratch) & 7u) == 0 && p->scratch_bytes >= scratch2(p)) {
         return launchQ(p, st);
     }
+    if (mlkd_score_softmax q; variant != 1 && padScore(p, q)) return launchPaddedQ(p, q, st);
     const bool fast = p->qk_dtype == MLKD_F16 && p->bias_dtype == MLKD_F32 && p->s_dtype == MLKD_F32 &&
                       p->seq % 128 == 0 && p->dim % 16 == 0 && p->dim > 0 && p->seq < (1 << 20) &&
                       (reinterpret_cast<uintptr_t>(p->q) & 15u) == 0 &&

@@ -72,6 +72,13 @@ typedef struct mlkd_score_softmax {
        (mlkd_score_scratch_bytes); may be NULL, which selects another form. */
     void* scratch;
     int64_t scratch_bytes;
+    /* Workspace for a sequence length off the two-pass form's 256-row blocks
+       (mlkd_score_pad_bytes): Q, K and the bias are copied into zero-padded
+       blocks (padded keys get a -inf bias), the two passes run there and S
+       is copied back. NULL (or too small) keeps such shapes on the general
+       kernels. */
+    void* work;
+    int64_t work_bytes;
 } mlkd_score_softmax;
 
 #ifdef __cplusplus

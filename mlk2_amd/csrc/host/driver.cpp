@@ -290,6 +290,8 @@ void HipLoadedKernel::fillScoreParams(const Step& st, const std::vector<void*>& 
     p.div = st.div;
     p.scratch = nullptr;
     p.scratch_bytes = 0;
+    p.work = nullptr;
+    p.work_bytes = 0;
 }
 
 int HipLoadedKernel::ensureNestForm(size_t si, int form, void*& fn, std::string& why) const {
@@ -354,6 +356,10 @@ const char* HipLoadedKernel::stepKernelName(size_t si) const {
             if (const int64_t need = mlkd_score_scratch_bytes(&p); need > 0) {
                 p.scratch = ptr[0];
                 p.scratch_bytes = need;
+            }
+            if (const int64_t need = mlkd_score_pad_bytes(&p); need > 0) {
+                p.work = ptr[0];   // runDevice gives such a step its padding workspace
+                p.work_bytes = need;
             }
             name = mlkd_score_kernel_names(&p);
         }
@@ -659,6 +665,20 @@ int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* 
                     }
                     p.scratch = rs->step[si];
                     p.scratch_bytes = rs->stepBytes[si];
+                } else if (const int64_t pad = mlkd_score_pad_bytes(&p); pad > 0 && arena == nullptr) {
+                    // A sequence length off the two-pass blocks runs on
+                    // zero-padded copies, as for GEMM shapes off the MFMA
+                    // tiles; without the workspace the general kernels run.
+                    std::lock_guard<std::mutex> g(scratchLock_);
+                    if (rs->step[si] == nullptr || rs->stepBytes[si] < pad) {
+                        if (rs->step[si] != nullptr) mlkd_rt_free(rs->step[si]);
+                        rs->step[si] = nullptr;
+                        rs->stepBytes[si] = 0;
+                        if (mlkd_rt_malloc(&rs->step[si], static_cast<size_t>(pad)) != 0) rs->step[si] = nullptr;
+                        else rs->stepBytes[si] = pad;
+                    }
+                    p.work = rs->step[si];
+                    p.work_bytes = rs->stepBytes[si];
                 }
                 rc = mlkd_launch_score_softmax(&p, stream);
                 break;

@@ -550,6 +550,41 @@ def test_c5_long_rows_sampled(hip, s, two_pass):
         bb.free()
 
 
+@pytest.mark.parametrize("b,s", [(1, 2000), (4, 1000), (16, 300), (64, 128)])
+def test_c5_ragged_seq_runs_padded(hip, b, s):
+    # A sequence length off the two-pass form's 256-row blocks runs on
+    # zero-padded copies of Q and K (padded keys take a -inf bias, so they
+    # add exp(-inf) = 0 to each row's sum; padded query rows are dropped).
+    # At 64x128 the padded length is 256 and pass 1's second key half is
+    # all padding. Sampled rows of the first and last batch are held to the
+    # composed oracle reference; a fully masked bias gives NaN rows, as the
+    # reference does.
+    dm = 128
+    say(f"c5 ragged seq b={b} s={s}")
+    d = inputs.config_inputs("c5", {"batch": b, "seq": s, "dim": dm})
+    km = fx.score_softmax_module(b, s, dm)
+    art = hip.build(km)
+    assert art.step_kernel_name(0) == "scoreStatsQ+scoreStoreQ"
+    got = art.run({0: d["Q"], 1: d["K"], 2: d["bias"]})[3].reshape(b, s, s)
+    rows = np.random.default_rng(7).choice(s, min(s, 16), replace=False)
+    rows[0], rows[1] = 0, s - 1
+    for bb in sorted({0, b - 1}):
+        ref = _score_ref(d["Q"][bb:bb + 1], d["K"][bb:bb + 1], d["bias"], rows=rows)
+        e = max_rel(got[bb][rows], ref)
+        say(f"c5 ragged b={b} s={s} batch {bb} max_rel={e:.3e}")
+        assert e <= 1e-2
+    sums = got.reshape(b * s, s)[::37].astype(np.float64).sum(axis=1)
+    assert np.abs(sums - 1.0).max() < 1e-3
+    masked = art.run({0: d["Q"], 1: d["K"], 2: np.full(s, -np.inf)})[3]
+    assert np.isnan(masked).all()
+
+
+def test_c5_small_ragged_seq_stays_general(hip):
+    # Below 2^20 scores the copies would cost more than the general kernels.
+    km = fx.score_softmax_module(1, 300, 128)
+    assert hip.build(km).step_kernel_name(0).startswith("scoresGeneral+")
+
+
 # ------------------------------------------------------------- entries ----
 def test_device_entry_matches_host_entry(hip):
     say("device entry vs host entry")
