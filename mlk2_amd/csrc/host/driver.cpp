@@ -391,7 +391,7 @@ void HipLoadedKernel::fillGemmParams(const Step& st, const std::vector<void*>& p
 
 int HipLoadedKernel::arenaLayout(const DeviceBinding* binds, int64_t elements, const ScratchArena& arena,
                                  std::vector<size_t>& tempOff, std::vector<size_t>& stepOff,
-                                 std::string& why) const {
+                                 std::vector<size_t>& padOff, std::string& why) const {
     size_t used = 0;
     tempOff.assign(km_.buffers.size(), 0);
     stepOff.assign(plan_.steps.size(), 0);
@@ -438,6 +438,27 @@ int HipLoadedKernel::arenaLayout(const DeviceBinding* binds, int64_t elements, c
               std::to_string(arena.bytes);
         return MLKHIP_REFUSED;
     }
+    // Padding workspaces (GEMM shapes off the MFMA tiles, score-softmax
+    // lengths off the two-pass blocks) take the room that is left, in step
+    // order; a step whose workspace does not fit runs on the general kernels.
+    padOff.assign(plan_.steps.size(), SIZE_MAX);
+    for (size_t si = 0; si < plan_.steps.size(); ++si) {
+        const Step& st = plan_.steps[si];
+        int64_t pad = 0;
+        if (st.kind == StepKind::Gemm) {
+            mlkd_gemm p;
+            fillGemmParams(st, ptr, p);
+            pad = mlkd_gemm_pad_bytes(&p);
+        } else if (st.kind == StepKind::ScoreSoftmax) {
+            mlkd_score_softmax p;
+            fillScoreParams(st, ptr, p);
+            pad = mlkd_score_pad_bytes(&p);
+        }
+        if (pad > 0 && align256(static_cast<size_t>(pad)) <= arena.bytes - used) {
+            padOff[si] = used;
+            used += align256(static_cast<size_t>(pad));
+        }
+    }
     return MLKHIP_OK;
 }
 
@@ -450,9 +471,11 @@ int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* 
     }
     // Scratch comes from the caller's arena (the allocation-free entry), laid
     // out before anything is launched, or from this stream's own allocations.
-    std::vector<size_t> tempOff, stepOff;
+    std::vector<size_t> tempOff, stepOff, padOff;
     if (arena != nullptr) {
-        if (const int rc = arenaLayout(binds, elements, *arena, tempOff, stepOff, why); rc != MLKHIP_OK) return rc;
+        if (const int rc = arenaLayout(binds, elements, *arena, tempOff, stepOff, padOff, why); rc != MLKHIP_OK) {
+            return rc;
+        }
     }
     RunScratch* rs = nullptr;
     if (arena == nullptr) {
@@ -574,10 +597,14 @@ int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* 
                 // sum) is taken inside the MFMA kernel, per wave: one launch,
                 // no host read-back.
                 // A shape the MFMA forms do not tile runs on zero-padded
-                // copies in a per-stream workspace. The allocation-free entry
-                // has no room for them and keeps such shapes on the general
-                // kernel.
-                if (const int64_t need = mlkd_gemm_pad_bytes(&p); need > 0 && arena == nullptr) {
+                // copies in a per-stream workspace, or, for the
+                // allocation-free entry, in the arena when they fit there
+                // (else on the general kernel).
+                const int64_t need = mlkd_gemm_pad_bytes(&p);
+                if (need > 0 && arena != nullptr && padOff[si] != SIZE_MAX) {
+                    p.work = arena->base + padOff[si];
+                    p.work_bytes = need;
+                } else if (need > 0 && arena == nullptr) {
                     std::lock_guard<std::mutex> g(scratchLock_);
                     if (rs->step[si] == nullptr || rs->stepBytes[si] < need) {
                         if (rs->step[si] != nullptr) mlkd_rt_free(rs->step[si]);
@@ -665,7 +692,12 @@ int HipLoadedKernel::runDevice(const DeviceBinding* binds, int n, const double* 
                     }
                     p.scratch = rs->step[si];
                     p.scratch_bytes = rs->stepBytes[si];
-                } else if (const int64_t pad = mlkd_score_pad_bytes(&p); pad > 0 && arena == nullptr) {
+                } else if (const int64_t pad = mlkd_score_pad_bytes(&p); pad > 0 && arena != nullptr) {
+                    if (padOff[si] != SIZE_MAX) {
+                        p.work = arena->base + padOff[si];
+                        p.work_bytes = pad;
+                    }
+                } else if (pad > 0) {
                     // A sequence length off the two-pass blocks runs on
                     // zero-padded copies, as for GEMM shapes off the MFMA
                     // tiles; without the workspace the general kernels run.

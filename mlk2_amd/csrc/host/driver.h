@@ -120,7 +120,8 @@ private:
     /// Offsets of a run's scratch in `arena`; refuses what does not fit or
     /// needs a host read-back.
     int arenaLayout(const DeviceBinding* binds, int64_t elements, const ScratchArena& arena,
-                    std::vector<size_t>& tempOff, std::vector<size_t>& stepOff, std::string& why) const;
+                    std::vector<size_t>& tempOff, std::vector<size_t>& stepOff, std::vector<size_t>& padOff,
+                    std::string& why) const;
     void fillScoreParams(const Step& st, const std::vector<void*>& ptr, mlkd_score_softmax& p) const;
     void fillGemmParams(const Step& st, const std::vector<void*>& ptr, mlkd_gemm& p) const;
     void fillSoftmaxParams(const Step& st, const std::vector<void*>& ptr, mlkd_softmax& p) const;
