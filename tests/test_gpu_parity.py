@@ -550,13 +550,15 @@ def test_c5_long_rows_sampled(hip, s, two_pass):
         bb.free()
 
 
-@pytest.mark.parametrize("b,s", [(1, 2000), (4, 1000), (16, 300), (64, 128)])
+@pytest.mark.parametrize("b,s", [(1, 2000), (4, 1000), (16, 300), (64, 128), (1, 8000), (2, 1500), (8, 700),
+                                 (32, 257)])
 def test_c5_ragged_seq_runs_padded(hip, b, s):
     # A sequence length off the two-pass form's 256-row blocks runs on
     # zero-padded copies of Q and K (padded keys take a -inf bias, so they
     # add exp(-inf) = 0 to each row's sum; padded query rows are dropped).
     # At 64x128 the padded length is 256 and pass 1's second key half is
-    # all padding. Sampled rows of the first and last batch are held to the
+    # all padding; 1x8000 pads to the longest two-pass row (8192); 32x257
+    # pads 257 rows to 512, the most padding per row. Sampled rows of the first and last batch are held to the
     # composed oracle reference; a fully masked bias gives NaN rows, as the
     # reference does.
     dm = 128
