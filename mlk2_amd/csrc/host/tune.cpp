@@ -382,13 +382,12 @@ std::string launchCoverage(const KernelModule& km, const Step& st, int64_t eleme
         case StepKind::ScoreSoftmax: {
             // Output scores; the two-pass form (dim 128, seq % 256 == 0)
             // gives each workgroup of a pass 128 rows x half the keys. A
-            // longer-than-2^20-score sequence off the 256-row blocks runs it
-            // on copies padded to seq' (a multiple of 256).
+            // sequence off the 256-row blocks runs it on copies padded to
+            // seq' (a multiple of 256).
             instances = st.batch * st.seq * st.seq;
             const int64_t sp = (st.seq + 255) / 256 * 256;
             const bool padded = st.seq % 256 != 0;
-            const bool twoPass = st.dim == 128 && sp <= 8192 && st.variant != 1 &&
-                                 (!padded || instances >= (int64_t{1} << 20));
+            const bool twoPass = st.dim == 128 && sp <= 8192 && st.variant != 1;
             workgroups = twoPass ? st.batch * (sp / 128) * 2 : st.batch * ((st.seq + 63) / 64) * ((st.seq + 127) / 128);
             perGroup = twoPass ? 64 * sp : 64 * 128;
             covered = workgroups * perGroup >= instances;

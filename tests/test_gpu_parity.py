@@ -551,7 +551,7 @@ def test_c5_long_rows_sampled(hip, s, two_pass):
 
 
 @pytest.mark.parametrize("b,s", [(1, 2000), (4, 1000), (16, 300), (64, 128), (1, 8000), (2, 1500), (8, 700),
-                                 (32, 257)])
+                                 (32, 257), (1, 100), (3, 129)])
 def test_c5_ragged_seq_runs_padded(hip, b, s):
     # A sequence length off the two-pass form's 256-row blocks runs on
     # zero-padded copies of Q and K (padded keys take a -inf bias, so they
@@ -581,10 +581,12 @@ def test_c5_ragged_seq_runs_padded(hip, b, s):
     assert np.isnan(masked).all()
 
 
-def test_c5_small_ragged_seq_stays_general(hip):
-    # Below 2^20 scores the copies would cost more than the general kernels.
-    km = fx.score_softmax_module(1, 300, 128)
-    assert hip.build(km).step_kernel_name(0).startswith("scoresGeneral+")
+def test_c5_ragged_seq_forms(hip):
+    # Padded at any size with dim 128 up to the longest two-pass row; other
+    # head dims and longer rows take the general kernels.
+    assert hip.build(fx.score_softmax_module(1, 100, 128)).step_kernel_name(0) == "scoreStatsQ+scoreStoreQ"
+    assert hip.build(fx.score_softmax_module(1, 300, 64)).step_kernel_name(0).startswith("scoresGeneral+")
+    assert hip.build(fx.score_softmax_module(1, 8200, 128)).step_kernel_name(0).startswith("scoresGeneral+")
 
 
 # ------------------------------------------------------------- entries ----
