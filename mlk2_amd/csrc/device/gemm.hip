@@ -1901,16 +1901,20 @@ bool padShape(const mlkd_gemm* p, PadShape& ps) {
     if (!(f16 || f32) || p->m <= 0 || p->n <= 0 || p->k <= 0) return false;
     if (p->skip_zero_a != 0 && p->accumulate == 0) return false;   // that launch takes the general kernel
     if (mfmaForm(p) >= 0) return false;                             // already tiled
-    if (2.0 * static_cast<double>(p->m) * static_cast<double>(p->n) * static_cast<double>(p->k) <
-        static_cast<double>(int64_t{1} << 30)) {
-        return false;
-    }
     const int64_t tm = f16 ? kBM : kFM, tn = f16 ? kBN : kFN, tk = 64;
     ps.m = (p->m + tm - 1) / tm * tm;
     ps.n = (p->n + tn - 1) / tn * tn;
     ps.k = (p->k + tk - 1) / tk * tk;
     ps.es = f16 ? 2 : 4;
-    return ps.m < (int64_t{1} << 31) && ps.n < (int64_t{1} << 31) && ps.k < (int64_t{1} << 31);
+    if (ps.m >= (int64_t{1} << 31) || ps.n >= (int64_t{1} << 31) || ps.k >= (int64_t{1} << 31)) return false;
+    // Padded when the product is large (2^30 flop and up) or the padding at
+    // most 8 times the work: the general kernel takes 36 us at 100^3 and
+    // 150 us at 500^3, the padded MFMA launch tens of us at either. Thin
+    // shapes padded further (a few rows against 256-row tiles) stay on the
+    // general kernel, whose work is then small.
+    const double work = static_cast<double>(p->m) * static_cast<double>(p->n) * static_cast<double>(p->k);
+    const double padded = static_cast<double>(ps.m) * static_cast<double>(ps.n) * static_cast<double>(ps.k);
+    return 2.0 * work >= static_cast<double>(int64_t{1} << 30) || padded <= 8.0 * work;
 }
 
 size_t align256g(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }

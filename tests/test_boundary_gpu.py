@@ -314,10 +314,13 @@ def test_step_kernel_names_name_the_launched_kernels(hip):
     art.set_step_variant(0, 7)
     assert art.step_kernel_name(0) == "gemmF16Dma<true>"
     # Shapes the MFMA forms do not tile run on zero-padded copies (named by
-    # the MFMA form); small ones stay on the general kernel.
+    # the MFMA form); thin ones, padded more than 8 times their work, stay
+    # on the general kernel.
     assert hip.build(fx.config4_module(1000, 600, 1000, "f16", tier=2)).step_kernel_name(0) == "gemmF16Dma8s<false>"
     assert hip.build(fx.config4_module(700, 1000, 900, "f32", tier=1)).step_kernel_name(0) == "gemmF32Dma<true>"
-    assert hip.build(fx.config4_module(300, 50, 70, "f16", tier=2)).step_kernel_name(0) == "gemmGeneral<float>"
+    assert hip.build(fx.config4_module(300, 50, 70, "f16", tier=2)).step_kernel_name(0) == "gemmF16Dma8s<false>"
+    assert hip.build(fx.config4_module(100, 100, 100, "f32", tier=2)).step_kernel_name(0) == "gemmF32Dma<false>"
+    assert hip.build(fx.config4_module(8, 512, 512, "f16", tier=2)).step_kernel_name(0) == "gemmGeneral<float>"
     art = hip.build(fx.config1_module(n=4096))
     assert art.step_kernel_name(0).startswith("mlk_elementwise_")
 
