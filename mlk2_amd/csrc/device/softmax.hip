@@ -137,6 +137,51 @@ __global__ __launch_bounds__(256) void softmaxWaveRow(const float* x,
     }
 }
 
+/// Rows the float4 loads cannot take (cols % 4 != 0, or a row start off 16
+/// bytes), up to 256 * CH columns: one wave per row with the arithmetic of
+/// softmaxWaveRow<CH, true, true> (f32 max, v_exp_f32, f64 sum of f32 sums
+/// of 4-element groups), 4-byte loads and stores that are lane-contiguous
+/// per instruction. v[c][e] holds element c * 256 + e * 64 + lane; elements
+/// past the row read as -inf and add exp2(-inf) = 0 to their group.
+template <int CH>
+__global__ __launch_bounds__(256) void softmaxWaveRowScalar(const float* __restrict__ x, float* __restrict__ y,
+                                                            int64_t rows, int64_t cols, int64_t xs, int64_t ys) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int64_t waves = static_cast<int64_t>(gridDim.x) * 4;
+    for (int64_t row = wave; row < rows; row += waves) {
+        const float* xr = x + row * xs;
+        float* yr = y + row * ys;
+        f32x4 v[CH];
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int64_t col = static_cast<int64_t>(c) * 256 + e * 64 + lane;
+                v[c][e] = col < cols ? xr[col] : -INFINITY;
+            }
+        }
+        const float m = rowMax<CH>(v);
+        double s = 0.0;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[c][e] = __builtin_amdgcn_exp2f((v[c][e] - m) * 1.44269504088896340736f);
+            s += static_cast<double>((v[c][0] + v[c][1]) + (v[c][2] + v[c][3]));
+        }
+        s = waveSum(s);
+        const float inv = static_cast<float>(1.0 / s);
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int64_t col = static_cast<int64_t>(c) * 256 + e * 64 + lane;
+                if (col < cols) __builtin_nontemporal_store(v[c][e] * inv, yr + col);
+            }
+        }
+    }
+}
+
 /// Two adjacent rows per wave: the second row's loads are issued once the
 /// first row's max is known, so they land while the first row is
 /// exponentiated, summed and stored. The per-row arithmetic is that of form 0
@@ -301,6 +346,22 @@ int launchWave(const mlkd_softmax& p, hipStream_t st) {
     return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
 }
 
+template <int CH>
+int launchScalar(const mlkd_softmax& p, hipStream_t st) {
+    int64_t blocks = (p.rows + 3) / 4;
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL(softmaxWaveRowScalar<CH>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st,
+                       static_cast<const float*>(p.x), static_cast<float*>(p.y), p.rows, p.cols, p.x_row_stride,
+                       p.y_row_stride);
+    return hipGetLastError() == hipSuccess ? 0 : MLKD_RT_LAUNCH;
+}
+
+/// f32 rows up to 8192 columns that the float4 path does not take.
+bool scalarApplies(const mlkd_softmax* p) {
+    return p->x_dtype == MLKD_F32 && p->y_dtype == MLKD_F32 && p->cols <= 8192 &&
+           (reinterpret_cast<uintptr_t>(p->x) & 3u) == 0 && (reinterpret_cast<uintptr_t>(p->y) & 3u) == 0;
+}
+
 }  // namespace
 
 extern "C" void mlkd_softmax_set_variant(int variant, int64_t waves) {
@@ -313,11 +374,13 @@ extern "C" const char* mlkd_softmax_kernel_name(const mlkd_softmax* p) {
     const bool aligned = (reinterpret_cast<uintptr_t>(p->x) & 15u) == 0 &&
                          (reinterpret_cast<uintptr_t>(p->y) & 15u) == 0 &&
                          (p->x_row_stride & 3) == 0 && (p->y_row_stride & 3) == 0;
-    if (!(p->x_dtype == MLKD_F32 && p->y_dtype == MLKD_F32 && (p->cols & 3) == 0 && aligned && p->cols <= 8192)) {
-        return "softmaxBlockRow";
-    }
     int ch = 1;
     while (256 * ch < p->cols) ch *= 2;
+    if (!(p->x_dtype == MLKD_F32 && p->y_dtype == MLKD_F32 && (p->cols & 3) == 0 && aligned && p->cols <= 8192)) {
+        if (!scalarApplies(p)) return "softmaxBlockRow";
+        std::snprintf(name, sizeof(name), "softmaxWaveRowScalar<%d>", ch);
+        return name;
+    }
     const int variant = p->variant >= 0 ? p->variant : gSoftmaxVariant;
     if (variant == 1) {
         std::snprintf(name, sizeof(name), "softmaxWaveRowPipelined<%d>", ch);
@@ -345,6 +408,14 @@ extern "C" int mlkd_launch_softmax(const mlkd_softmax* p, void* stream) {
         if (p->cols <= 2048) return launchWave<8>(*p, st);
         if (p->cols <= 4096) return launchWave<16>(*p, st);
         if (p->cols <= 8192) return launchWave<32>(*p, st);
+    }
+    if (scalarApplies(p)) {
+        if (p->cols <= 256) return launchScalar<1>(*p, st);
+        if (p->cols <= 512) return launchScalar<2>(*p, st);
+        if (p->cols <= 1024) return launchScalar<4>(*p, st);
+        if (p->cols <= 2048) return launchScalar<8>(*p, st);
+        if (p->cols <= 4096) return launchScalar<16>(*p, st);
+        return launchScalar<32>(*p, st);
     }
     int64_t blocks = p->rows < 65536 ? p->rows : 65536;
     hipLaunchKernelGGL(softmaxBlockRow, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, *p);

@@ -297,7 +297,7 @@ def test_step_kernel_names_name_the_launched_kernels(hip):
     # Profiles name kernels by these; bench.py reports them per config.
     cases = [
         (fx.config2_module(64, 4096, tier=1), ["softmaxWaveRowPair<16, true>"]),
-        (fx.config2_module(64, 1001, tier=1), ["softmaxBlockRow"]),
+        (fx.config2_module(64, 1001, tier=1), ["softmaxWaveRowScalar<4>"]),
         (fx.config4_module(256, 256, 256, "f16", tier=1), ["gemmF16Dma8s<true>"]),
         (fx.config4_module(256, 192, 256, "f16", tier=1), ["gemmF16Dma8s<true>"]),   # K % 128 == 64
         (fx.config4_module(256, 256, 256, "f16", tier=2), ["gemmF16Dma8s<false>"]),

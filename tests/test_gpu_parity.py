@@ -410,6 +410,32 @@ def test_matmul_call_accumulates_into_c(hip):
     assert max_rel(got, ref) <= 1e-5 * math.sqrt(k)
 
 
+@pytest.mark.parametrize("m,n", [(64, 1001), (33, 4095), (8, 8191), (5, 1), (7, 3), (16, 257), (2, 4097)])
+def test_c2_ragged_rows(hip, m, n):
+    # Row lengths off the float4 path (n % 4 != 0) take one wave per row
+    # with 4-byte loads (softmaxWaveRowScalar) up to 8192 columns, with the
+    # float4 path's arithmetic and the class bound of 1e-6; longer rows take
+    # the workgroup-per-row kernel. Rows of -inf, a NaN and +inf give the
+    # reference's NaN rows.
+    say(f"c2 ragged rows {m}x{n}")
+    km = fx.config2_module(m, n, tier=1)
+    x = inputs.config_inputs("c2", {"m": m, "k": n})["x"].astype(np.float64).reshape(m, n)
+    if m >= 8:
+        x[1, :] = -np.inf
+        x[2, n // 2] = np.nan
+        x[3, n - 1] = np.inf
+    art = hip.build(km)
+    assert art.step_kernel_name(0) == ("softmaxBlockRow" if n > 8192 else
+                                       "softmaxWaveRowScalar<%d>" % max(1, 1 << max(0, (n - 1).bit_length() - 8)))
+    got = art.run({0: x.reshape(-1)})[1].reshape(m, n)
+    ref = oracle.run(km, {0: x.reshape(-1)}, hw_threads=8)[1].reshape(m, n)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    fin = np.isfinite(ref)
+    e = max_rel(got[fin], ref[fin])
+    say(f"c2 ragged {m}x{n} max_rel={e:.3e}")
+    assert e <= 1e-6
+
+
 # ------------------------------------------------------------------ C5 ----
 @pytest.mark.parametrize("b,s,dm", [(2, 128, 128), (1, 24, 8)])
 def test_c5_score_softmax(hip, b, s, dm):
